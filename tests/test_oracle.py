@@ -1,0 +1,318 @@
+"""Pins for the CPU checker (oracle/). Each check compares the oracle with something
+other than itself: numpy/scipy float64, hand-derived bit tables, closed forms, the
+reference's own test vectors, or brute force on tiny inputs."""
+import json
+import math
+import os
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import scipy.sparse as sp
+
+from oracle import oracle as O
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+# ------------------------------------------------------------------ generator
+def _splitmix_py(state):
+    """Published SplitMix64 step (Steele, Lea, Flood 2014): returns (next_state, output)."""
+    M = (1 << 64) - 1
+    state = (state + 0x9E3779B97F4A7C15) & M
+    z = state
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+    return state, z ^ (z >> 31)
+
+
+def _mix(z):
+    M = (1 << 64) - 1
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+    return z ^ (z >> 31)
+
+
+def test_splitmix_known_answer_and_counter_form():
+    # Published first outputs of SplitMix64 from state 0.
+    s, o1 = _splitmix_py(0)
+    s, o2 = _splitmix_py(s)
+    assert o1 == 0xE220A8397B1DCDAF
+    assert o2 == 0x6E789E6AA1B965F4
+    # The oracle's counter form equals the sequential generator started at its base.
+    for seed, stream in [(42, 0), (42, 1), (7, 123456789)]:
+        base = seed ^ _mix((stream + 0x632BE59BD9B4E019) & ((1 << 64) - 1))
+        st = base
+        for i in range(5):
+            st, out = _splitmix_py(st)
+            assert O.lib().orc_splitmix64(seed, stream, i) == out
+
+
+def test_uniform_normal_moments_and_determinism():
+    u = O.uniform((1 << 16,), 42, 1, -1.0, 1.0)
+    assert u.min() >= -1.0 and u.max() < 1.0
+    assert abs(u.mean()) < 0.02 and abs(u.var() - 1.0 / 3.0) < 0.01
+    n = O.normal((1 << 16,), 42, 2, 0.0, 0.02)
+    assert abs(n.mean()) < 0.02 * 0.02 and abs(n.std() - 0.02) < 0.02 * 0.02
+    assert np.array_equal(n, O.normal((1 << 16,), 42, 2, 0.0, 0.02))
+    assert not np.array_equal(n, O.normal((1 << 16,), 42, 3, 0.0, 0.02))
+
+
+# ------------------------------------------------------------------ GEMM
+@pytest.mark.parametrize("tA,tB", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_f64_matches_numpy_all_transposes(tA, tB):
+    z = np.load(os.path.join(GOLD, "gemm_small.npz"))
+    for key in ["1x1x1", "8x8x8", "3x5x7", "17x33x9", "64x48x40", "33x65x130"]:
+        A, B, C = z[f"A_{key}"], z[f"B_{key}"], z[f"C64_{key}"]
+        As = np.ascontiguousarray(A.T) if tA else A
+        Bs = np.ascontiguousarray(B.T) if tB else B
+        R = O.gemm_f64(As, Bs, transA=bool(tA), transB=bool(tB))
+        np.testing.assert_allclose(R, C, rtol=1e-12, atol=1e-12)
+
+
+def test_gemm_f64_alpha_beta_and_closed_forms():
+    rng = np.random.default_rng(1)
+    A = rng.standard_normal((20, 30)).astype(np.float32)
+    B = rng.standard_normal((30, 10)).astype(np.float32)
+    C0 = rng.standard_normal((20, 10))
+    R = O.gemm_f64(A, B, alpha=0.5, beta=-2.0, C=C0)
+    np.testing.assert_allclose(R, 0.5 * (A.astype(np.float64) @ B) - 2.0 * C0, rtol=1e-12, atol=1e-12)
+    # identity and permutation
+    I = np.eye(30, dtype=np.float32)
+    np.testing.assert_array_equal(O.gemm_f64(A, I), A.astype(np.float64))
+    P = np.eye(30, dtype=np.float32)[rng.permutation(30)]
+    np.testing.assert_array_equal(O.gemm_f64(A, P), A.astype(np.float64) @ P)
+    # rank-1 outer product is exact in float64
+    u = rng.standard_normal((12, 1)).astype(np.float32)
+    v = rng.standard_normal((1, 9)).astype(np.float32)
+    np.testing.assert_array_equal(O.gemm_f64(u, v), u.astype(np.float64) * v.astype(np.float64))
+    # small integers: exact
+    Ai = rng.integers(-8, 8, size=(16, 24)).astype(np.float32)
+    Bi = rng.integers(-8, 8, size=(24, 7)).astype(np.float32)
+    np.testing.assert_array_equal(O.gemm_f64(Ai, Bi), Ai.astype(np.float64) @ Bi)
+    # (AB)^T = B^T A^T through the transpose flags
+    np.testing.assert_allclose(O.gemm_f64(B, A, transA=True, transB=True), (A.astype(np.float64) @ B).T, rtol=1e-12)
+
+
+def test_gemm_f64_rows_subset():
+    rng = np.random.default_rng(2)
+    A = rng.standard_normal((50, 40)).astype(np.float32)
+    B = rng.standard_normal((40, 30)).astype(np.float32)
+    rows = np.array([0, 7, 49, 13])
+    full = A.astype(np.float64) @ B
+    np.testing.assert_allclose(O.gemm_f64_rows(A, B, rows), full[rows], rtol=1e-12)
+    np.testing.assert_allclose(O.gemm_f64_rows(np.ascontiguousarray(A.T), B, rows, transA=True), full[rows], rtol=1e-12)
+
+
+def test_gemm_f64_k_zero():
+    A = np.zeros((3, 0), np.float32)
+    B = np.zeros((0, 4), np.float32)
+    np.testing.assert_array_equal(O.gemm_f64(A, B), np.zeros((3, 4)))
+
+
+# ------------------------------------------------------------------ fp16
+def test_f16_table_hand_derived():
+    t = json.load(open(os.path.join(GOLD, "f16_table.json")))
+    for c in t["cases"]:
+        # array entry points carry raw bits (a scalar ctypes float would quiet an sNaN)
+        x = np.array([int(c["f32"], 16)], dtype=np.uint32).view(np.float32)
+        assert int(O.f32_to_f16_bits(x, rtz=True)[0]) == int(c["rtz"], 16), c["what"]
+        got = int(O.f32_to_f16_bits(x, rtz=False)[0])
+        if c["rne"] == "nan":
+            assert (got & 0x7C00) == 0x7C00 and (got & 0x3FF) != 0, c["what"]
+        else:
+            assert got == int(c["rne"], 16), c["what"]
+
+
+def _rtz_numpy(x):
+    """Independent IEEE round-toward-zero via numpy's RNE cast + one nextafter step."""
+    x = np.asarray(x, dtype=np.float32)
+    h = x.astype(np.float16)
+    over = np.abs(h.astype(np.float64)) > np.abs(x.astype(np.float64))
+    h = np.where(over, np.nextafter(h, np.float16(0)), h)
+    return h.view(np.uint16)
+
+
+def test_rtz_equals_ieee_round_toward_zero():
+    rng = np.random.default_rng(3)
+    # log-uniform magnitudes spanning fp16 subnormals .. just below overflow, both signs
+    mag = np.exp2(rng.uniform(-26, 15.99, size=200000)).astype(np.float32)
+    x = (mag * rng.choice([-1, 1], size=mag.size)).astype(np.float32)
+    got = O.f32_to_f16_bits(x, rtz=True)
+    np.testing.assert_array_equal(got, _rtz_numpy(x))
+    # every fp16 value, and the fp32 just above/below it, truncates to the right code
+    allh = np.arange(0, 0x7C00, dtype=np.uint16)
+    hv = allh.view(np.float16).astype(np.float32)
+    np.testing.assert_array_equal(O.f32_to_f16_bits(hv, True), allh)
+    up = np.nextafter(hv, np.float32(np.inf))
+    np.testing.assert_array_equal(O.f32_to_f16_bits(up[up < 65536], True), allh[up < 65536])
+
+
+def test_rne_equals_numpy():
+    rng = np.random.default_rng(4)
+    mag = np.exp2(rng.uniform(-27, 16.5, size=200000)).astype(np.float32)
+    x = (mag * rng.choice([-1, 1], size=mag.size)).astype(np.float32)
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(O.f32_to_f16_bits(x, rtz=False), ref)
+    # exact midpoints between consecutive fp16 values (ties to even)
+    h = np.arange(0, 0x7BFF, dtype=np.uint16).view(np.float16).astype(np.float64)
+    mid = ((h[:-1] + h[1:]) / 2).astype(np.float32)
+    with np.errstate(over="ignore"):
+        np.testing.assert_array_equal(O.f32_to_f16_bits(mid, False), mid.astype(np.float16).view(np.uint16))
+
+
+def test_f16_to_f32_all_patterns():
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = O.f16_bits_to_f32(allh)
+    ref = allh.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    np.testing.assert_array_equal(np.isnan(got), nan)
+    np.testing.assert_array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+# ------------------------------------------------------------------ CSR
+def test_coo_to_csr_golden():
+    z = np.load(os.path.join(GOLD, "csr_64.npz"))
+    rc, rowptr, idx, data = O.coo_to_csr(64, 64, z["ri"], z["ci"], z["v"])
+    assert rc == 0
+    np.testing.assert_array_equal(rowptr, z["rowptr"])
+    np.testing.assert_array_equal(idx, z["idx"])
+    np.testing.assert_array_equal(data, z["data"])  # stable order keeps duplicate order
+    assert rowptr[0] == 0 and rowptr[-1] == z["v"].size and np.all(np.diff(rowptr) >= 0)
+    for r in range(64):
+        assert np.all(np.diff(idx[rowptr[r]:rowptr[r + 1]]) >= 0)
+
+
+def test_coo_validation_errors():
+    ri = np.array([0, 1], np.int32)
+    ci = np.array([0, 1], np.int32)
+    v = np.ones(2, np.float32)
+    assert O.coo_to_csr(2, 2, ri, ci, v)[0] == 0
+    assert O.coo_to_csr(1, 2, ri, ci, v)[0] == -2   # row out of range
+    assert O.coo_to_csr(2, 1, ri, ci, v)[0] == -3   # col out of range
+    rc, rowptr, idx, data = O.coo_to_csr(4, 4, ri[:0], ci[:0], v[:0])
+    assert rc == 0 and np.array_equal(rowptr, np.zeros(5, np.int32)) and idx.size == 0
+
+
+def test_csr_to_dense_last_duplicate_wins():
+    rowptr = np.array([0, 2, 2], np.int32)
+    idx = np.array([1, 1], np.int32)
+    data = np.array([3.0, 5.0], np.float32)
+    np.testing.assert_array_equal(O.csr_to_dense(2, 2, rowptr, idx, data), [[0, 5], [0, 0]])
+
+
+# ------------------------------------------------------------------ SpMM / SpMV
+def _fma_f32(a, b, c):
+    """Correctly rounded fp32 fma via exact rationals (brute force for tiny cases)."""
+    exact = Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c))
+    f = np.float32(float(exact))
+    cands = [np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))]
+    best = min(cands, key=lambda y: (abs(Fraction(float(y)) - exact), int(np.array(y).view(np.uint32)) & 1))
+    return np.float32(best)
+
+
+def test_spmm_golden_and_semantics():
+    z = np.load(os.path.join(GOLD, "csr_64.npz"))
+    rp, idx, data, D = z["rowptr"], z["idx"], z["data"], z["D"]
+    C64 = O.spmm_f64(rp, idx, data, D)
+    np.testing.assert_allclose(C64, z["C64"], rtol=1e-12, atol=1e-12)  # duplicates summed (scipy)
+    for fma in (True, False):
+        C = O.spmm_f32(rp, idx, data, D, use_fma=fma)
+        assert O.rel_frob(C, z["C64"]) < 1e-6
+        for r in (0, 5, 6, 31, 63):  # empty rows
+            assert np.all(C[r] == 0)
+
+
+def test_spmm_f32_rounding_order_brute_force():
+    z = np.load(os.path.join(GOLD, "csr_64.npz"))
+    rp, idx, data, D = z["rowptr"], z["idx"], z["data"], z["D"]
+    Cf = O.spmm_f32(rp, idx, data, D, use_fma=True)
+    Cn = O.spmm_f32(rp, idx, data, D, use_fma=False)
+    for i in (1, 3, 10, 62):
+        for j in range(D.shape[1]):
+            accf = np.float32(0)
+            accn = np.float32(0)
+            for k in range(rp[i], rp[i + 1]):
+                accf = _fma_f32(data[k], D[idx[k], j], accf)
+                accn = np.float32(accn + np.float32(data[k] * D[idx[k], j]))
+            assert Cf[i, j] == accf
+            assert Cn[i, j] == accn
+
+
+def test_spmm_equals_dense_gemm_without_duplicates():
+    rp, col, val = O.random_csr(200, 300, 6.0, seed=11)
+    D = O.normal((300, 32), 11, 5)
+    dense = O.csr_to_dense(200, 300, rp, col, val)
+    np.testing.assert_allclose(O.spmm_f64(rp, col, val, D), O.gemm_f64(dense, D), rtol=1e-12, atol=1e-12)
+    S = sp.csr_matrix((val.astype(np.float64), col, rp), shape=(200, 300))
+    np.testing.assert_allclose(O.spmm_f64(rp, col, val, D), S @ D.astype(np.float64), rtol=1e-12, atol=1e-12)
+
+
+def test_spmv_golden():
+    z = np.load(os.path.join(GOLD, "csr_64.npz"))
+    rp, idx, data, x = z["rowptr"], z["idx"], z["data"], z["x"]
+    np.testing.assert_allclose(O.spmv_f64(rp, idx, data, x), z["y64"], rtol=1e-12, atol=1e-12)
+    y = O.spmv_f32(rp, idx, data, x, use_fma=False)
+    # sequential fp32 sum, brute force
+    for i in range(64):
+        acc = np.float32(0)
+        for k in range(rp[i], rp[i + 1]):
+            acc = np.float32(acc + np.float32(data[k] * x[idx[k]]))
+        assert y[i] == acc
+    assert O.rel_frob(O.spmv_f32(rp, idx, data, x, use_fma=True), z["y64"]) < 1e-6
+
+
+# ------------------------------------------------------------------ activations / linear
+def test_activation_reference_vectors():
+    # gpu/matrix/activation_test.go:32-51 (ReLU), :200-220 (LeakyReLU alpha=0.1)
+    x = np.array([-2.0, -1.0, 0.0, 1.0, 2.0, 3.0], np.float32)
+    np.testing.assert_allclose(O.act_f32(0, x), [0, 0, 0, 1, 2, 3], atol=1e-6)
+    np.testing.assert_allclose(O.act_f32(4, x[:4], 0.1), [-0.2, -0.1, 0.0, 1.0], atol=1e-6)
+    x4 = np.array([-2.0, -1.0, 0.0, 1.0], np.float32)
+    assert abs(O.act_f32(7, x4)[2]) <= 1e-6   # GELU(0)=0, activation_test.go:282-285
+    assert abs(O.act_f32(1, x4)[2] - 0.5) <= 1e-6  # Sigmoid(0)=0.5, :96-98
+    assert abs(O.act_f32(2, x4)[2]) <= 1e-6   # Tanh(0)=0, :124-126
+    assert abs(O.act_f32(6, x4)[2]) <= 1e-6   # Swish(0)=0
+    e = O.act_f32(5, x4, 1.0)
+    assert abs(e[3] - 1.0) <= 1e-6 and e[0] < 0  # ELU, :236-244
+
+
+def test_activation_closed_forms():
+    xs = np.array([-30.0, -3.0, -0.5, 0.0, 0.25, 2.0, 30.0])
+    for x in xs:
+        g = O.lib().orc_act_f64(7, 0.0, x)
+        assert g == pytest.approx(0.5 * x * (1 + math.tanh(math.sqrt(2 / math.pi) * (x + 0.044715 * x ** 3))), abs=1e-12)
+        assert O.lib().orc_act_f64(1, 0.0, x) == pytest.approx(1 / (1 + math.exp(-x)), rel=1e-12)
+        assert O.lib().orc_act_f64(2, 0.0, x) == pytest.approx(math.tanh(x), rel=1e-12)
+    # GELU limits: x for large x, 0 for large negative x; ReLU/GELU agree asymptotically
+    assert O.lib().orc_act_f64(7, 0.0, 50.0) == 50.0
+    assert O.lib().orc_act_f64(7, 0.0, -50.0) == 0.0
+    assert math.isnan(O.lib().orc_act_f64(3, 0.0, 1.0))  # softmax is not an epilogue
+    # fp32 restatement tracks the float64 one
+    x = np.linspace(-8, 8, 1001).astype(np.float32)
+    for code in (0, 1, 2, 4, 5, 6, 7):
+        np.testing.assert_allclose(O.act_f32(code, x, 0.1), O.act_f64(code, x.astype(np.float64), 0.1), rtol=2e-6, atol=2e-6)
+
+
+@pytest.mark.parametrize("w_out_in", [0, 1])
+def test_linear_f64_matches_numpy(w_out_in):
+    rng = np.random.default_rng(5)
+    X = rng.standard_normal((9, 33)).astype(np.float32)
+    W = (rng.standard_normal((17, 33)) if w_out_in else rng.standard_normal((33, 17))).astype(np.float32)
+    b = rng.standard_normal(17).astype(np.float32)
+    Wm = W.T.astype(np.float64) if w_out_in else W.astype(np.float64)
+    pre = X.astype(np.float64) @ Wm + b
+    np.testing.assert_allclose(O.linear_f64(X, W, b, 0, w_out_in), np.maximum(pre, 0), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(O.linear_f64(X, W, None, -1, w_out_in), X.astype(np.float64) @ Wm, rtol=1e-12, atol=1e-12)
+
+
+def test_transpose():
+    X = np.arange(12, dtype=np.float32).reshape(3, 4)
+    np.testing.assert_array_equal(O.transpose_f32(X), X.T)
+
+
+def test_rel_frob():
+    R = np.array([3.0, 4.0])
+    assert O.rel_frob(np.array([3.0, 4.0], np.float32), R) == 0.0
+    assert O.rel_frob(np.array([3.0, 4.5], np.float32), R) == pytest.approx(0.1)
