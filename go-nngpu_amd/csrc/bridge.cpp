@@ -1,0 +1,346 @@
+// bridge.cpp — extern "C" entry points of libgonngpu.so (declared in include/gonngpu.h).
+// Part 1 keeps the reference bridge's names, signatures and return codes
+// (internal/cgo/metal_bridge*.m); Part 2 is the device-pointer API.
+#include <cstdlib>
+#include <cstring>
+
+#include "common.h"
+
+using gn::Buffer;
+using gn::set_error;
+
+namespace {
+
+struct Scratch {  // device scratch released on scope exit (after the stream is synchronized)
+  void *p = nullptr;
+  ~Scratch() { gn::dev_free(p); }
+};
+
+int sync(hipStream_t s, CError *err, int code) {
+  hipError_t e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return gn::hip_error(err, code, "device execution", e);
+  return 0;
+}
+
+bool fits(const Buffer *b, long rows, long cols, size_t esz) {
+  if (rows < 0 || cols < 0) return false;
+  return (size_t)rows * (size_t)cols * esz <= b->bytes;
+}
+
+// Uploads host CSR index arrays into device scratch, runs fn, and converts the
+// kernel's validation flags into the reference's error convention.
+template <typename Fn>
+int with_csr(const int *rowptr, long rows, const int *cols, long nnz, hipStream_t s, CError *err, Fn fn) {
+  Scratch d_rp, d_col, d_flags;
+  d_rp.p = gn::dev_alloc(sizeof(int) * (size_t)(rows + 1), err);
+  if (!d_rp.p) return -3;
+  if (nnz > 0) {
+    d_col.p = gn::dev_alloc(sizeof(int) * (size_t)nnz, err);
+    if (!d_col.p) return -3;
+  }
+  d_flags.p = gn::dev_alloc(2 * sizeof(int), err);
+  if (!d_flags.p) return -3;
+  if (int rc = gn::upload(d_rp.p, rowptr, sizeof(int) * (size_t)(rows + 1), s, err)) return rc;
+  if (nnz > 0)
+    if (int rc = gn::upload(d_col.p, cols, sizeof(int) * (size_t)nnz, s, err)) return rc;
+  if (int rc = gn::launch_zero_i32(static_cast<int *>(d_flags.p), 2, s, err)) return rc;
+  if (int rc = fn(static_cast<const int32_t *>(d_rp.p), static_cast<const int32_t *>(d_col.p),
+                  static_cast<int *>(d_flags.p)))
+    return rc;
+  int flags[2] = {0, 0};
+  if (int rc = gn::download(flags, d_flags.p, sizeof(flags), s, err)) return rc;
+  if (flags[0]) return set_error(err, -3, "malformed CSR: row pointers are not monotone within [0, nnz]");
+  if (flags[1]) return set_error(err, -3, "malformed CSR: column index outside [0, cols)");
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+// =========================================================================== Part 1
+
+int create_gpu_buffer(float *data, long length_bytes, GPUPtr *outGPUPtr, DevicePtr *outDevicePtr, CError *err) {
+  gn::Context *ctx = gn::context(err);
+  if (!ctx) return -1;
+  if (length_bytes < 0 || !outGPUPtr) return set_error(err, -3, "Could not create GPU buffer: invalid length or output");
+  void *d = gn::dev_alloc((size_t)length_bytes, err);
+  if (!d) return -3;
+  int rc = 0;
+  if (length_bytes > 0) {
+    if (data) {
+      rc = gn::upload(d, data, (size_t)length_bytes, ctx->stream, err);
+    } else {
+      hipError_t e = hipMemsetAsync(d, 0, (size_t)length_bytes, ctx->stream);
+      if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+      if (e != hipSuccess) rc = gn::hip_error(err, -4, "zero fill", e);
+    }
+  }
+  if (rc) {
+    gn::dev_free(d);
+    return rc;
+  }
+  *outGPUPtr = gn::register_buffer(d, (size_t)length_bytes);
+  if (outDevicePtr) *outDevicePtr = ctx;
+  return 0;
+}
+
+int retrieve_gpu_buffer_data(GPUPtr gpuPtr, float *data, long length_bytes, CError *err) {
+  Buffer *b = gn::as_buffer(gpuPtr);
+  if (!b) return set_error(err, -1, "Invalid GPU buffer pointer.");
+  if (length_bytes < 0 || (size_t)length_bytes > b->bytes)
+    return set_error(err, -2, "Buffer length mismatch during retrieval.");
+  if (length_bytes == 0) return 0;
+  if (!data) return set_error(err, -1, "Invalid host pointer.");
+  gn::Context *ctx = gn::context(err);
+  if (!ctx) return -1;
+  return gn::download(data, b->dptr, (size_t)length_bytes, ctx->stream, err);
+}
+
+int release_gpu_buffer(GPUPtr gpuPtr) {
+  if (!gpuPtr) return 0;
+  Buffer *b = gn::as_buffer(gpuPtr);
+  if (!b) return 0;
+  (void)hipDeviceSynchronize();  // no pending work may still reference the block
+  void *d = b->dptr;
+  if (gn::unregister_buffer(b)) {
+    gn::dev_free(d);
+    delete b;
+  }
+  return 0;
+}
+
+int perform_mps_matrix_multiplication(GPUPtr aMatrixPtr, long aRows, long aCols, GPUPtr bMatrixPtr, long bRows,
+                                      long bCols, GPUPtr resultMatrixPtr, long resultRows, long resultCols,
+                                      DevicePtr mtlDevicePtr, CError *err) {
+  (void)mtlDevicePtr;
+  gn::Context *ctx = gn::context(err);
+  if (!ctx) return -1;
+  Buffer *a = gn::as_buffer(aMatrixPtr), *b = gn::as_buffer(bMatrixPtr), *c = gn::as_buffer(resultMatrixPtr);
+  if (!a || !b || !c) return set_error(err, -2, "Invalid input or output buffer pointers.");
+  if (aRows < 0 || aCols < 0 || bCols < 0 || aCols != bRows || resultRows != aRows || resultCols != bCols)
+    return set_error(err, -3, "Invalid matrix dimensions: A %ldx%ld, B %ldx%ld, C %ldx%ld", aRows, aCols, bRows, bCols,
+                     resultRows, resultCols);
+  if (!fits(a, aRows, aCols, 4) || !fits(b, bRows, bCols, 4) || !fits(c, resultRows, resultCols, 4))
+    return set_error(err, -3, "Buffer smaller than the matrix it describes.");
+  gn::GemmDesc d{GN_F32, false, false, aRows, bCols, aCols, 1.0f, 0.0f, a->dptr, aCols, 0, b->dptr, bCols, 0,
+                 static_cast<float *>(c->dptr), bCols, 0, 1, nullptr, GN_ACT_NONE, 0.0f};
+  if (int rc = gn::launch_gemm(d, ctx->stream, err)) return rc == -1 ? -3 : rc;
+  return sync(ctx->stream, err, -6);
+}
+
+int perform_mps_matrix_transpose(GPUPtr inputMatrixPtr, long inputRows, long inputCols, GPUPtr outputMatrixPtr,
+                                 long outputRows, long outputCols, DevicePtr mtlDevicePtr, CError *err) {
+  (void)mtlDevicePtr;
+  gn::Context *ctx = gn::context(err);
+  if (!ctx) return -1;
+  if (inputRows != outputCols || inputCols != outputRows || inputRows < 0 || inputCols < 0)
+    return set_error(err, -2, "Invalid transpose dimensions.");
+  Buffer *in = gn::as_buffer(inputMatrixPtr), *out = gn::as_buffer(outputMatrixPtr);
+  if (!in || !out) return set_error(err, -3, "Invalid input or output buffer pointers.");
+  if (!fits(in, inputRows, inputCols, 4) || !fits(out, outputRows, outputCols, 4))
+    return set_error(err, -3, "Buffer smaller than the matrix it describes.");
+  if (int rc = gn::launch_transpose_f32(static_cast<const float *>(in->dptr), inputRows, inputCols,
+                                        static_cast<float *>(out->dptr), ctx->stream, err))
+    return rc == -1 ? -3 : rc;
+  return sync(ctx->stream, err, -6);
+}
+
+static int batched_gemm(GPUPtr aPtr, GPUPtr bPtr, GPUPtr cPtr, long batch, long M, long N, long K, float alpha,
+                        float beta, CError *err) {
+  gn::Context *ctx = gn::context(err);
+  if (!ctx) return -1;
+  Buffer *a = gn::as_buffer(aPtr), *b = gn::as_buffer(bPtr), *c = gn::as_buffer(cPtr);
+  if (!a || !b || !c) return set_error(err, -2, "Invalid buffer pointers");
+  if (batch < 0 || M < 0 || N < 0 || K < 0) return set_error(err, -3, "Invalid GEMM sizes");
+  if (batch == 0) return 0;
+  if (!fits(a, batch * M, K, 4) || !fits(b, batch * K, N, 4) || !fits(c, batch * M, N, 4))
+    return set_error(err, -3, "Buffer smaller than the matrices it describes.");
+  gn::GemmDesc d{GN_F32, false, false, M, N, K, alpha, beta, a->dptr, K, M * K, b->dptr, N, K * N,
+                 static_cast<float *>(c->dptr), N, M * N, batch, nullptr, GN_ACT_NONE, 0.0f};
+  if (int rc = gn::launch_gemm(d, ctx->stream, err)) return rc == -1 ? -3 : -4;
+  return sync(ctx->stream, err, -4);
+}
+
+int perform_optimized_gemm(GPUPtr aPtr, GPUPtr bPtr, GPUPtr cPtr, long M, long N, long K, float alpha, float beta,
+                           DevicePtr mtlDevicePtr, CError *err) {
+  (void)mtlDevicePtr;
+  return batched_gemm(aPtr, bPtr, cPtr, 1, M, N, K, alpha, beta, err);
+}
+
+int perform_batch_matmul_optimized(GPUPtr aPtr, GPUPtr bPtr, GPUPtr cPtr, long batchSize, long M, long N, long K,
+                                   DevicePtr mtlDevicePtr, CError *err) {
+  (void)mtlDevicePtr;
+  return batched_gemm(aPtr, bPtr, cPtr, batchSize, M, N, K, 1.0f, 0.0f, err);
+}
+
+int perform_fused_linear_activation(GPUPtr input, long batch_size, long input_size, GPUPtr weight, long output_size,
+                                    GPUPtr bias, int activation_type, float alpha, GPUPtr output, DevicePtr device,
+                                    CError *error) {
+  (void)device;
+  gn::Context *ctx = gn::context(error);
+  if (!ctx) return -1;
+  Buffer *x = gn::as_buffer(input), *w = gn::as_buffer(weight), *y = gn::as_buffer(output);
+  Buffer *bb = bias ? gn::as_buffer(bias) : nullptr;
+  if (!x || !w || !y || (bias && !bb)) return set_error(error, -1, "Invalid GPU buffers");
+  if (activation_type == GN_ACT_NONE || !gn::act_supported(activation_type))
+    return set_error(error, -1, "Unsupported activation type %d", activation_type);
+  if (batch_size < 0 || input_size < 0 || output_size < 0) return set_error(error, -1, "Invalid sizes");
+  if (!fits(x, batch_size, input_size, 4) || !fits(w, input_size, output_size, 4) ||
+      !fits(y, batch_size, output_size, 4) || (bb && !fits(bb, 1, output_size, 4)))
+    return set_error(error, -1, "Buffer smaller than the tensor it describes.");
+  gn::GemmDesc d{GN_F32, false, false, batch_size, output_size, input_size, 1.0f, 0.0f, x->dptr, input_size, 0,
+                 w->dptr, output_size, 0, static_cast<float *>(y->dptr), output_size, 0, 1,
+                 bb ? static_cast<const float *>(bb->dptr) : nullptr, activation_type, alpha};
+  if (gn::launch_gemm(d, ctx->stream, error)) return -1;
+  return sync(ctx->stream, error, -1);
+}
+
+int perform_sparse_dense_matmul(GPUPtr aValuesPtr, int *aRowPtr, long aRowPtrLen, int *aColIndices,
+                                long aColIndicesLen, long aRows, long aCols, long aNNZ, GPUPtr bMatrixPtr,
+                                long bRows, long bCols, GPUPtr resultMatrixPtr, long resultRows, long resultCols,
+                                DevicePtr mtlDevicePtr, CError *err) {
+  (void)mtlDevicePtr;
+  gn::Context *ctx = gn::context(err);
+  if (!ctx) return -1;
+  Buffer *v = aValuesPtr ? gn::as_buffer(aValuesPtr) : nullptr;
+  Buffer *b = gn::as_buffer(bMatrixPtr), *c = gn::as_buffer(resultMatrixPtr);
+  if (!b || !c || (aNNZ > 0 && !v) || (aValuesPtr && !v))
+    return set_error(err, -1, "Invalid buffer pointers for sparse-dense multiplication.");
+  if (aRows < 0 || aCols < 0 || aNNZ < 0 || aRowPtrLen != aRows + 1 || aColIndicesLen < aNNZ || aCols != bRows ||
+      resultRows != aRows || resultCols != bCols || !aRowPtr || (aNNZ > 0 && !aColIndices))
+    return set_error(err, -2, "Incompatible dimensions for sparse-dense multiplication.");
+  if (!fits(b, bRows, bCols, 4) || !fits(c, resultRows, resultCols, 4) || (v && !fits(v, 1, aNNZ, 4)))
+    return set_error(err, -2, "Buffer smaller than the matrix it describes.");
+  const float *vals = v ? static_cast<const float *>(v->dptr) : nullptr;
+  return with_csr(aRowPtr, aRows, aColIndices, aNNZ, ctx->stream, err,
+                  [&](const int32_t *rp, const int32_t *col, int *flags) -> int {
+                    int rc = gn::launch_spmm(aRows, bCols, aCols, aNNZ, rp, col, vals,
+                                             static_cast<const float *>(b->dptr), bCols,
+                                             static_cast<float *>(c->dptr), resultCols, flags, ctx->stream, err);
+                    return rc ? (rc == -1 ? -2 : rc) : sync(ctx->stream, err, -6);
+                  });
+}
+
+int perform_sparse_matvec(GPUPtr aValuesPtr, int *aRowPtr, long aRowPtrLen, int *aColIndices, long aColIndicesLen,
+                          long aRows, long aCols, long aNNZ, GPUPtr xVectorPtr, long xSize, GPUPtr resultVectorPtr,
+                          long resultSize, DevicePtr mtlDevicePtr, CError *err) {
+  (void)mtlDevicePtr;
+  if (aCols != xSize || aRows != resultSize)  // metal_bridge_sparse.m:306-309
+    return set_error(err, -1, "Incompatible dimensions for sparse matrix-vector multiplication.");
+  gn::Context *ctx = gn::context(err);
+  if (!ctx) return -1;
+  Buffer *v = aValuesPtr ? gn::as_buffer(aValuesPtr) : nullptr;
+  Buffer *x = gn::as_buffer(xVectorPtr), *y = gn::as_buffer(resultVectorPtr);
+  if (!x || !y || (aNNZ > 0 && !v) || (aValuesPtr && !v))
+    return set_error(err, -1, "Invalid buffer pointers for sparse matrix-vector multiplication.");
+  if (aRows < 0 || aCols < 0 || aNNZ < 0 || aRowPtrLen != aRows + 1 || aColIndicesLen < aNNZ || !aRowPtr ||
+      (aNNZ > 0 && !aColIndices))
+    return set_error(err, -1, "Incompatible CSR arrays for sparse matrix-vector multiplication.");
+  if (!fits(x, 1, xSize, 4) || !fits(y, 1, resultSize, 4) || (v && !fits(v, 1, aNNZ, 4)))
+    return set_error(err, -1, "Buffer smaller than the vector it describes.");
+  const float *vals = v ? static_cast<const float *>(v->dptr) : nullptr;
+  return with_csr(aRowPtr, aRows, aColIndices, aNNZ, ctx->stream, err,
+                  [&](const int32_t *rp, const int32_t *col, int *flags) -> int {
+                    int rc = gn::launch_spmv(aRows, aCols, aNNZ, rp, col, vals,
+                                             static_cast<const float *>(x->dptr), static_cast<float *>(y->dptr),
+                                             flags, ctx->stream, err);
+                    return rc ? rc : sync(ctx->stream, err, -6);
+                  });
+}
+
+void free_c_error_message(char *message) { free(message); }
+
+// =========================================================================== Part 2
+
+const char *gn_version(void) { return "gonngpu-mi355x 0.1 (gfx950)"; }
+
+int gn_init(CError *err) { return gn::context(err) ? 0 : -1; }
+
+void *gn_stream(void) {
+  gn::Context *ctx = gn::context(nullptr);
+  return ctx ? (void *)ctx->stream : nullptr;
+}
+
+void *gn_buffer_device_ptr(GPUPtr buf) {
+  Buffer *b = gn::as_buffer(buf);
+  return b ? b->dptr : nullptr;
+}
+
+long gn_buffer_bytes(GPUPtr buf) {
+  Buffer *b = gn::as_buffer(buf);
+  return b ? (long)b->bytes : -1;
+}
+
+void gn_memory_stats(long *current_bytes, long *peak_bytes, long *num_allocations) {
+  gn::memory_stats(current_bytes, peak_bytes, num_allocations);
+}
+
+int gn_malloc(void **ptr, size_t bytes, CError *err) {
+  if (!ptr) return set_error(err, -1, "gn_malloc: NULL output");
+  *ptr = gn::dev_alloc(bytes, err);
+  return *ptr ? 0 : -3;
+}
+
+int gn_free(void *ptr) {
+  if (!ptr) return 0;
+  (void)hipDeviceSynchronize();
+  gn::dev_free(ptr);
+  return 0;
+}
+
+int gn_synchronize(void *stream, CError *err) {
+  if (!gn::context(err)) return -1;
+  return sync(gn::resolve_stream(stream), err, -6);
+}
+
+int gn_gemm(int dtype, int transA, int transB, long M, long N, long K, float alpha, const void *A, long lda,
+            long strideA, const void *B, long ldb, long strideB, float beta, float *C, long ldc, long strideC,
+            long batch, const float *bias, int act, float act_alpha, void *stream, CError *err) {
+  if (!gn::context(err)) return -1;
+  gn::GemmDesc d{dtype, transA != 0, transB != 0, M, N, K, alpha, beta, A, lda, strideA, B, ldb, strideB,
+                 C, ldc, strideC, batch, bias, act, act_alpha};
+  return gn::launch_gemm(d, gn::resolve_stream(stream), err);
+}
+
+int gn_cast_f32_f16(const float *in, uint16_t *out, size_t n, int round_mode, void *stream, CError *err) {
+  if (!gn::context(err)) return -1;
+  return gn::launch_cast_f32_f16(in, out, n, round_mode, gn::resolve_stream(stream), err);
+}
+
+int gn_cast_f16_f32(const uint16_t *in, float *out, size_t n, void *stream, CError *err) {
+  if (!gn::context(err)) return -1;
+  return gn::launch_cast_f16_f32(in, out, n, gn::resolve_stream(stream), err);
+}
+
+int gn_transpose_f32(const float *in, long rows, long cols, float *out, void *stream, CError *err) {
+  if (!gn::context(err)) return -1;
+  return gn::launch_transpose_f32(in, rows, cols, out, gn::resolve_stream(stream), err);
+}
+
+int gn_spmm_csr(long M, long N, long K, long nnz, const int32_t *rowptr, const int32_t *col, const float *val,
+                const float *D, long ldd, float *C, long ldc, int *error_flags, void *stream, CError *err) {
+  if (!gn::context(err)) return -1;
+  return gn::launch_spmm(M, N, K, nnz, rowptr, col, val, D, ldd, C, ldc, error_flags, gn::resolve_stream(stream),
+                         err);
+}
+
+int gn_spmv_csr(long M, long K, long nnz, const int32_t *rowptr, const int32_t *col, const float *val,
+                const float *x, float *y, int *error_flags, void *stream, CError *err) {
+  if (!gn::context(err)) return -1;
+  return gn::launch_spmv(M, K, nnz, rowptr, col, val, x, y, error_flags, gn::resolve_stream(stream), err);
+}
+
+int gn_fill_uniform_f32(float *out, size_t n, uint64_t seed, uint64_t stream_id, float lo, float hi, void *stream,
+                        CError *err) {
+  if (!gn::context(err)) return -1;
+  return gn::launch_fill_uniform(out, n, seed, stream_id, lo, hi, gn::resolve_stream(stream), err);
+}
+
+int gn_fill_normal_f32(float *out, size_t n, uint64_t seed, uint64_t stream_id, float mean, float stddev,
+                       void *stream, CError *err) {
+  if (!gn::context(err)) return -1;
+  return gn::launch_fill_normal(out, n, seed, stream_id, mean, stddev, gn::resolve_stream(stream), err);
+}
+
+}  // extern "C"

@@ -1,0 +1,93 @@
+// common.h — internal declarations shared by the HIP translation units of
+// libgonngpu.so (runtime, kernels, C-ABI bridge). Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/gonngpu.h"
+
+namespace gn {
+
+// ---------------------------------------------------------------- errors
+// Formats into a malloc'd message stored in err (if non-NULL) and returns code.
+int set_error(CError *err, int code, const char *fmt, ...) __attribute__((format(printf, 3, 4)));
+// Maps a failed HIP call to code with "<what>: <hip error string>".
+int hip_error(CError *err, int code, const char *what, hipError_t e);
+
+// ---------------------------------------------------------------- context
+struct Context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int num_cus = 0;
+  size_t lds_per_block = 0;
+  char arch[64] = {0};
+};
+// Initialises the process-wide context once; returns nullptr (and sets err) on failure.
+Context *context(CError *err);
+hipStream_t resolve_stream(void *stream);  // NULL -> library stream
+
+// ---------------------------------------------------------------- allocator
+// Caching device allocator: size-binned free lists over hipMalloc, never returns
+// memory to the driver while the process lives (reuse keeps hipMalloc off hot paths).
+void *dev_alloc(size_t bytes, CError *err);
+void dev_free(void *p);
+void memory_stats(long *cur, long *peak, long *n);
+
+// ---------------------------------------------------------------- host <-> device
+// Synchronous copies of pageable host memory through a pinned staging ring.
+int upload(void *dst_dev, const void *src_host, size_t bytes, hipStream_t s, CError *err);
+int download(void *dst_host, const void *src_dev, size_t bytes, hipStream_t s, CError *err);
+
+// ---------------------------------------------------------------- GPUPtr handles
+struct Buffer {
+  uint64_t magic;
+  void *dptr;
+  size_t bytes;
+};
+constexpr uint64_t kBufferMagic = 0x676E6E6770754246ULL;  // "gnngpuBF"
+Buffer *as_buffer(GPUPtr p);  // nullptr if p is not a live handle
+
+// ---------------------------------------------------------------- kernel launchers
+// All launchers validate shapes on the host before any launch, then enqueue on s.
+struct GemmDesc {
+  int dtype;  // GN_F32 / GN_F16
+  bool ta, tb;
+  long M, N, K;
+  float alpha, beta;
+  const void *A;
+  long lda, strideA;
+  const void *B;
+  long ldb, strideB;
+  float *C;
+  long ldc, strideC;
+  long batch;
+  const float *bias;
+  int act;
+  float act_alpha;
+};
+int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err);
+int launch_cast_f32_f16(const float *in, uint16_t *out, size_t n, int mode, hipStream_t s, CError *err);
+int launch_cast_f16_f32(const uint16_t *in, float *out, size_t n, hipStream_t s, CError *err);
+int launch_transpose_f32(const float *in, long rows, long cols, float *out, hipStream_t s, CError *err);
+int launch_spmm(long M, long N, long K, long nnz, const int32_t *rowptr, const int32_t *col, const float *val,
+                const float *D, long ldd, float *C, long ldc, int *flags, hipStream_t s, CError *err);
+int launch_spmv(long M, long K, long nnz, const int32_t *rowptr, const int32_t *col, const float *val,
+                const float *x, float *y, int *flags, hipStream_t s, CError *err);
+int launch_fill_uniform(float *out, size_t n, uint64_t seed, uint64_t sid, float lo, float hi, hipStream_t s,
+                        CError *err);
+int launch_fill_normal(float *out, size_t n, uint64_t seed, uint64_t sid, float mean, float sd, hipStream_t s,
+                       CError *err);
+int launch_zero_i32(int *p, long n, hipStream_t s, CError *err);
+
+bool act_supported(int act);
+
+}  // namespace gn
+
+namespace gn {
+Buffer *register_buffer(void *dptr, size_t bytes);
+bool unregister_buffer(Buffer *b);
+}  // namespace gn

@@ -1,0 +1,191 @@
+// elementwise.hip — bandwidth-bound helpers: fp32<->fp16 casts, LDS-tiled
+// transpose, synthetic-data generators and a flag-clearing kernel.
+#include "common.h"
+
+namespace gn {
+namespace {
+
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+unsigned grid_for(size_t work_items, unsigned block) {
+  size_t g = (work_items + block - 1) / block;
+  const size_t cap = 256u * 32u;  // 32 workgroups per CU on 256 CUs, grid-stride beyond
+  if (g > cap) g = cap;
+  if (g == 0) g = 1;
+  return (unsigned)g;
+}
+
+// ------------------------------------------------------------------ casts
+// Float32ToFloatMP16 semantics (gpu/matrix/mixed-precision.go:106-151): truncation,
+// fp32 subnormal -> signed zero, exponent overflow -> inf, NaN -> 0x7C00 | mant>>13.
+__device__ __forceinline__ uint32_t f16_rtz_ref(uint32_t bits) {
+  const uint32_t sign = (bits >> 31) << 15;
+  const uint32_t exp = (bits >> 23) & 0xFFu;
+  uint32_t mant = bits & 0x7FFFFFu;
+  if (exp == 0) return sign;
+  if (exp == 0xFF) return sign | 0x7C00u | (mant >> 13);
+  const int e = (int)exp - 112;  // exp - 127 + 15
+  if (e >= 31) return sign | 0x7C00u;
+  if (e <= 0) {
+    if (e < -10) return sign;
+    mant = (mant | 0x800000u) >> (uint32_t)(1 - e);
+    return sign | (mant >> 13);
+  }
+  return sign | ((uint32_t)e << 10) | (mant >> 13);
+}
+
+__device__ __forceinline__ uint32_t f16_rne(float x) {
+  const _Float16 h = (_Float16)x;  // v_cvt_f16_f32, round-to-nearest-even mode
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+template <int MODE>
+__global__ void cast_f32_f16_vec(const float4_t *__restrict__ in, u32x2_t *__restrict__ out, size_t n4) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
+    const float4_t v = in[i];
+    uint32_t h[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) h[e] = MODE ? f16_rtz_ref(__builtin_bit_cast(uint32_t, v[e])) : f16_rne(v[e]);
+    out[i] = u32x2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+  }
+}
+
+template <int MODE>
+__global__ void cast_f32_f16_scalar(const float *__restrict__ in, uint16_t *__restrict__ out, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    out[i] = (uint16_t)(MODE ? f16_rtz_ref(__builtin_bit_cast(uint32_t, in[i])) : f16_rne(in[i]));
+}
+
+__global__ void cast_f16_f32_kernel(const uint16_t *__restrict__ in, float *__restrict__ out, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    out[i] = (float)__builtin_bit_cast(_Float16, in[i]);  // exact widening
+}
+
+// ------------------------------------------------------------------ transpose
+// 64x64 tiles through LDS (row pitch 65 floats: column reads hit distinct banks).
+__global__ void __launch_bounds__(256) transpose_kernel(const float *__restrict__ in, long rows, long cols,
+                                                        float *__restrict__ out) {
+  __shared__ float tile[64][65];
+  const long tiles_c = (cols + 63) / 64;
+  const long r0 = (long)(blockIdx.x / tiles_c) * 64;
+  const long c0 = (long)(blockIdx.x % tiles_c) * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int r = ty + 4 * k;
+    if (r0 + r < rows && c0 + tx < cols) tile[r][tx] = in[(r0 + r) * cols + c0 + tx];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int c = ty + 4 * k;  // output row = input column
+    if (c0 + c < cols && r0 + tx < rows) out[(c0 + c) * rows + r0 + tx] = tile[tx][c];
+  }
+}
+
+// ------------------------------------------------------------------ generators
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+  return z ^ (z >> 31);
+}
+
+__global__ void fill_uniform_kernel(float *out, size_t n, uint64_t base, float lo, float hi) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const double u = (double)(mix64(base + (i + 1) * 0x9E3779B97F4A7C15ULL) >> 40) * (1.0 / 16777216.0);
+    out[i] = (float)((double)lo + ((double)hi - (double)lo) * u);
+  }
+}
+
+__global__ void fill_normal_kernel(float *out, size_t n, uint64_t base, float mean, float sd) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const uint64_t a = mix64(base + (2 * i + 1) * 0x9E3779B97F4A7C15ULL);
+    const uint64_t b = mix64(base + (2 * i + 2) * 0x9E3779B97F4A7C15ULL);
+    const double u1 = ((double)(a >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+    const double u2 = (double)(b >> 11) * (1.0 / 9007199254740992.0);
+    const double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586476925286766559 * u2);
+    out[i] = (float)((double)mean + (double)sd * z);
+  }
+}
+
+__global__ void zero_i32_kernel(int *p, long n) {
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = 0;
+}
+
+uint64_t stream_base(uint64_t seed, uint64_t sid) {
+  uint64_t z = sid + 0x632BE59BD9B4E019ULL;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+  return seed ^ (z ^ (z >> 31));
+}
+
+}  // namespace
+
+int launch_cast_f32_f16(const float *in, uint16_t *out, size_t n, int mode, hipStream_t s, CError *err) {
+  if (mode != GN_ROUND_NEAREST_EVEN && mode != GN_ROUND_TOWARD_ZERO)
+    return set_error(err, -1, "cast: unknown rounding mode %d", mode);
+  if (n == 0) return 0;
+  if (!in || !out) return set_error(err, -1, "cast: NULL pointer");
+  const bool vec = (n % 4 == 0) && ((uintptr_t)in % 16 == 0) && ((uintptr_t)out % 8 == 0);
+  if (vec) {
+    const size_t n4 = n / 4;
+    if (mode) hipLaunchKernelGGL(cast_f32_f16_vec<1>, dim3(grid_for(n4, 256)), dim3(256), 0, s,
+                                 (const float4_t *)in, (u32x2_t *)out, n4);
+    else hipLaunchKernelGGL(cast_f32_f16_vec<0>, dim3(grid_for(n4, 256)), dim3(256), 0, s,
+                            (const float4_t *)in, (u32x2_t *)out, n4);
+  } else {
+    if (mode) hipLaunchKernelGGL(cast_f32_f16_scalar<1>, dim3(grid_for(n, 256)), dim3(256), 0, s, in, out, n);
+    else hipLaunchKernelGGL(cast_f32_f16_scalar<0>, dim3(grid_for(n, 256)), dim3(256), 0, s, in, out, n);
+  }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : hip_error(err, -6, "cast launch", e);
+}
+
+int launch_cast_f16_f32(const uint16_t *in, float *out, size_t n, hipStream_t s, CError *err) {
+  if (n == 0) return 0;
+  if (!in || !out) return set_error(err, -1, "cast: NULL pointer");
+  hipLaunchKernelGGL(cast_f16_f32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, in, out, n);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : hip_error(err, -6, "cast launch", e);
+}
+
+int launch_transpose_f32(const float *in, long rows, long cols, float *out, hipStream_t s, CError *err) {
+  if (rows < 0 || cols < 0) return set_error(err, -1, "transpose: negative size");
+  if (rows == 0 || cols == 0) return 0;
+  if (!in || !out) return set_error(err, -1, "transpose: NULL pointer");
+  const long tiles = ((rows + 63) / 64) * ((cols + 63) / 64);
+  if (tiles > 0x7FFFFFFFL) return set_error(err, -1, "transpose: too large");
+  hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)tiles), dim3(256), 0, s, in, rows, cols, out);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : hip_error(err, -6, "transpose launch", e);
+}
+
+int launch_fill_uniform(float *out, size_t n, uint64_t seed, uint64_t sid, float lo, float hi, hipStream_t s,
+                        CError *err) {
+  if (n == 0) return 0;
+  if (!out) return set_error(err, -1, "fill: NULL pointer");
+  hipLaunchKernelGGL(fill_uniform_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, out, n, stream_base(seed, sid),
+                     lo, hi);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : hip_error(err, -6, "fill launch", e);
+}
+
+int launch_fill_normal(float *out, size_t n, uint64_t seed, uint64_t sid, float mean, float sd, hipStream_t s,
+                       CError *err) {
+  if (n == 0) return 0;
+  if (!out) return set_error(err, -1, "fill: NULL pointer");
+  hipLaunchKernelGGL(fill_normal_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, out, n, stream_base(seed, sid),
+                     mean, sd);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : hip_error(err, -6, "fill launch", e);
+}
+
+int launch_zero_i32(int *p, long n, hipStream_t s, CError *err) {
+  if (n <= 0) return 0;
+  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, s, p, n);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : hip_error(err, -6, "zero launch", e);
+}
+
+}  // namespace gn

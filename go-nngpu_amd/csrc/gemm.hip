@@ -1,0 +1,486 @@
+// gemm.hip — MFMA GEMM kernels for gfx950 (CDNA4), fp16-in/fp32-acc and fp32.
+//
+//   C[M,N] = act(alpha * op(A) * op(B) + beta * C + bias[n]),  row-major, batched.
+//
+// Replaces the reference's MPSMatrixMultiplication call (internal/cgo/
+// metal_bridge_matrix.m:90-113), its optimized_gemm / batch_matmul_optimized MSL
+// kernels (metal_bridge_kernels.m:28-110) and the fused_linear_activation kernel
+// (default.metal:459-509).
+//
+// Structure (one workgroup per BM x BN output tile, WM x WN waves, 64 lanes each):
+//  * global -> VGPR prefetch of the next BK slice overlaps the MFMAs of the current
+//    one; LDS is double buffered, one barrier per BK slice;
+//  * operands whose K index is contiguous in memory are kept K-contiguous in LDS and
+//    read with ds_read_b128; fp16 operands whose M/N index is contiguous are kept in
+//    their memory layout and read with ds_read_b64_tr_b16, which transposes 4x16
+//    blocks across a 16-lane group (out lane i, element e <- source lane 4e+i/4,
+//    element i%4), giving the MFMA K-contiguous operand directly;
+//  * fp32 operands are always stored K-contiguous; an M/N-contiguous fp32 tile is
+//    transposed on its way into LDS;
+//  * a grouped, XCD-aware tile order: hardware dispatches workgroup w to XCD w % 8,
+//    so w is remapped to give each XCD a contiguous band of tiles that share A/B
+//    panels in that XCD's L2.
+#include "common.h"
+
+namespace gn {
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef __fp16 trh4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+
+#define LDS_AS __attribute__((address_space(3)))
+
+struct GemmParams {
+  const void *A;
+  const void *B;
+  float *C;
+  const float *bias;
+  long M, N, K;
+  long lda, ldb, ldc;
+  long strideA, strideB, strideC;
+  float alpha, beta, act_alpha;
+  int act;
+  int tiles_m, tiles_n;
+};
+
+// ------------------------------------------------------------------ epilogue
+__device__ __forceinline__ float apply_act(int act, float x, float a) {
+  switch (act) {
+    case 0: return fmaxf(0.0f, x);
+    case 1: { float c = fmaxf(-88.0f, fminf(88.0f, x)); return 1.0f / (1.0f + __expf(-c)); }
+    case 2: return tanhf(x);
+    case 4: return x > 0.0f ? x : a * x;
+    case 5: return x > 0.0f ? x : a * (__expf(fmaxf(-88.0f, x)) - 1.0f);
+    case 6: { float c = fmaxf(-88.0f, fminf(88.0f, x)); return c / (1.0f + __expf(-c)); }
+    case 7: {
+      float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+      inner = fmaxf(-88.0f, fminf(88.0f, inner));
+      return 0.5f * x * (1.0f + tanhf(inner));
+    }
+    default: return x;
+  }
+}
+
+// Writes one 16x16 MFMA accumulator block (lane l holds rows 4*(l/16)+r, column l%16).
+__device__ __forceinline__ void store_block(const GemmParams &p, float *C, long row0, long col0, float4_t acc) {
+  const int lane = threadIdx.x & 63;
+  const long col = col0 + (lane & 15);
+  if (col >= p.N) return;
+  const float b = p.bias ? p.bias[col] : 0.0f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const long row = row0 + 4 * (lane >> 4) + r;
+    if (row < p.M) {
+      float *dst = C + row * p.ldc + col;
+      float v = p.alpha * acc[r];
+      if (p.beta != 0.0f) v += p.beta * *dst;
+      v += b;
+      *dst = apply_act(p.act, v, p.act_alpha);
+    }
+  }
+}
+
+// Grouped + XCD-aware mapping of the linear workgroup id to a (tile_m, tile_n) pair.
+__device__ __forceinline__ void tile_coords(const GemmParams &p, int &tm, int &tn) {
+  const int total = p.tiles_m * p.tiles_n;
+  int w = blockIdx.x;
+  if ((total & 7) == 0) {
+    const int per = total >> 3;
+    w = (w & 7) * per + (w >> 3);
+  }
+  const int GROUP_M = 4;
+  const int in_group = GROUP_M * p.tiles_n;
+  const int group = w / in_group;
+  const int first_m = group * GROUP_M;
+  const int gsize = min(p.tiles_m - first_m, GROUP_M);
+  const int r = w - group * in_group;
+  tm = first_m + r % gsize;
+  tn = r / gsize;
+}
+
+// ------------------------------------------------------------------ tile loads
+// A tile of R rows x CC contiguous elements is moved global -> registers -> LDS in
+// 16-byte vectors (8 halves or 4 floats). VEC: the contiguous extent, the leading
+// dimension and the base are multiples of the vector, so a vector is either fully
+// in or fully out of bounds; otherwise elements are bounds-checked one by one.
+template <typename T, int R, int CC, int NT, bool VEC>
+struct TileLoader {
+  static constexpr int EPV = 16 / sizeof(T);  // elements per vector
+  static constexpr int VPR = CC / EPV;        // vectors per row
+  static constexpr int NV = R * CC / EPV;
+  static_assert(NV % NT == 0, "tile vectors must divide evenly among threads");
+  static constexpr int VPT = NV / NT;
+  u32x4_t reg[VPT];
+
+  __device__ __forceinline__ void load(const T *base, long ld, long rlim, long clim) {
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int v = threadIdx.x + j * NT;
+      const int r = v / VPR;
+      const int c = (v % VPR) * EPV;
+      if (VEC) {
+        if (r < rlim && c < clim) {
+          reg[j] = *reinterpret_cast<const u32x4_t *>(base + (long)r * ld + c);
+        } else {
+          reg[j] = u32x4_t{0, 0, 0, 0};
+        }
+      } else {
+        T tmp[EPV];
+#pragma unroll
+        for (int e = 0; e < EPV; ++e)
+          tmp[e] = (r < rlim && c + e < clim) ? base[(long)r * ld + c + e] : T(0);
+        reg[j] = *reinterpret_cast<u32x4_t *>(tmp);
+      }
+    }
+  }
+  // Same-layout store: LDS row pitch P elements.
+  template <int P>
+  __device__ __forceinline__ void store(T *lds) const {
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int v = threadIdx.x + j * NT;
+      const int r = v / VPR;
+      const int c = (v % VPR) * EPV;
+      *reinterpret_cast<u32x4_t *>(lds + r * P + c) = reg[j];
+    }
+  }
+  // Transposed store (fp32 only): element (r, c+e) goes to lds[(c+e)*P + r].
+  template <int P>
+  __device__ __forceinline__ void store_t(T *lds) const {
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int v = threadIdx.x + j * NT;
+      const int r = v / VPR;
+      const int c = (v % VPR) * EPV;
+      const T *e4 = reinterpret_cast<const T *>(&reg[j]);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) lds[(c + e) * P + r] = e4[e];
+    }
+  }
+};
+
+// ------------------------------------------------------------------ fp16 fragments
+// K-contiguous LDS ([rows][P]): lane (i = l%16, g = l/16) gets row0+i, k0+8g..+7.
+__device__ __forceinline__ half8_t frag_kc(const _Float16 *lds, int P, int row0, int k0) {
+  const int lane = threadIdx.x & 63;
+  const _Float16 *p = lds + (row0 + (lane & 15)) * P + k0 + 8 * (lane >> 4);
+  return *reinterpret_cast<const half8_t *>(p);
+}
+
+// MN-contiguous LDS ([k][P]): lane (i, g) gets elements (k0+8g+e, col0+i), e=0..7,
+// via two transposing 64-bit reads (rows k0+8g..+3 and k0+8g+4..+7).
+__device__ __forceinline__ half8_t frag_tr(const _Float16 *lds, int P, int col0, int k0) {
+  const int lane = threadIdx.x & 63;
+  const int s = lane & 15, g = lane >> 4;
+  const _Float16 *p0 = lds + (k0 + 8 * g + (s >> 2)) * P + col0 + 4 * (s & 3);
+  const _Float16 *p1 = p0 + 4 * P;
+  trh4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((LDS_AS trh4_t *)(p0));
+  trh4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((LDS_AS trh4_t *)(p1));
+  const half4_t l4 = __builtin_bit_cast(half4_t, lo);
+  const half4_t h4 = __builtin_bit_cast(half4_t, hi);
+  return __builtin_shufflevector(l4, h4, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// ------------------------------------------------------------------ fp16 kernel
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VEC>
+__global__ void __launch_bounds__(WM * WN * 64) gemm_f16_kernel(GemmParams p) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
+  constexpr int FM = WTM / 16, FN = WTN / 16;  // 16x16 blocks per wave
+  static_assert(BK % 32 == 0 && WTM % 16 == 0 && WTN % 16 == 0, "tile shape");
+  // LDS pitches (halves): K-contiguous rows get +8 (16 B); MN-contiguous rows +16.
+  constexpr int PA = TA ? BM + 16 : BK + 8;
+  constexpr int PB = TB ? BK + 8 : BN + 16;
+  constexpr int A_ELEMS = TA ? BK * PA : BM * PA;
+  constexpr int B_ELEMS = TB ? BN * PB : BK * PB;
+  __shared__ __attribute__((aligned(16))) _Float16 smem[2 * (A_ELEMS + B_ELEMS)];
+
+  int tm, tn;
+  tile_coords(p, tm, tn);
+  const long m0 = (long)tm * BM, n0 = (long)tn * BN;
+  const long z = blockIdx.z;
+  const _Float16 *A = static_cast<const _Float16 *>(p.A) + z * p.strideA;
+  const _Float16 *B = static_cast<const _Float16 *>(p.B) + z * p.strideB;
+  float *C = p.C + z * p.strideC;
+
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  TileLoader<_Float16, TA ? BK : BM, TA ? BM : BK, NT, VEC> la;
+  TileLoader<_Float16, TB ? BN : BK, TB ? BK : BN, NT, VEC> lb;
+
+  auto load_tiles = [&](long k0) {
+    if (TA) la.load(A + k0 * p.lda + m0, p.lda, p.K - k0, p.M - m0);
+    else    la.load(A + m0 * p.lda + k0, p.lda, p.M - m0, p.K - k0);
+    if (TB) lb.load(B + n0 * p.ldb + k0, p.ldb, p.N - n0, p.K - k0);
+    else    lb.load(B + k0 * p.ldb + n0, p.ldb, p.K - k0, p.N - n0);
+  };
+  auto store_tiles = [&](int stage) {
+    _Float16 *as = smem + stage * (A_ELEMS + B_ELEMS);
+    _Float16 *bs = as + A_ELEMS;
+    la.template store<PA>(as);
+    lb.template store<PB>(bs);
+  };
+
+  float4_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = (int)((p.K + BK - 1) / BK);
+  if (nk > 0) {
+    load_tiles(0);
+    store_tiles(0);
+  }
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const bool more = kt + 1 < nk;
+    if (more) load_tiles((long)(kt + 1) * BK);
+    const _Float16 *as = smem + (kt & 1) * (A_ELEMS + B_ELEMS);
+    const _Float16 *bs = as + A_ELEMS;
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 32) {
+      half8_t af[FM], bf[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        af[i] = TA ? frag_tr(as, PA, wm * WTM + i * 16, kk) : frag_kc(as, PA, wm * WTM + i * 16, kk);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bf[j] = TB ? frag_kc(bs, PB, wn * WTN + j * 16, kk) : frag_tr(bs, PB, wn * WTN + j * 16, kk);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) store_tiles((kt + 1) & 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      store_block(p, C, m0 + wm * WTM + i * 16, n0 + wn * WTN + j * 16, acc[i][j]);
+}
+
+// ------------------------------------------------------------------ fp32 kernel
+// v_mfma_f32_16x16x4_f32: lane (i, g) supplies A[i][k_g], B[k_g][j]. Within a
+// 16-wide K chunk, MFMA step s uses k = 4g + s, so each lane's 4 steps read one
+// 16-byte K-contiguous vector of A and of B.
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VEC>
+__global__ void __launch_bounds__(WM * WN * 64) gemm_f32_kernel(GemmParams p) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 16, FN = WTN / 16;
+  static_assert(BK % 16 == 0, "tile shape");
+  constexpr int P = BK + 4;  // K-contiguous rows, 16 B pad
+  __shared__ __attribute__((aligned(16))) float smem[2 * (BM + BN) * P];
+
+  int tm, tn;
+  tile_coords(p, tm, tn);
+  const long m0 = (long)tm * BM, n0 = (long)tn * BN;
+  const long z = blockIdx.z;
+  const float *A = static_cast<const float *>(p.A) + z * p.strideA;
+  const float *B = static_cast<const float *>(p.B) + z * p.strideB;
+  float *C = p.C + z * p.strideC;
+
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int lane = threadIdx.x & 63;
+
+  TileLoader<float, TA ? BK : BM, TA ? BM : BK, NT, VEC> la;
+  TileLoader<float, TB ? BN : BK, TB ? BK : BN, NT, VEC> lb;
+
+  auto load_tiles = [&](long k0) {
+    if (TA) la.load(A + k0 * p.lda + m0, p.lda, p.K - k0, p.M - m0);
+    else    la.load(A + m0 * p.lda + k0, p.lda, p.M - m0, p.K - k0);
+    if (TB) lb.load(B + n0 * p.ldb + k0, p.ldb, p.N - n0, p.K - k0);
+    else    lb.load(B + k0 * p.ldb + n0, p.ldb, p.K - k0, p.N - n0);
+  };
+  auto store_tiles = [&](int stage) {
+    float *as = smem + stage * (BM + BN) * P;
+    float *bs = as + BM * P;
+    if (TA) la.template store_t<P>(as); else la.template store<P>(as);
+    if (TB) lb.template store<P>(bs); else lb.template store_t<P>(bs);
+  };
+
+  float4_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = (int)((p.K + BK - 1) / BK);
+  if (nk > 0) {
+    load_tiles(0);
+    store_tiles(0);
+  }
+  __syncthreads();
+
+  const int li = lane & 15, lg = lane >> 4;
+  for (int kt = 0; kt < nk; ++kt) {
+    const bool more = kt + 1 < nk;
+    if (more) load_tiles((long)(kt + 1) * BK);
+    const float *as = smem + (kt & 1) * (BM + BN) * P;
+    const float *bs = as + BM * P;
+#pragma unroll
+    for (int kc = 0; kc < BK; kc += 16) {
+      float4_t af[FM], bf[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        af[i] = *reinterpret_cast<const float4_t *>(as + (wm * WTM + i * 16 + li) * P + kc + 4 * lg);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bf[j] = *reinterpret_cast<const float4_t *>(bs + (wn * WTN + j * 16 + li) * P + kc + 4 * lg);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);
+    }
+    if (more) store_tiles((kt + 1) & 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      store_block(p, C, m0 + wm * WTM + i * 16, n0 + wn * WTN + j * 16, acc[i][j]);
+}
+
+// ------------------------------------------------------------------ dispatch
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VEC>
+hipError_t launch_f16(GemmParams p, long batch, hipStream_t s) {
+  p.tiles_m = (int)((p.M + BM - 1) / BM);
+  p.tiles_n = (int)((p.N + BN - 1) / BN);
+  dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
+  hipLaunchKernelGGL((gemm_f16_kernel<BM, BN, BK, WM, WN, TA, TB, VEC>), grid, dim3(WM * WN * 64), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VEC>
+hipError_t launch_f32(GemmParams p, long batch, hipStream_t s) {
+  p.tiles_m = (int)((p.M + BM - 1) / BM);
+  p.tiles_n = (int)((p.N + BN - 1) / BN);
+  dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
+  hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, TA, TB, VEC>), grid, dim3(WM * WN * 64), 0, s, p);
+  return hipGetLastError();
+}
+
+template <bool TA, bool TB, bool VEC>
+hipError_t pick_f16(const GemmParams &p, long batch, hipStream_t s) {
+  if constexpr (!VEC) {
+    // Unaligned shapes take the element-wise load path on the smallest tile only.
+    return launch_f16<64, 64, 64, 2, 2, TA, TB, VEC>(p, batch, s);
+  } else {
+    const long tiles256 = ((p.M + 255) / 256) * ((p.N + 255) / 256) * batch;
+    if (tiles256 >= 512) return launch_f16<256, 256, 64, 2, 4, TA, TB, VEC>(p, batch, s);
+    const long tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
+    if (tiles128 >= 128) return launch_f16<128, 128, 64, 2, 2, TA, TB, VEC>(p, batch, s);
+    return launch_f16<64, 64, 64, 2, 2, TA, TB, VEC>(p, batch, s);
+  }
+}
+
+template <bool TA, bool TB, bool VEC>
+hipError_t pick_f32(const GemmParams &p, long batch, hipStream_t s) {
+  if constexpr (!VEC) {
+    return launch_f32<64, 64, 16, 2, 2, TA, TB, VEC>(p, batch, s);
+  } else {
+    const long tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
+    if (tiles128 >= 256) return launch_f32<128, 128, 16, 2, 2, TA, TB, VEC>(p, batch, s);
+    return launch_f32<64, 64, 16, 2, 2, TA, TB, VEC>(p, batch, s);
+  }
+}
+
+template <bool VEC>
+hipError_t dispatch(const GemmDesc &d, const GemmParams &p, hipStream_t s) {
+  const int v = (d.ta ? 2 : 0) | (d.tb ? 1 : 0);
+  if (d.dtype == GN_F16) {
+    switch (v) {
+      case 0: return pick_f16<false, false, VEC>(p, d.batch, s);
+      case 1: return pick_f16<false, true, VEC>(p, d.batch, s);
+      case 2: return pick_f16<true, false, VEC>(p, d.batch, s);
+      default: return pick_f16<true, true, VEC>(p, d.batch, s);
+    }
+  }
+  switch (v) {
+    case 0: return pick_f32<false, false, VEC>(p, d.batch, s);
+    case 1: return pick_f32<false, true, VEC>(p, d.batch, s);
+    case 2: return pick_f32<true, false, VEC>(p, d.batch, s);
+    default: return pick_f32<true, true, VEC>(p, d.batch, s);
+  }
+}
+
+// Zero-K / empty-product epilogue: C = act(beta*C + bias) (alpha*0 contributes nothing).
+__global__ void gemm_k0_kernel(GemmParams p, long batch) {
+  const long total = p.M * p.N * batch;
+  for (long t = blockIdx.x * (long)blockDim.x + threadIdx.x; t < total; t += (long)gridDim.x * blockDim.x) {
+    const long z = t / (p.M * p.N);
+    const long r = (t / p.N) % p.M;
+    const long c = t % p.N;
+    float *dst = p.C + z * p.strideC + r * p.ldc + c;
+    float v = p.beta != 0.0f ? p.beta * *dst : 0.0f;
+    v += p.bias ? p.bias[c] : 0.0f;
+    *dst = apply_act(p.act, v, p.act_alpha);
+  }
+}
+
+}  // namespace
+
+bool act_supported(int act) { return act == -1 || act == 0 || act == 1 || act == 2 || (act >= 4 && act <= 7); }
+
+int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
+  if (d.dtype != GN_F32 && d.dtype != GN_F16) return set_error(err, -1, "gemm: unsupported dtype %d", d.dtype);
+  if (d.M < 0 || d.N < 0 || d.K < 0 || d.batch < 1) return set_error(err, -1, "gemm: negative size");
+  if (!act_supported(d.act)) return set_error(err, -1, "gemm: unsupported activation %d", d.act);
+  if (d.M == 0 || d.N == 0) return 0;
+  if (!d.C) return set_error(err, -1, "gemm: NULL C");
+  if (d.K > 0 && (!d.A || !d.B)) return set_error(err, -1, "gemm: NULL operand");
+  const long a_rows = d.ta ? d.K : d.M, a_cols = d.ta ? d.M : d.K;
+  const long b_rows = d.tb ? d.N : d.K, b_cols = d.tb ? d.K : d.N;
+  if ((d.K > 0 && (d.lda < a_cols || d.ldb < b_cols)) || d.ldc < d.N)
+    return set_error(err, -1, "gemm: leading dimension smaller than row length");
+  if (d.batch > 65535) return set_error(err, -1, "gemm: batch %ld exceeds 65535", d.batch);
+  (void)a_rows; (void)b_rows;
+  const long tiles = ((d.M + 63) / 64) * ((d.N + 63) / 64);
+  if (tiles > (1L << 30)) return set_error(err, -1, "gemm: problem too large for the grid");
+
+  GemmParams p{};
+  p.A = d.A; p.B = d.B; p.C = d.C; p.bias = d.bias;
+  p.M = d.M; p.N = d.N; p.K = d.K;
+  p.lda = d.lda; p.ldb = d.ldb; p.ldc = d.ldc;
+  p.strideA = d.strideA; p.strideB = d.strideB; p.strideC = d.strideC;
+  p.alpha = d.alpha; p.beta = d.beta; p.act = d.act; p.act_alpha = d.act_alpha;
+
+  hipError_t e;
+  if (d.K == 0) {
+    hipLaunchKernelGGL(gemm_k0_kernel, dim3(1024), dim3(256), 0, s, p, d.batch);
+    e = hipGetLastError();
+  } else {
+    const size_t esz = d.dtype == GN_F16 ? 2 : 4;
+    const long epv = 16 / (long)esz;
+    auto aligned = [&](const void *ptr, long ld, long stride) {
+      return ((uintptr_t)ptr % 16 == 0) && (ld % epv == 0) && (d.batch == 1 || stride % epv == 0);
+    };
+    // Vector path needs every contiguous extent (K for K-contiguous, M/N otherwise)
+    // to be a multiple of the vector length.
+    const long a_contig = d.ta ? d.M : d.K, b_contig = d.tb ? d.K : d.N;
+    const bool vec = aligned(d.A, d.lda, d.strideA) && aligned(d.B, d.ldb, d.strideB) && a_contig % epv == 0 &&
+                     b_contig % epv == 0;
+    e = vec ? dispatch<true>(d, p, s) : dispatch<false>(d, p, s);
+  }
+  if (e != hipSuccess) return hip_error(err, -6, "gemm launch", e);
+  return 0;
+}
+
+}  // namespace gn

@@ -1,0 +1,289 @@
+// runtime.cpp — process-wide HIP context, caching device allocator, pinned staging
+// ring for pageable host copies, and GPUPtr handle registry.
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <unordered_map>
+#include <unordered_set>
+#include <vector>
+
+#include "common.h"
+
+namespace gn {
+
+// ------------------------------------------------------------------ errors
+int set_error(CError *err, int code, const char *fmt, ...) {
+  if (err) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    err->message = strdup(buf);
+  }
+  return code;
+}
+
+int hip_error(CError *err, int code, const char *what, hipError_t e) {
+  return set_error(err, code, "%s: %s", what, hipGetErrorString(e));
+}
+
+// ------------------------------------------------------------------ context
+static Context g_ctx;
+static std::once_flag g_ctx_once;
+static int g_ctx_status = 0;
+static char g_ctx_msg[256];
+
+static void init_context() {
+  hipError_t e = hipGetDevice(&g_ctx.device);
+  if (e != hipSuccess) {
+    snprintf(g_ctx_msg, sizeof(g_ctx_msg), "no HIP device: %s", hipGetErrorString(e));
+    g_ctx_status = -1;
+    return;
+  }
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, g_ctx.device);
+  if (e != hipSuccess) {
+    snprintf(g_ctx_msg, sizeof(g_ctx_msg), "hipGetDeviceProperties: %s", hipGetErrorString(e));
+    g_ctx_status = -1;
+    return;
+  }
+  g_ctx.num_cus = prop.multiProcessorCount;
+  g_ctx.lds_per_block = prop.sharedMemPerBlock;
+  snprintf(g_ctx.arch, sizeof(g_ctx.arch), "%s", prop.gcnArchName);
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    snprintf(g_ctx_msg, sizeof(g_ctx_msg), "device is %s; this library is built for gfx950 only", prop.gcnArchName);
+    g_ctx_status = -1;
+    return;
+  }
+  // Default-priority, non-blocking stream (never a non-default priority).
+  e = hipStreamCreateWithFlags(&g_ctx.stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    snprintf(g_ctx_msg, sizeof(g_ctx_msg), "hipStreamCreate: %s", hipGetErrorString(e));
+    g_ctx_status = -1;
+    return;
+  }
+}
+
+Context *context(CError *err) {
+  std::call_once(g_ctx_once, init_context);
+  if (g_ctx_status != 0) {
+    set_error(err, -1, "%s", g_ctx_msg);
+    return nullptr;
+  }
+  return &g_ctx;
+}
+
+hipStream_t resolve_stream(void *stream) {
+  return stream ? reinterpret_cast<hipStream_t>(stream) : g_ctx.stream;
+}
+
+// ------------------------------------------------------------------ allocator
+namespace {
+struct Pool {
+  std::mutex mu;
+  std::unordered_map<size_t, std::vector<void *>> free_lists;  // rounded size -> blocks
+  std::unordered_map<void *, size_t> live;                     // block -> rounded size
+  long cur = 0, peak = 0;
+  long fail_after = -1;  // fault injection: GONNGPU_FAIL_ALLOC_AFTER
+  long n_calls = 0;
+  bool env_read = false;
+};
+Pool &pool() {
+  static Pool *p = new Pool();  // leaked on purpose: outlives static destructors
+  return *p;
+}
+
+size_t round_size(size_t b) {
+  if (b == 0) b = 1;
+  if (b <= (1u << 20)) {
+    size_t r = 256;
+    while (r < b) r <<= 1;
+    return r;
+  }
+  const size_t g = 2u << 20;
+  return (b + g - 1) / g * g;
+}
+
+void release_cached_locked(Pool &p) {
+  for (auto &kv : p.free_lists)
+    for (void *q : kv.second) (void)hipFree(q);
+  p.free_lists.clear();
+}
+}  // namespace
+
+void *dev_alloc(size_t bytes, CError *err) {
+  if (!context(err)) return nullptr;
+  Pool &p = pool();
+  std::lock_guard<std::mutex> lk(p.mu);
+  if (!p.env_read) {
+    const char *f = getenv("GONNGPU_FAIL_ALLOC_AFTER");
+    if (f && *f) p.fail_after = atol(f);
+    p.env_read = true;
+  }
+  if (p.fail_after >= 0 && p.n_calls++ >= p.fail_after) {
+    set_error(err, -3, "device allocation of %zu bytes failed (injected by GONNGPU_FAIL_ALLOC_AFTER)", bytes);
+    return nullptr;
+  }
+  size_t r = round_size(bytes);
+  void *ptr = nullptr;
+  auto it = p.free_lists.find(r);
+  if (it != p.free_lists.end() && !it->second.empty()) {
+    ptr = it->second.back();
+    it->second.pop_back();
+  } else {
+    hipError_t e = hipMalloc(&ptr, r);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      release_cached_locked(p);
+      e = hipMalloc(&ptr, r);
+    }
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      set_error(err, -3, "hipMalloc(%zu): %s", r, hipGetErrorString(e));
+      return nullptr;
+    }
+  }
+  p.live[ptr] = r;
+  p.cur += (long)r;
+  if (p.cur > p.peak) p.peak = p.cur;
+  return ptr;
+}
+
+void dev_free(void *ptr) {
+  if (!ptr) return;
+  Pool &p = pool();
+  std::lock_guard<std::mutex> lk(p.mu);
+  auto it = p.live.find(ptr);
+  if (it == p.live.end()) return;  // not ours: ignore
+  size_t r = it->second;
+  p.live.erase(it);
+  p.cur -= (long)r;
+  p.free_lists[r].push_back(ptr);
+}
+
+void memory_stats(long *cur, long *peak, long *n) {
+  Pool &p = pool();
+  std::lock_guard<std::mutex> lk(p.mu);
+  if (cur) *cur = p.cur;
+  if (peak) *peak = p.peak;
+  if (n) *n = (long)p.live.size();
+}
+
+// ------------------------------------------------------------------ staging
+namespace {
+constexpr size_t kStageBytes = 8u << 20;  // two 8 MiB pinned buffers
+struct Staging {
+  std::mutex mu;
+  void *buf[2] = {nullptr, nullptr};
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  bool ready = false;
+};
+Staging &staging() {
+  static Staging *s = new Staging();
+  return *s;
+}
+int staging_init(Staging &st, CError *err) {
+  if (st.ready) return 0;
+  for (int i = 0; i < 2; ++i) {
+    hipError_t e = hipHostMalloc(&st.buf[i], kStageBytes, hipHostMallocDefault);
+    if (e != hipSuccess) return hip_error(err, -4, "hipHostMalloc(staging)", e);
+    e = hipEventCreateWithFlags(&st.ev[i], hipEventDisableTiming);
+    if (e != hipSuccess) return hip_error(err, -4, "hipEventCreate(staging)", e);
+  }
+  st.ready = true;
+  return 0;
+}
+}  // namespace
+
+int upload(void *dst_dev, const void *src_host, size_t bytes, hipStream_t s, CError *err) {
+  if (bytes == 0) return 0;
+  Staging &st = staging();
+  std::lock_guard<std::mutex> lk(st.mu);
+  if (int rc = staging_init(st, err)) return rc;
+  size_t off = 0;
+  int b = 0;
+  bool used[2] = {false, false};
+  while (off < bytes) {
+    size_t n = bytes - off < kStageBytes ? bytes - off : kStageBytes;
+    if (used[b]) {
+      hipError_t e = hipEventSynchronize(st.ev[b]);
+      if (e != hipSuccess) return hip_error(err, -4, "upload wait", e);
+    }
+    memcpy(st.buf[b], static_cast<const char *>(src_host) + off, n);
+    hipError_t e = hipMemcpyAsync(static_cast<char *>(dst_dev) + off, st.buf[b], n, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) return hip_error(err, -4, "upload hipMemcpyAsync", e);
+    e = hipEventRecord(st.ev[b], s);
+    if (e != hipSuccess) return hip_error(err, -4, "upload hipEventRecord", e);
+    used[b] = true;
+    off += n;
+    b ^= 1;
+  }
+  hipError_t e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_error(err, -4, "upload sync", e);
+  return 0;
+}
+
+int download(void *dst_host, const void *src_dev, size_t bytes, hipStream_t s, CError *err) {
+  if (bytes == 0) return 0;
+  Staging &st = staging();
+  std::lock_guard<std::mutex> lk(st.mu);
+  if (int rc = staging_init(st, err)) return rc;
+  // Pipeline: enqueue chunk i into buffer i%2, then drain chunk i-1 to the host.
+  size_t nchunks = (bytes + kStageBytes - 1) / kStageBytes;
+  for (size_t i = 0; i <= nchunks; ++i) {
+    if (i < nchunks) {
+      size_t off = i * kStageBytes;
+      size_t n = bytes - off < kStageBytes ? bytes - off : kStageBytes;
+      int b = (int)(i & 1);
+      hipError_t e = hipMemcpyAsync(st.buf[b], static_cast<const char *>(src_dev) + off, n, hipMemcpyDeviceToHost, s);
+      if (e != hipSuccess) return hip_error(err, -4, "download hipMemcpyAsync", e);
+      e = hipEventRecord(st.ev[b], s);
+      if (e != hipSuccess) return hip_error(err, -4, "download hipEventRecord", e);
+    }
+    if (i > 0) {
+      size_t j = i - 1;
+      size_t off = j * kStageBytes;
+      size_t n = bytes - off < kStageBytes ? bytes - off : kStageBytes;
+      int b = (int)(j & 1);
+      hipError_t e = hipEventSynchronize(st.ev[b]);
+      if (e != hipSuccess) return hip_error(err, -4, "download wait", e);
+      memcpy(static_cast<char *>(dst_host) + off, st.buf[b], n);
+    }
+  }
+  return 0;
+}
+
+// ------------------------------------------------------------------ handles
+namespace {
+std::mutex g_handles_mu;
+std::unordered_set<Buffer *> &handles() {
+  static auto *h = new std::unordered_set<Buffer *>();
+  return *h;
+}
+}  // namespace
+
+Buffer *as_buffer(GPUPtr p) {
+  if (!p) return nullptr;
+  std::lock_guard<std::mutex> lk(g_handles_mu);
+  Buffer *b = static_cast<Buffer *>(p);
+  if (!handles().count(b)) return nullptr;
+  return b->magic == kBufferMagic ? b : nullptr;
+}
+
+Buffer *register_buffer(void *dptr, size_t bytes) {
+  Buffer *b = new Buffer{kBufferMagic, dptr, bytes};
+  std::lock_guard<std::mutex> lk(g_handles_mu);
+  handles().insert(b);
+  return b;
+}
+
+bool unregister_buffer(Buffer *b) {
+  std::lock_guard<std::mutex> lk(g_handles_mu);
+  if (!handles().erase(b)) return false;
+  b->magic = 0;
+  return true;
+}
+
+}  // namespace gn

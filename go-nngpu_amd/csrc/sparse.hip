@@ -1,0 +1,215 @@
+// sparse.hip — CSR x dense SpMM and CSR SpMV for gfx950.
+//
+// Replaces the reference's single-threaded CPU loops perform_sparse_dense_matmul
+// (internal/cgo/metal_bridge_sparse.m:117-133) and perform_sparse_matvec (:325-339).
+//
+// SpMM: a group of LPR lanes owns one CSR row (LPR = 64 for N >= 256: one wave64 per
+// row). Lane l of the group accumulates columns 4l..4l+3 (+4*LPR per chunk), so every
+// stored entry triggers one fully coalesced gather of a D-row segment (1 KiB per wave
+// for N = 256). Each output is accumulated in CSR order with one fma per entry, which
+// reproduces the reference loop's summation order exactly (bit-identical to an fmaf
+// restatement of it). Row pointers and column indices are validated in the kernel:
+// an invalid row pointer pair empties the row and raises flags[0]; an out-of-range
+// column skips that entry and raises flags[1]. No access ever leaves its array.
+//
+// SpMV: LPR lanes per row stride over the row's entries and combine their partial
+// sums with an xor-shuffle tree (a different, tolerance-level summation order).
+#include "common.h"
+
+namespace gn {
+namespace {
+
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kBlock = 256;  // 4 waves
+
+__device__ __forceinline__ void row_bounds(const int32_t *rowptr, long row, long nnz, int &s, int &e, int *flags,
+                                           bool leader) {
+  s = rowptr[row];
+  e = rowptr[row + 1];
+  if (s < 0 || e < s || (long)e > nnz) {
+    if (leader && flags) flags[0] = 1;
+    s = e = 0;
+  }
+}
+
+template <int LPR>
+__global__ void __launch_bounds__(kBlock) spmm_vec4_kernel(long M, long N, long K, long nnz,
+                                                           const int32_t *__restrict__ rowptr,
+                                                           const int32_t *__restrict__ col,
+                                                           const float *__restrict__ val,
+                                                           const float *__restrict__ D, long ldd,
+                                                           float *__restrict__ C, long ldc, int *flags) {
+  constexpr int RPW = 64 / LPR;  // rows per wave
+  const int lane = threadIdx.x & 63;
+  const int li = lane % LPR;
+  long row = ((long)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  if (LPR == 64) row = __builtin_amdgcn_readfirstlane((int)row);  // one row per wave: make it uniform
+  if (row >= M) return;
+  int s, e;
+  row_bounds(rowptr, row, nnz, s, e, flags, li == 0);
+  for (long c0 = 4L * li; c0 < N; c0 += 4L * LPR) {
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    int k = s;
+    for (; k + 4 <= e; k += 4) {
+      int cc[4];
+      float vv[4];
+      float4_t dd[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        cc[u] = col[k + u];
+        vv[u] = val[k + u];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const bool ok = (unsigned)cc[u] < (unsigned long)K;
+        dd[u] = ok ? *reinterpret_cast<const float4_t *>(D + (long)cc[u] * ldd + c0) : float4_t{0.f, 0.f, 0.f, 0.f};
+        if (!ok) {
+          vv[u] = 0.f;
+          if (flags) flags[1] = 1;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if ((unsigned)cc[u] < (unsigned long)K) {
+          acc[0] = __builtin_fmaf(vv[u], dd[u][0], acc[0]);
+          acc[1] = __builtin_fmaf(vv[u], dd[u][1], acc[1]);
+          acc[2] = __builtin_fmaf(vv[u], dd[u][2], acc[2]);
+          acc[3] = __builtin_fmaf(vv[u], dd[u][3], acc[3]);
+        }
+      }
+    }
+    for (; k < e; ++k) {
+      const int c = col[k];
+      if ((unsigned)c < (unsigned long)K) {
+        const float v = val[k];
+        const float4_t d = *reinterpret_cast<const float4_t *>(D + (long)c * ldd + c0);
+        acc[0] = __builtin_fmaf(v, d[0], acc[0]);
+        acc[1] = __builtin_fmaf(v, d[1], acc[1]);
+        acc[2] = __builtin_fmaf(v, d[2], acc[2]);
+        acc[3] = __builtin_fmaf(v, d[3], acc[3]);
+      } else if (flags) {
+        flags[1] = 1;
+      }
+    }
+    *reinterpret_cast<float4_t *>(C + row * ldc + c0) = acc;
+  }
+}
+
+// Element-wise variant for N or pitches that are not multiples of 4 floats.
+template <int LPR>
+__global__ void __launch_bounds__(kBlock) spmm_scalar_kernel(long M, long N, long K, long nnz,
+                                                             const int32_t *__restrict__ rowptr,
+                                                             const int32_t *__restrict__ col,
+                                                             const float *__restrict__ val,
+                                                             const float *__restrict__ D, long ldd,
+                                                             float *__restrict__ C, long ldc, int *flags) {
+  constexpr int RPW = 64 / LPR;
+  const int lane = threadIdx.x & 63;
+  const int li = lane % LPR;
+  const long row = ((long)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  if (row >= M) return;
+  int s, e;
+  row_bounds(rowptr, row, nnz, s, e, flags, li == 0);
+  for (long c0 = li; c0 < N; c0 += LPR) {
+    float acc = 0.f;
+    for (int k = s; k < e; ++k) {
+      const int c = col[k];
+      if ((unsigned)c < (unsigned long)K) acc = __builtin_fmaf(val[k], D[(long)c * ldd + c0], acc);
+      else if (flags) flags[1] = 1;
+    }
+    C[row * ldc + c0] = acc;
+  }
+}
+
+template <int LPR>
+__global__ void __launch_bounds__(kBlock) spmv_kernel(long M, long K, long nnz, const int32_t *__restrict__ rowptr,
+                                                      const int32_t *__restrict__ col,
+                                                      const float *__restrict__ val, const float *__restrict__ x,
+                                                      float *__restrict__ y, int *flags) {
+  constexpr int RPW = 64 / LPR;
+  const int lane = threadIdx.x & 63;
+  const int li = lane % LPR;
+  const long row = ((long)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  // Lanes past M still take part in the shuffles below (with an empty row).
+  int s = 0, e = 0;
+  if (row < M) row_bounds(rowptr, row, nnz, s, e, flags, li == 0);
+  float acc = 0.f;
+  for (int k = s + li; k < e; k += LPR) {
+    const int c = col[k];
+    if ((unsigned)c < (unsigned long)K) acc = __builtin_fmaf(val[k], x[c], acc);
+    else if (flags) flags[1] = 1;
+  }
+#pragma unroll
+  for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (row < M && li == 0) y[row] = acc;
+}
+
+int next_pow2_lanes(long n) {
+  int l = 1;
+  while (l < 64 && l < n) l <<= 1;
+  return l;
+}
+
+}  // namespace
+
+int launch_spmm(long M, long N, long K, long nnz, const int32_t *rowptr, const int32_t *col, const float *val,
+                const float *D, long ldd, float *C, long ldc, int *flags, hipStream_t s, CError *err) {
+  if (M < 0 || N < 0 || K < 0 || nnz < 0) return set_error(err, -1, "spmm: negative size");
+  if (M == 0 || N == 0) return 0;
+  if (!rowptr || !C || (nnz > 0 && (!col || !val)) || (K > 0 && !D)) return set_error(err, -1, "spmm: NULL pointer");
+  if (ldd < N || ldc < N) return set_error(err, -1, "spmm: leading dimension smaller than N");
+  if (nnz > 0x7FFFFFFFL || M > 0x7FFFFFF0L) return set_error(err, -1, "spmm: exceeds int32 CSR indexing");
+  const bool vec = N % 4 == 0 && ldd % 4 == 0 && ldc % 4 == 0 && (uintptr_t)D % 16 == 0 && (uintptr_t)C % 16 == 0;
+  const int lpr = next_pow2_lanes(vec ? (N + 3) / 4 : N);
+  const long rows_per_block = (kBlock / 64) * (64 / lpr);
+  const long blocks = (M + rows_per_block - 1) / rows_per_block;
+  if (blocks > 0x7FFFFFFFL) return set_error(err, -1, "spmm: too many rows");
+  dim3 g((unsigned)blocks), b(kBlock);
+#define GN_SPMM_CASE(L)                                                                                         \
+  case L:                                                                                                       \
+    if (vec) hipLaunchKernelGGL(spmm_vec4_kernel<L>, g, b, 0, s, M, N, K, nnz, rowptr, col, val, D, ldd, C, ldc, \
+                                flags);                                                                         \
+    else hipLaunchKernelGGL(spmm_scalar_kernel<L>, g, b, 0, s, M, N, K, nnz, rowptr, col, val, D, ldd, C, ldc,  \
+                            flags);                                                                             \
+    break;
+  switch (lpr) {
+    GN_SPMM_CASE(1)
+    GN_SPMM_CASE(2)
+    GN_SPMM_CASE(4)
+    GN_SPMM_CASE(8)
+    GN_SPMM_CASE(16)
+    GN_SPMM_CASE(32)
+    GN_SPMM_CASE(64)
+  }
+#undef GN_SPMM_CASE
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : hip_error(err, -6, "spmm launch", e);
+}
+
+int launch_spmv(long M, long K, long nnz, const int32_t *rowptr, const int32_t *col, const float *val,
+                const float *x, float *y, int *flags, hipStream_t s, CError *err) {
+  if (M < 0 || K < 0 || nnz < 0) return set_error(err, -1, "spmv: negative size");
+  if (M == 0) return 0;
+  if (!rowptr || !y || (nnz > 0 && (!col || !val)) || (K > 0 && !x)) return set_error(err, -1, "spmv: NULL pointer");
+  if (nnz > 0x7FFFFFFFL || M > 0x7FFFFFF0L) return set_error(err, -1, "spmv: exceeds int32 CSR indexing");
+  // Lanes per row from the mean row length (clamped to 4..64).
+  const long mean = nnz / M;
+  int lpr = 4;
+  while (lpr < 64 && lpr * 2 <= mean / 2) lpr <<= 1;
+  const long rows_per_block = (kBlock / 64) * (64 / lpr);
+  const long blocks = (M + rows_per_block - 1) / rows_per_block;
+  if (blocks > 0x7FFFFFFFL) return set_error(err, -1, "spmv: too many rows");
+  dim3 g((unsigned)blocks), b(kBlock);
+  switch (lpr) {
+    case 4: hipLaunchKernelGGL(spmv_kernel<4>, g, b, 0, s, M, K, nnz, rowptr, col, val, x, y, flags); break;
+    case 8: hipLaunchKernelGGL(spmv_kernel<8>, g, b, 0, s, M, K, nnz, rowptr, col, val, x, y, flags); break;
+    case 16: hipLaunchKernelGGL(spmv_kernel<16>, g, b, 0, s, M, K, nnz, rowptr, col, val, x, y, flags); break;
+    case 32: hipLaunchKernelGGL(spmv_kernel<32>, g, b, 0, s, M, K, nnz, rowptr, col, val, x, y, flags); break;
+    default: hipLaunchKernelGGL(spmv_kernel<64>, g, b, 0, s, M, K, nnz, rowptr, col, val, x, y, flags); break;
+  }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : hip_error(err, -6, "spmv launch", e);
+}
+
+}  // namespace gn

@@ -1,0 +1,193 @@
+/*
+ * gonngpu.h — C ABI of the MI355X (gfx950) GEMM / SpMM backend for go-nngpu
+ * (module github.com/tsawler/gometal).
+ *
+ * Part 1 re-exports, with identical names and signatures, the subset of the
+ * reference bridge header internal/cgo/metal_bridge.h that the matmul path binds
+ * (each declaration cites the prototype it replaces). The Go call sites
+ * (tensor/tensor.go:130,171,198; gpu/matrix/matrix.go:87,387;
+ * gpu/matrix/sparse-matrix.go:167,562; gpu/matrix/optimized-kernels.go:57,118;
+ * gpu/matrix/fused-operations.go:441) compile unchanged against it.
+ *
+ * Part 2 adds gn_* entry points that take raw device pointers, explicit
+ * transposes, dtypes, epilogues and a HIP stream; they have no reference
+ * counterpart and are what a caller that keeps data resident in HBM uses.
+ *
+ * Conventions shared by every entry point:
+ *  - return 0 on success, a negative code on failure; on failure, if err is
+ *    non-NULL, err->message holds a malloc'd string the caller releases with
+ *    free_c_error_message() (metal_bridge_common.m:20-34 convention);
+ *  - Part-1 calls are synchronous: they return after the device work finished
+ *    (as the reference's commit + waitUntilCompleted, metal_bridge_matrix.m:115-116);
+ *  - Part-2 calls are asynchronous on the given stream (NULL = the library stream);
+ *  - all matrices are row-major; fp32 = IEEE binary32, fp16 = IEEE binary16.
+ */
+#ifndef GONNGPU_H
+#define GONNGPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ========================================================================== */
+/* Part 1 — drop-in subset of internal/cgo/metal_bridge.h                      */
+/* ========================================================================== */
+
+/* metal_bridge.h:9-11. GPUPtr is an opaque handle to a device buffer owned by this
+ * library (HBM allocation + size); DevicePtr is an opaque, non-NULL context token.
+ * Callers never dereference either. */
+typedef void *GPUPtr;
+typedef void *DevicePtr;
+
+/* metal_bridge.h:14-16. */
+typedef struct {
+  char *message;
+} CError;
+
+/* metal_bridge.h:23. Allocates length_bytes of HBM and copies length_bytes from
+ * data (host) into it (data may be NULL: the buffer is zero-filled). Unlike the
+ * reference (newBufferWithBytesNoCopy, metal_bridge_buffer.m:46-49) the buffer does
+ * not alias host memory: later host writes need a new upload.
+ * Codes: -1 device unavailable, -3 allocation failed, -4 copy failed. */
+int create_gpu_buffer(float *data, long length_bytes, GPUPtr *outGPUPtr, DevicePtr *outDevicePtr, CError *err);
+
+/* metal_bridge.h:24. Copies length_bytes from the buffer into data.
+ * Codes: -1 invalid handle, -2 length_bytes exceeds the buffer
+ * (metal_bridge_buffer.m:65-72), -4 copy failed. */
+int retrieve_gpu_buffer_data(GPUPtr gpuPtr, float *data, long length_bytes, CError *err);
+
+/* metal_bridge.h:25. Returns the allocation to the library's pool. NULL is a no-op. */
+int release_gpu_buffer(GPUPtr gpuPtr);
+
+/* metal_bridge.h:28-34. C[resultRows,resultCols] = A[aRows,aCols] * B[bRows,bCols],
+ * fp32, row-major (metal_bridge_matrix.m:67-97). mtlDevicePtr may be NULL (the
+ * reference required a device that its Go caller never set).
+ * Codes: -2 NULL buffer, -3 inconsistent dimensions or buffer too small,
+ * -6 device execution error. */
+int perform_mps_matrix_multiplication(GPUPtr aMatrixPtr, long aRows, long aCols, GPUPtr bMatrixPtr, long bRows,
+                                      long bCols, GPUPtr resultMatrixPtr, long resultRows, long resultCols,
+                                      DevicePtr mtlDevicePtr, CError *err);
+
+/* metal_bridge.h:36-41. out[j,i] = in[i,j] (metal_bridge_matrix.m:162-166).
+ * Codes: -2 dimensions not transposed (:145-148), -3 NULL buffer / too small,
+ * -6 device execution error. */
+int perform_mps_matrix_transpose(GPUPtr inputMatrixPtr, long inputRows, long inputCols, GPUPtr outputMatrixPtr,
+                                 long outputRows, long outputCols, DevicePtr mtlDevicePtr, CError *err);
+
+/* metal_bridge.h:1423-1429. C = alpha*A[M,K]*B[K,N] + beta*C (metal_bridge_kernels.m:81).
+ * Codes: -2 NULL buffer, -3 bad sizes / buffer too small, -4 execution error. */
+int perform_optimized_gemm(GPUPtr aPtr, GPUPtr bPtr, GPUPtr cPtr, long M, long N, long K, float alpha, float beta,
+                           DevicePtr mtlDevicePtr, CError *err);
+
+/* metal_bridge.h:1432-1437. C_b = A_b[M,K]*B_b[K,N] for b < batchSize, batches packed
+ * back to back (metal_bridge_kernels.m:85-110). Codes as perform_optimized_gemm. */
+int perform_batch_matmul_optimized(GPUPtr aPtr, GPUPtr bPtr, GPUPtr cPtr, long batchSize, long M, long N, long K,
+                                   DevicePtr mtlDevicePtr, CError *err);
+
+/* metal_bridge.h:1348-1353. output[b,o] = act(sum_i input[b,i]*weight[i,o] + bias[o]);
+ * weight is [input_size, output_size] (fused-operations.go:413-415,
+ * default.metal:477-484); bias may be NULL. activation_type uses the Go
+ * ActivationType codes (gpu/matrix/activation.go:20-29): 0 ReLU, 1 Sigmoid, 2 Tanh,
+ * 4 LeakyReLU(alpha), 5 ELU(alpha), 6 Swish, 7 GELU (tanh form); any other code
+ * (including 3 Softmax, which is not element-wise) is rejected with -1.
+ * Codes: -1 invalid argument / NULL buffer / execution error (as the reference). */
+int perform_fused_linear_activation(GPUPtr input, long batch_size, long input_size, GPUPtr weight, long output_size,
+                                    GPUPtr bias, int activation_type, float alpha, GPUPtr output, DevicePtr device,
+                                    CError *error);
+
+/* metal_bridge.h:180-187. C = S*B with S in CSR (values in aValuesPtr, host row
+ * pointers and column indices valid for the call, sparse-matrix.go:167-177) and B,
+ * C dense row-major fp32. Sums duplicates and keeps explicit zeros exactly as the
+ * reference loop (metal_bridge_sparse.m:117-133); nnz = 0 returns C = 0.
+ * Codes: -1 NULL buffer, -2 inconsistent dimensions, -3 malformed CSR
+ * (row pointers not monotone / out of [0,nnz], column index outside [0,aCols)),
+ * -6 execution error. */
+int perform_sparse_dense_matmul(GPUPtr aValuesPtr, int *aRowPtr, long aRowPtrLen, int *aColIndices,
+                                long aColIndicesLen, long aRows, long aCols, long aNNZ, GPUPtr bMatrixPtr,
+                                long bRows, long bCols, GPUPtr resultMatrixPtr, long resultRows, long resultCols,
+                                DevicePtr mtlDevicePtr, CError *err);
+
+/* metal_bridge.h:221-228. y = S*x (metal_bridge_sparse.m:297-342).
+ * Codes: -1 dimension mismatch (:306-309) or NULL buffer, -3 malformed CSR,
+ * -6 execution error. */
+int perform_sparse_matvec(GPUPtr aValuesPtr, int *aRowPtr, long aRowPtrLen, int *aColIndices, long aColIndicesLen,
+                          long aRows, long aCols, long aNNZ, GPUPtr xVectorPtr, long xSize, GPUPtr resultVectorPtr,
+                          long resultSize, DevicePtr mtlDevicePtr, CError *err);
+
+/* metal_bridge.h:250. */
+void free_c_error_message(char *message);
+
+/* ========================================================================== */
+/* Part 2 — device-pointer API (no reference counterpart)                      */
+/* ========================================================================== */
+
+typedef enum { GN_F32 = 0, GN_F16 = 1 } gn_dtype;
+typedef enum { GN_ROUND_NEAREST_EVEN = 0, GN_ROUND_TOWARD_ZERO = 1 } gn_round;
+/* Epilogue activations: GN_ACT_NONE plus the Go ActivationType codes. */
+enum { GN_ACT_NONE = -1, GN_ACT_RELU = 0, GN_ACT_SIGMOID = 1, GN_ACT_TANH = 2, GN_ACT_LEAKY_RELU = 4,
+       GN_ACT_ELU = 5, GN_ACT_SWISH = 6, GN_ACT_GELU = 7 };
+
+/* Library version string (static storage). */
+const char *gn_version(void);
+/* Initialises the device context once (thread-safe). 0 on success. */
+int gn_init(CError *err);
+/* The library's stream (a hipStream_t, returned as void*). */
+void *gn_stream(void);
+/* Device pointer of a GPUPtr handle (NULL for an invalid handle), and its size. */
+void *gn_buffer_device_ptr(GPUPtr buf);
+long gn_buffer_bytes(GPUPtr buf);
+/* Live/peak bytes and live allocations of the library's device pool
+ * (the GlobalMemoryPool statistics of tensor/tensor.go:65-77). */
+void gn_memory_stats(long *current_bytes, long *peak_bytes, long *num_allocations);
+/* Device memory from the library pool (async-safe caching allocator). */
+int gn_malloc(void **ptr, size_t bytes, CError *err);
+int gn_free(void *ptr);
+int gn_synchronize(void *stream, CError *err);
+
+/* General GEMM on device pointers:
+ *   C[M,N] = act( alpha * op(A) * op(B) + beta * C + bias[n] )
+ * op(A) is A[M,K] (lda >= K) or, with transA, A stored [K,M] (lda >= M); likewise B.
+ * dtype GN_F32: A, B fp32, fp32 MFMA (v_mfma_f32_16x16x4_f32).
+ * dtype GN_F16: A, B fp16, fp32 accumulate (v_mfma_f32_16x16x32_f16).
+ * C and bias are fp32; bias may be NULL; beta == 0 never reads C.
+ * batch >= 1 with element strides strideA/B/C between consecutive problems.
+ * Codes: -1 invalid argument, -6 launch error. */
+int gn_gemm(int dtype, int transA, int transB, long M, long N, long K, float alpha, const void *A, long lda,
+            long strideA, const void *B, long ldb, long strideB, float beta, float *C, long ldc, long strideC,
+            long batch, const float *bias, int act, float act_alpha, void *stream, CError *err);
+
+/* fp32 -> fp16 element-wise cast. GN_ROUND_NEAREST_EVEN is IEEE RNE;
+ * GN_ROUND_TOWARD_ZERO reproduces Float32ToFloatMP16 (gpu/matrix/mixed-precision.go:106-151)
+ * bit for bit, including its fp32-subnormal flush and NaN/overflow handling. */
+int gn_cast_f32_f16(const float *in, uint16_t *out, size_t n, int round_mode, void *stream, CError *err);
+int gn_cast_f16_f32(const uint16_t *in, float *out, size_t n, void *stream, CError *err);
+
+/* out[cols,rows] = in[rows,cols]^T, fp32, LDS-tiled. */
+int gn_transpose_f32(const float *in, long rows, long cols, float *out, void *stream, CError *err);
+
+/* CSR SpMM on device arrays: C[M,N] = S[M,K] * D[K,N] (ld = row pitch in elements).
+ * Accumulates each output in CSR order with one fused multiply-add per stored entry.
+ * error_flags (2 ints, may be NULL) receive nonzero values if a row pointer pair is
+ * invalid ([0]) or a column index is outside [0,K) ([1]); offending rows / entries
+ * contribute nothing and never cause an out-of-bounds access. */
+int gn_spmm_csr(long M, long N, long K, long nnz, const int32_t *rowptr, const int32_t *col, const float *val,
+                const float *D, long ldd, float *C, long ldc, int *error_flags, void *stream, CError *err);
+/* CSR SpMV on device arrays: y[M] = S[M,K] * x[K]; error_flags as gn_spmm_csr. */
+int gn_spmv_csr(long M, long K, long nnz, const int32_t *rowptr, const int32_t *col, const float *val,
+                const float *x, float *y, int *error_flags, void *stream, CError *err);
+
+/* Synthetic data on device: the counter-based SplitMix64 generator
+ * (element i of stream s: mix64(seed ^ mix64(s + 0x632BE59BD9B4E019) + (i+1)*0x9E3779B97F4A7C15)),
+ * uniform = (u >> 40) * 2^-24 mapped to [lo,hi); normal = Box-Muller (cos branch) in fp64. */
+int gn_fill_uniform_f32(float *out, size_t n, uint64_t seed, uint64_t stream_id, float lo, float hi, void *stream,
+                        CError *err);
+int gn_fill_normal_f32(float *out, size_t n, uint64_t seed, uint64_t stream_id, float mean, float stddev,
+                       void *stream, CError *err);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GONNGPU_H */

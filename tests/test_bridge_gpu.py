@@ -1,0 +1,87 @@
+"""GPU checks of the reference-compatible buffer ABI and its error conventions
+(internal/cgo/metal_bridge_buffer.m:24-86, metal_bridge_common.m:20-34)."""
+import os
+import subprocess
+import sys
+import textwrap
+
+import numpy as np
+import pytest
+
+import gonngpu as G
+
+pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_buffer_roundtrip_and_partial_retrieve(dev):
+    x = np.arange(1000, dtype=np.float32)
+    b = G.Buffer.from_array(x)
+    assert b.device is not None  # DevicePtr is a non-NULL context token
+    np.testing.assert_array_equal(b.to_array((1000,)), x)
+    np.testing.assert_array_equal(b.to_array((10,)), x[:10])  # shorter retrieve is allowed
+    big = np.empty(1001, np.float32)
+    rc, msg = G.call_rc("retrieve_gpu_buffer_data", b.handle, big.ctypes.data, big.nbytes)
+    assert rc == -2 and "length mismatch" in msg
+    b.release()
+    rc, _ = G.call_rc("retrieve_gpu_buffer_data", b.handle, big.ctypes.data, 4)
+    assert rc == -1  # released handle is no longer valid
+
+
+def test_large_buffer_crosses_staging_chunks(dev):
+    x = np.random.default_rng(0).standard_normal(5_000_003).astype(np.float32)  # > 2 staging chunks, odd size
+    b = G.Buffer.from_array(x)
+    np.testing.assert_array_equal(b.to_array(x.shape), x)
+
+
+def test_zero_filled_buffer_and_stats(dev):
+    cur0, peak0, n0 = G.memory_stats()
+    b = G.Buffer(4096)
+    assert np.all(b.to_array((1024,)) == 0)
+    cur1, peak1, n1 = G.memory_stats()
+    assert n1 == n0 + 1 and cur1 >= cur0 + 4096 and peak1 >= cur1
+    b.release()
+    assert G.memory_stats()[2] == n0
+
+
+def test_matmul_dimension_errors(dev):
+    a, b, c = G.Buffer(4 * 6), G.Buffer(4 * 6), G.Buffer(4 * 4)
+    rc, _ = G.call_rc("perform_mps_matrix_multiplication", a.handle, 2, 3, b.handle, 2, 3, c.handle, 2, 3, None)
+    assert rc == -3  # aCols != bRows
+    rc, _ = G.call_rc("perform_mps_matrix_multiplication", None, 2, 3, b.handle, 3, 2, c.handle, 2, 2, None)
+    assert rc == -2
+    rc, _ = G.call_rc("perform_mps_matrix_multiplication", a.handle, 20, 30, b.handle, 30, 20, c.handle, 20, 20, None)
+    assert rc == -3  # buffers too small for the claimed shapes
+
+
+def test_optimized_gemm_alpha_beta(dev):
+    rng = np.random.default_rng(2)
+    A = rng.standard_normal((31, 45)).astype(np.float32)
+    B = rng.standard_normal((45, 27)).astype(np.float32)
+    C0 = rng.standard_normal((31, 27)).astype(np.float32)
+    ba, bb, bc = G.Buffer.from_array(A), G.Buffer.from_array(B), G.Buffer.from_array(C0)
+    G.call("perform_optimized_gemm", ba.handle, bb.handle, bc.handle, 31, 27, 45, 2.0, 0.5, None)
+    ref = 2.0 * (A.astype(np.float64) @ B) + 0.5 * C0
+    got = bc.to_array((31, 27))
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-5
+
+
+def test_injected_allocation_failure_is_clean(dev):
+    """GONNGPU_FAIL_ALLOC_AFTER makes the Nth device allocation fail; the call must
+    return -3 with a message, and the process must keep working."""
+    code = textwrap.dedent(f"""
+        import sys
+        sys.path.insert(0, {os.path.join(ROOT, 'go-nngpu_amd')!r})
+        import numpy as np, gonngpu as G
+        G.init()
+        ok = G.Buffer.from_array(np.ones(16, np.float32))
+        import ctypes
+        h, d = ctypes.c_void_p(), ctypes.c_void_p()
+        rc, msg = G.call_rc("create_gpu_buffer", None, 64, ctypes.byref(h), ctypes.byref(d))
+        assert rc == -3 and "injected" in msg, (rc, msg)
+        assert np.all(ok.to_array((16,)) == 1)
+        print("OK")
+    """)
+    env = dict(os.environ, GONNGPU_FAIL_ALLOC_AFTER="1")
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0 and "OK" in out.stdout, out.stderr[-2000:]

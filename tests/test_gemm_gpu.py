@@ -1,0 +1,301 @@
+"""GPU parity of the MFMA GEMMs (fp32 and fp16-in/fp32-acc) against the oracle.
+
+Tolerances: fp32 relFrob <= 1e-5 vs float64 GEMM; fp16-in
+relFrob <= 2e-2 vs float64 GEMM of the unrounded fp32 inputs. The fp16 path is also
+checked at 1e-5 against the float64 product of the fp16-ROUNDED inputs, which pins
+the GEMM itself rather than the input cast."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import gonngpu as G
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+VARIANTS = [(False, False), (False, True), (True, False), (True, True)]
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def _stored(X, trans):
+    return np.ascontiguousarray(X.T) if trans else X
+
+
+def _gemm_dev(dev, A, B, tA, tB, dtype, **kw):
+    import torch
+
+    As, Bs = _stored(A, tA), _stored(B, tB)
+    ad = torch.from_numpy(As).to(dev)
+    bd = torch.from_numpy(Bs).to(dev)
+    if dtype == G.GN_F16:
+        a16 = torch.empty(ad.shape, dtype=torch.float16, device=dev)
+        b16 = torch.empty(bd.shape, dtype=torch.float16, device=dev)
+        mode = kw.pop("round_mode", G.ROUND_NEAREST_EVEN)
+        G.cast_f32_f16(ad, a16, mode)
+        G.cast_f32_f16(bd, b16, mode)
+        ad, bd = a16, b16
+    M, N = A.shape[0], B.shape[1]
+    C = kw.pop("C", None)
+    cd = torch.from_numpy(C).to(dev) if C is not None else torch.empty((M, N), dtype=torch.float32, device=dev)
+    bias = kw.pop("bias", None)
+    bd_bias = torch.from_numpy(bias).to(dev) if bias is not None else None
+    G.gemm(ad, bd, cd, transA=tA, transB=tB, bias=bd_bias, **kw)
+    return cd.cpu().numpy()
+
+
+# ------------------------------------------------------------------ fp32
+@pytest.mark.parametrize("tA,tB", VARIANTS)
+def test_f32_golden_small_all_transposes(dev, tA, tB):
+    z = np.load(os.path.join(GOLD, "gemm_small.npz"))
+    for key in ["1x1x1", "8x8x8", "3x5x7", "17x33x9", "64x48x40", "33x65x130"]:
+        _say("f32 golden", key, tA, tB)
+        C = _gemm_dev(dev, z[f"A_{key}"], z[f"B_{key}"], tA, tB, G.GN_F32)
+        assert O.rel_frob(C, z[f"C64_{key}"]) <= 1e-5, key
+
+
+def test_f32_c1_256_reference_abi(dev):
+    """Config C1 through perform_mps_matrix_multiplication (metal_bridge.h:28-34)."""
+    z = np.load(os.path.join(GOLD, "gemm_256.npz"))
+    A, B = z["A"], z["B"]
+    ba, bb, bc = G.Buffer.from_array(A), G.Buffer.from_array(B), G.Buffer(256 * 256 * 4)
+    G.call("perform_mps_matrix_multiplication", ba.handle, 256, 256, bb.handle, 256, 256, bc.handle, 256, 256, None)
+    C = bc.to_array((256, 256))
+    err = O.rel_frob(C, z["C64"])
+    _say("C1 relFrob", err)
+    assert err <= 1e-5
+    # the oracle generator's inputs too (seed 42, U[-1,1])
+    A2, B2 = O.uniform((256, 256), 42, 1), O.uniform((256, 256), 42, 2)
+    ba2, bb2 = G.Buffer.from_array(A2), G.Buffer.from_array(B2)
+    G.call("perform_mps_matrix_multiplication", ba2.handle, 256, 256, bb2.handle, 256, 256, bc.handle, 256, 256, None)
+    assert O.rel_frob(bc.to_array((256, 256)), O.gemm_f64(A2, B2)) <= 1e-5
+
+
+def test_f32_closed_forms(dev):
+    rng = np.random.default_rng(3)
+    A = rng.integers(-8, 8, size=(96, 160)).astype(np.float32)
+    B = rng.integers(-8, 8, size=(160, 72)).astype(np.float32)
+    # small integers: every partial sum is exact in fp32, so the product is exact
+    np.testing.assert_array_equal(_gemm_dev(dev, A, B, False, False, G.GN_F32), A.astype(np.float64) @ B)
+    I = np.eye(160, dtype=np.float32)
+    X = rng.standard_normal((96, 160)).astype(np.float32)
+    np.testing.assert_array_equal(_gemm_dev(dev, X, I, False, False, G.GN_F32), X)
+    P = np.eye(160, dtype=np.float32)[rng.permutation(160)]
+    np.testing.assert_array_equal(_gemm_dev(dev, X, P, False, True, G.GN_F32), X @ P)
+
+
+@pytest.mark.parametrize("tA,tB", VARIANTS)
+def test_f32_c2_4096_all_transposes(dev, tA, tB):
+    """Config C2: 4096^3, N(0,1), four transpose variants; rows sampled against float64."""
+    n = 4096
+    A = O.normal((n, n), 42, 11)
+    B = O.normal((n, n), 42, 12)
+    _say("C2", tA, tB)
+    C = _gemm_dev(dev, A, B, tA, tB, G.GN_F32)
+    rows = np.random.default_rng(7).choice(n, 48, replace=False)
+    ref = O.gemm_f64_rows(A, B, rows)
+    err = O.rel_frob(C[rows], ref)
+    _say("C2 relFrob", tA, tB, err)
+    assert err <= 1e-5
+    assert np.isfinite(C).all()
+
+
+def test_f32_transpose_variants_bit_identical(dev):
+    """All four load paths feed MFMA the same operands in the same order."""
+    rng = np.random.default_rng(5)
+    A = rng.standard_normal((640, 384)).astype(np.float32)
+    B = rng.standard_normal((384, 512)).astype(np.float32)
+    outs = [_gemm_dev(dev, A, B, tA, tB, G.GN_F32) for tA, tB in VARIANTS]
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])
+
+
+def test_f32_alpha_beta_bias_activation(dev):
+    rng = np.random.default_rng(9)
+    A = rng.standard_normal((130, 70)).astype(np.float32)
+    B = rng.standard_normal((70, 90)).astype(np.float32)
+    C0 = rng.standard_normal((130, 90)).astype(np.float32)
+    bias = rng.standard_normal(90).astype(np.float32)
+    base = A.astype(np.float64) @ B
+    out = _gemm_dev(dev, A, B, False, False, G.GN_F32, alpha=0.5, beta=-1.5, C=C0)
+    assert O.rel_frob(out, 0.5 * base - 1.5 * C0) <= 1e-5
+    for act, alpha in [(G.ACT_RELU, 0.0), (G.ACT_GELU, 0.0), (G.ACT_SIGMOID, 0.0), (G.ACT_TANH, 0.0),
+                       (G.ACT_LEAKY_RELU, 0.1), (G.ACT_ELU, 1.0), (G.ACT_SWISH, 0.0)]:
+        out = _gemm_dev(dev, A, B, False, False, G.GN_F32, bias=bias, act=act, act_alpha=alpha)
+        ref = O.act_f64(act, base + bias, alpha)
+        assert O.rel_frob(out, ref) <= 1e-5, act
+
+
+def test_f32_unaligned_leading_dims_and_batch(dev):
+    import torch
+
+    rng = np.random.default_rng(11)
+    # leading dimensions larger than the row length (views into wider buffers)
+    Aw = torch.from_numpy(rng.standard_normal((50, 37)).astype(np.float32)).to(dev)
+    Bw = torch.from_numpy(rng.standard_normal((29, 45)).astype(np.float32)).to(dev)
+    A, B = Aw[:, :29], Bw[:, :41]
+    C = torch.zeros((50, 41), dtype=torch.float32, device=dev)
+    G.gemm(A, B, C)
+    ref = A.cpu().numpy().astype(np.float64) @ B.cpu().numpy().astype(np.float64)
+    assert O.rel_frob(C.cpu().numpy(), ref) <= 1e-5
+    # strided batch through perform_batch_matmul_optimized (metal_bridge.h:1432-1437)
+    bs, M, N, K = 3, 33, 20, 17
+    A3 = rng.standard_normal((bs, M, K)).astype(np.float32)
+    B3 = rng.standard_normal((bs, K, N)).astype(np.float32)
+    ba, bb, bc = G.Buffer.from_array(A3), G.Buffer.from_array(B3), G.Buffer(bs * M * N * 4)
+    G.call("perform_batch_matmul_optimized", ba.handle, bb.handle, bc.handle, bs, M, N, K, None)
+    C3 = bc.to_array((bs, M, N))
+    for i in range(bs):
+        assert O.rel_frob(C3[i], A3[i].astype(np.float64) @ B3[i]) <= 1e-5
+
+
+def test_f32_k_zero_and_empty(dev):
+    import torch
+
+    A = torch.zeros((4, 0), dtype=torch.float32, device=dev)
+    B = torch.zeros((0, 3), dtype=torch.float32, device=dev)
+    C = torch.full((4, 3), 7.0, dtype=torch.float32, device=dev)
+    G.gemm(A, B, C, K=0)
+    assert torch.count_nonzero(C).item() == 0
+    bias = torch.arange(3, dtype=torch.float32, device=dev)
+    G.gemm(A, B, C, K=0, bias=bias, act=G.ACT_RELU)
+    np.testing.assert_array_equal(C.cpu().numpy(), np.tile(np.arange(3, dtype=np.float32), (4, 1)))
+
+
+# ------------------------------------------------------------------ fp16 cast
+def test_cast_f32_f16_bit_exact(dev):
+    import json
+
+    import torch
+
+    rng = np.random.default_rng(13)
+    mag = np.exp2(rng.uniform(-27, 17, size=1 << 20)).astype(np.float32)
+    x = (mag * rng.choice([-1, 1], size=mag.size)).astype(np.float32)
+    t = json.load(open(os.path.join(GOLD, "f16_table.json")))
+    special = np.array([int(c["f32"], 16) for c in t["cases"]], dtype=np.uint32).view(np.float32)
+    x = np.concatenate([special, x, special[:3]])  # odd length: exercises the scalar path too
+    xd = torch.from_numpy(x).to(dev)
+    for mode in (G.ROUND_NEAREST_EVEN, G.ROUND_TOWARD_ZERO):
+        for arr in (xd, xd[: (xd.numel() // 4) * 4]):
+            out = torch.empty(arr.shape, dtype=torch.float16, device=dev)
+            G.cast_f32_f16(arr, out, mode)
+            got = out.cpu().numpy().view(np.uint16)
+            ref = O.f32_to_f16_bits(arr.cpu().numpy(), rtz=bool(mode))
+            nan = np.isnan(arr.cpu().numpy())
+            if mode == G.ROUND_NEAREST_EVEN:
+                np.testing.assert_array_equal(got[~nan], ref[~nan])
+                assert np.all((got[nan] & 0x7C00) == 0x7C00) and np.all((got[nan] & 0x3FF) != 0)
+            else:
+                np.testing.assert_array_equal(got, ref)  # incl. the reference's NaN/overflow handling
+    # f16 -> f32 widening over all patterns
+    allh = torch.from_numpy(np.arange(65536, dtype=np.int32).astype(np.uint16).view(np.int16)).to(dev)
+    out = torch.empty(65536, dtype=torch.float32, device=dev)
+    G.cast_f16_f32(allh.view(torch.float16), out)
+    ref = O.f16_bits_to_f32(np.arange(65536, dtype=np.int32).astype(np.uint16))
+    got = out.cpu().numpy()
+    nan = np.isnan(ref)
+    np.testing.assert_array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    assert np.isnan(got[nan]).all()
+
+
+# ------------------------------------------------------------------ fp16 GEMM
+@pytest.mark.parametrize("tA,tB", VARIANTS)
+def test_f16_golden_small_all_transposes(dev, tA, tB):
+    z = np.load(os.path.join(GOLD, "gemm_small.npz"))
+    for key in ["1x1x1", "8x8x8", "3x5x7", "17x33x9", "64x48x40", "33x65x130"]:
+        A, B = z[f"A_{key}"], z[f"B_{key}"]
+        C = _gemm_dev(dev, A, B, tA, tB, G.GN_F16)
+        assert O.rel_frob(C, z[f"C64_{key}"]) <= 2e-2, key
+        ref_r = O.gemm_f64(O.round_f16(A, False), O.round_f16(B, False))
+        assert O.rel_frob(C, ref_r) <= 1e-5, key
+
+
+@pytest.mark.parametrize("tA,tB", VARIANTS)
+def test_f16_medium_all_transposes_rne_and_rtz(dev, tA, tB):
+    rng = np.random.default_rng(17)
+    A = rng.standard_normal((768, 1024)).astype(np.float32)
+    B = (0.02 * rng.standard_normal((1024, 640))).astype(np.float32)
+    for rtz in (False, True):
+        mode = G.ROUND_TOWARD_ZERO if rtz else G.ROUND_NEAREST_EVEN
+        C = _gemm_dev(dev, A, B, tA, tB, G.GN_F16, round_mode=mode)
+        assert O.rel_frob(C, O.gemm_f64(A, B)) <= 2e-2
+        assert O.rel_frob(C, O.gemm_f64(O.round_f16(A, rtz), O.round_f16(B, rtz))) <= 1e-5
+
+
+def test_f16_transpose_variants_bit_identical(dev):
+    rng = np.random.default_rng(19)
+    A = rng.standard_normal((512, 576)).astype(np.float32)
+    B = rng.standard_normal((576, 768)).astype(np.float32)
+    outs = [_gemm_dev(dev, A, B, tA, tB, G.GN_F16) for tA, tB in VARIANTS]
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])
+
+
+def test_f16_c3_8192(dev):
+    """Config C3: 8192^3, A ~ N(0,1), B ~ N(0,0.02^2), cast to fp16 (RNE); rows sampled."""
+    import torch
+
+    n = 8192
+    ad = torch.empty((n, n), dtype=torch.float32, device=dev)
+    bd = torch.empty((n, n), dtype=torch.float32, device=dev)
+    G.fill_normal(ad, 42, 21, 0.0, 1.0)
+    G.fill_normal(bd, 42, 22, 0.0, 0.02)
+    a16 = torch.empty((n, n), dtype=torch.float16, device=dev)
+    b16 = torch.empty((n, n), dtype=torch.float16, device=dev)
+    G.cast_f32_f16(ad, a16)
+    G.cast_f32_f16(bd, b16)
+    C = torch.empty((n, n), dtype=torch.float32, device=dev)
+    _say("C3 gemm")
+    G.gemm(a16, b16, C)
+    rows = np.random.default_rng(23).choice(n, 16, replace=False)
+    A = ad.cpu().numpy()
+    B = bd.cpu().numpy()
+    Cr = C[torch.from_numpy(rows).to(dev)].cpu().numpy()
+    err = O.rel_frob(Cr, O.gemm_f64_rows(A, B, rows))
+    err_r = O.rel_frob(Cr, O.gemm_f64_rows(O.round_f16(A[rows], False), O.round_f16(B, False), np.arange(16)))
+    _say("C3 relFrob vs fp32 inputs", err, "vs fp16-rounded inputs", err_r)
+    assert err <= 2e-2 and err_r <= 1e-5
+    assert torch.isfinite(C).all().item()
+
+
+@pytest.mark.parametrize("act", [G.ACT_RELU, G.ACT_GELU])
+def test_f16_c4_fused_linear(dev, act):
+    """Config C4: Y = act(X W^T + b), X 512x4096, W 11008x4096 (fp16), b fp32."""
+    X = O.normal((512, 4096), 42, 31)
+    W = O.normal((11008, 4096), 42, 32, 0.0, 0.02)
+    b = O.normal((11008,), 42, 33, 0.0, 0.01)
+    Y = _gemm_dev(dev, X, W, False, True, G.GN_F16, bias=b, act=act)
+    rows = np.arange(0, 512, 37)
+    pre = O.gemm_f64_rows(X, W, rows, transB=True) + b
+    ref = O.act_f64(act, pre)
+    err = O.rel_frob(Y[rows], ref)
+    _say("C4", act, "relFrob", err)
+    assert err <= 2e-2
+    pre_r = O.gemm_f64_rows(O.round_f16(X[rows], False), O.round_f16(W, False), np.arange(rows.size), transB=True) + b
+    ref_r = np.maximum(pre_r, 0) if act == G.ACT_RELU else O.act_f64(act, pre_r)
+    assert O.rel_frob(Y[rows], ref_r) <= 1e-5
+
+
+def test_fused_linear_reference_abi(dev):
+    """perform_fused_linear_activation (metal_bridge.h:1348-1353): W is [in, out]."""
+    rng = np.random.default_rng(29)
+    X = rng.standard_normal((40, 96)).astype(np.float32)
+    W = rng.standard_normal((96, 70)).astype(np.float32)
+    b = rng.standard_normal(70).astype(np.float32)
+    bx, bw, bb, by = G.Buffer.from_array(X), G.Buffer.from_array(W), G.Buffer.from_array(b), G.Buffer(40 * 70 * 4)
+    for act in (0, 7, 1, 2, 4, 5, 6):
+        G.call("perform_fused_linear_activation", bx.handle, 40, 96, bw.handle, 70, bb.handle, act, 0.2, by.handle, None)
+        Y = by.to_array((40, 70))
+        assert O.rel_frob(Y, O.linear_f64(X, W, b, act, 0, alpha=0.2)) <= 1e-5, act
+    # bias omitted (nullable)
+    G.call("perform_fused_linear_activation", bx.handle, 40, 96, bw.handle, 70, None, 0, 0.0, by.handle, None)
+    assert O.rel_frob(by.to_array((40, 70)), O.linear_f64(X, W, None, 0, 0)) <= 1e-5
+    # Softmax (3) is not an element-wise epilogue
+    rc, msg = G.call_rc("perform_fused_linear_activation", bx.handle, 40, 96, bw.handle, 70, None, 3, 0.0, by.handle,
+                        None)
+    assert rc == -1

@@ -1,0 +1,176 @@
+"""GPU parity of CSR SpMM / SpMV against the oracle's restatement of the reference
+loops (internal/cgo/metal_bridge_sparse.m:117-133, :325-339).
+
+SpMM accumulates in CSR order with one fma per stored entry, so it is compared
+bit-for-bit with the fmaf restatement; SpMV uses a parallel reduction and is held
+to relFrob <= 1e-5 against float64."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import gonngpu as G
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def _spmm_abi(rp, col, val, D, rows, cols):
+    N = D.shape[1]
+    bv = G.Buffer.from_array(val) if val.size else None
+    bd, bc = G.Buffer.from_array(D), G.Buffer(rows * N * 4)
+    col_ptr = col.ctypes.data if col.size else None
+    G.call("perform_sparse_dense_matmul", bv.handle if bv else None, rp.ctypes.data, rp.size, col_ptr, col.size, rows,
+           cols, val.size, bd.handle, cols, N, bc.handle, rows, N, None)
+    return bc.to_array((rows, N))
+
+
+def _spmv_abi(rp, col, val, x, rows, cols):
+    bv = G.Buffer.from_array(val) if val.size else None
+    bx, by = G.Buffer.from_array(x), G.Buffer(rows * 4)
+    col_ptr = col.ctypes.data if col.size else None
+    G.call("perform_sparse_matvec", bv.handle if bv else None, rp.ctypes.data, rp.size, col_ptr, col.size, rows, cols,
+           val.size, bx.handle, x.size, by.handle, rows, None)
+    return by.to_array((rows,))
+
+
+def test_spmm_golden_duplicates_zeros_empty_rows(dev):
+    z = np.load(os.path.join(GOLD, "csr_64.npz"))
+    rp, idx, data, D = z["rowptr"], z["idx"], z["data"], z["D"]
+    C = _spmm_abi(rp, idx, data, D, 64, 64)
+    np.testing.assert_array_equal(C, O.spmm_f32(rp, idx, data, D, use_fma=True))
+    assert O.rel_frob(C, z["C64"]) <= 1e-5
+    for r in (0, 5, 6, 31, 63):
+        assert np.all(C[r] == 0)
+
+
+@pytest.mark.parametrize("N", [1, 3, 4, 8, 20, 64, 100, 256, 300, 512])
+def test_spmm_widths_bit_exact(dev, N):
+    rp, col, val = O.random_csr(700, 900, 9.0, seed=N)
+    D = O.normal((900, N), 5, N)
+    C = _spmm_abi(rp, col, val, D, 700, 900)
+    np.testing.assert_array_equal(C, O.spmm_f32(rp, col, val, D, use_fma=True))
+
+
+def test_spmm_with_duplicates_unsorted_columns(dev):
+    rp, col, val = O.random_csr(300, 50, 20.0, seed=3, distinct=False)  # many duplicate columns
+    D = O.normal((50, 256), 6, 1)
+    C = _spmm_abi(rp, col, val, D, 300, 50)
+    np.testing.assert_array_equal(C, O.spmm_f32(rp, col, val, D, use_fma=True))
+    assert O.rel_frob(C, O.spmm_f64(rp, col, val, D)) <= 1e-5
+
+
+def test_spmm_nnz_zero_gives_zero(dev):
+    rp = np.zeros(11, np.int32)
+    D = O.normal((7, 16), 1, 1)
+    C = _spmm_abi(rp, np.zeros(0, np.int32), np.zeros(0, np.float32), D, 10, 7)
+    assert np.all(C == 0)
+
+
+def test_spmm_malformed_csr_is_an_error(dev):
+    rp = np.array([0, 2, 3], np.int32)
+    col = np.array([0, 9, 1], np.int32)  # 9 >= cols
+    val = np.ones(3, np.float32)
+    D = np.ones((4, 8), np.float32)
+    bv, bd, bc = G.Buffer.from_array(val), G.Buffer.from_array(D), G.Buffer(2 * 8 * 4)
+    rc, msg = G.call_rc("perform_sparse_dense_matmul", bv.handle, rp.ctypes.data, 3, col.ctypes.data, 3, 2, 4, 3,
+                        bd.handle, 4, 8, bc.handle, 2, 8, None)
+    assert rc == -3 and "column" in msg
+    rp_bad = np.array([0, 3, 2], np.int32)  # decreasing
+    col_ok = np.array([0, 1, 2], np.int32)
+    rc, msg = G.call_rc("perform_sparse_dense_matmul", bv.handle, rp_bad.ctypes.data, 3, col_ok.ctypes.data, 3, 2, 4, 3,
+                        bd.handle, 4, 8, bc.handle, 2, 8, None)
+    assert rc == -3 and "row pointers" in msg
+    # dimension mismatch: A cols != B rows
+    rc, _ = G.call_rc("perform_sparse_dense_matmul", bv.handle, rp.ctypes.data, 3, col_ok.ctypes.data, 3, 2, 5, 3,
+                      bd.handle, 4, 8, bc.handle, 2, 8, None)
+    assert rc == -2
+
+
+def test_spmm_c5_full_size_device_api(dev):
+    """Config C5: 65536x65536 CSR at 0.1% density (~4.3M nnz) x 65536x256."""
+    import torch
+
+    M = K = 65536
+    N = 256
+    rp, col, val = O.random_csr(M, K, 65.536, seed=42)
+    nnz = val.size
+    _say("C5 nnz", nnz)
+    d_rp = torch.from_numpy(rp).to(dev)
+    d_col = torch.from_numpy(col).to(dev)
+    d_val = torch.from_numpy(val).to(dev)
+    Dd = torch.empty((K, N), dtype=torch.float32, device=dev)
+    G.fill_normal(Dd, 42, 41)
+    Cd = torch.empty((M, N), dtype=torch.float32, device=dev)
+    flags = torch.zeros(2, dtype=torch.int32, device=dev)
+    G.spmm_csr(M, N, K, nnz, d_rp, d_col, d_val, Dd, Cd, flags)
+    assert flags.cpu().tolist() == [0, 0]
+    D = Dd.cpu().numpy()
+    C = Cd.cpu().numpy()
+    # sampled rows: bit-exact against the CSR-order fmaf loop
+    rows = np.random.default_rng(1).choice(M, 512, replace=False)
+    sub_rp = np.zeros(rows.size + 1, np.int32)
+    sub_rp[1:] = np.cumsum(rp[rows + 1] - rp[rows])
+    sub_col = np.concatenate([col[rp[r]:rp[r + 1]] for r in rows])
+    sub_val = np.concatenate([val[rp[r]:rp[r + 1]] for r in rows])
+    np.testing.assert_array_equal(C[rows], O.spmm_f32(sub_rp, sub_col, sub_val, D, use_fma=True))
+    # whole-output property: column sums 1^T C = (1^T S) D, in float64
+    colsum_S = np.bincount(col, weights=val.astype(np.float64), minlength=K)
+    lhs = C.astype(np.float64).sum(axis=0)
+    rhs = colsum_S @ D.astype(np.float64)
+    assert np.linalg.norm(lhs - rhs) / np.linalg.norm(rhs) <= 1e-5
+
+
+def test_spmv_golden_and_random(dev):
+    z = np.load(os.path.join(GOLD, "csr_64.npz"))
+    y = _spmv_abi(z["rowptr"], z["idx"], z["data"], z["x"], 64, 64)
+    assert O.rel_frob(y, z["y64"]) <= 1e-5
+    for mean in (0.5, 3.0, 40.0, 300.0):
+        rp, col, val = O.random_csr(1000, 2000, mean, seed=int(mean * 10))
+        x = O.normal((2000,), 3, int(mean))
+        y = _spmv_abi(rp, col, val, x, 1000, 2000)
+        assert O.rel_frob(y, O.spmv_f64(rp, col, val, x)) <= 1e-5
+        assert O.rel_frob(y, O.spmv_f32(rp, col, val, x).astype(np.float64)) <= 1e-5
+
+
+def test_spmv_dimension_and_csr_errors(dev):
+    rp = np.array([0, 1], np.int32)
+    col = np.array([5], np.int32)
+    val = np.ones(1, np.float32)
+    bv, bx, by = G.Buffer.from_array(val), G.Buffer.from_array(np.ones(3, np.float32)), G.Buffer(4)
+    rc, _ = G.call_rc("perform_sparse_matvec", bv.handle, rp.ctypes.data, 2, col.ctypes.data, 1, 1, 3, 1, bx.handle, 4,
+                      by.handle, 1, None)
+    assert rc == -1  # aCols != xSize
+    rc, msg = G.call_rc("perform_sparse_matvec", bv.handle, rp.ctypes.data, 2, col.ctypes.data, 1, 1, 3, 1, bx.handle,
+                        3, by.handle, 1, None)
+    assert rc == -3 and "column" in msg
+
+
+def test_spmv_c5_full_size(dev):
+    import torch
+
+    M = K = 65536
+    rp, col, val = O.random_csr(M, K, 65.536, seed=42)
+    x = O.normal((K,), 42, 51)
+    d = [torch.from_numpy(a).to(dev) for a in (rp, col, val, x)]
+    y = torch.empty(M, dtype=torch.float32, device=dev)
+    G.spmv_csr(M, K, val.size, d[0], d[1], d[2], d[3], y)
+    assert O.rel_frob(y.cpu().numpy(), O.spmv_f64(rp, col, val, x)) <= 1e-5
+
+
+def test_transpose_reference_abi(dev):
+    """perform_mps_matrix_transpose (metal_bridge.h:36-41)."""
+    for (r, c) in [(1, 1), (3, 70), (64, 64), (257, 129), (1000, 3)]:
+        X = O.normal((r, c), 9, r * 1000 + c)
+        bi, bo = G.Buffer.from_array(X), G.Buffer(r * c * 4)
+        G.call("perform_mps_matrix_transpose", bi.handle, r, c, bo.handle, c, r, None)
+        np.testing.assert_array_equal(bo.to_array((c, r)), O.transpose_f32(X))
+    rc, _ = G.call_rc("perform_mps_matrix_transpose", bi.handle, 1000, 3, bo.handle, 1000, 3, None)
+    assert rc == -2
