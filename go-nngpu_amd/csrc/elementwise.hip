@@ -5,8 +5,8 @@
 namespace gn {
 namespace {
 
-typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 unsigned grid_for(size_t work_items, unsigned block) {
   size_t g = (work_items + block - 1) / block;
@@ -40,13 +40,17 @@ __device__ __forceinline__ uint32_t f16_rne(float x) {
   return __builtin_bit_cast(uint16_t, h);
 }
 
+// The 16-byte load is taken as raw bits; each element is copied into a scalar
+// before any bit reinterpretation (a bit cast applied directly to a vector-element
+// lvalue reads the vector's first element, whatever the index).
 template <int MODE>
-__global__ void cast_f32_f16_vec(const float4_t *__restrict__ in, u32x2_t *__restrict__ out, size_t n4) {
+__global__ void cast_f32_f16_vec(const u32x4_t *__restrict__ in, u32x2_t *__restrict__ out, size_t n4) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
-    const float4_t v = in[i];
+    const u32x4_t v = in[i];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
     uint32_t h[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) h[e] = MODE ? f16_rtz_ref(__builtin_bit_cast(uint32_t, v[e])) : f16_rne(v[e]);
+    for (int e = 0; e < 4; ++e) h[e] = MODE ? f16_rtz_ref(w[e]) : f16_rne(__builtin_bit_cast(float, w[e]));
     out[i] = u32x2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
   }
 }
@@ -131,9 +135,9 @@ int launch_cast_f32_f16(const float *in, uint16_t *out, size_t n, int mode, hipS
   if (vec) {
     const size_t n4 = n / 4;
     if (mode) hipLaunchKernelGGL(cast_f32_f16_vec<1>, dim3(grid_for(n4, 256)), dim3(256), 0, s,
-                                 (const float4_t *)in, (u32x2_t *)out, n4);
+                                 (const u32x4_t *)in, (u32x2_t *)out, n4);
     else hipLaunchKernelGGL(cast_f32_f16_vec<0>, dim3(grid_for(n4, 256)), dim3(256), 0, s,
-                            (const float4_t *)in, (u32x2_t *)out, n4);
+                            (const u32x4_t *)in, (u32x2_t *)out, n4);
   } else {
     if (mode) hipLaunchKernelGGL(cast_f32_f16_scalar<1>, dim3(grid_for(n, 256)), dim3(256), 0, s, in, out, n);
     else hipLaunchKernelGGL(cast_f32_f16_scalar<0>, dim3(grid_for(n, 256)), dim3(256), 0, s, in, out, n);

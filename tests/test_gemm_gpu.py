@@ -269,7 +269,9 @@ def test_f16_c4_fused_linear(dev, act):
     X = O.normal((512, 4096), 42, 31)
     W = O.normal((11008, 4096), 42, 32, 0.0, 0.02)
     b = O.normal((11008,), 42, 33, 0.0, 0.01)
-    Y = _gemm_dev(dev, X, W, False, True, G.GN_F16, bias=b, act=act)
+    # _gemm_dev takes the logical K x N operand; W^T stored transposed is W itself.
+    Y = _gemm_dev(dev, X, W.T, False, True, G.GN_F16, bias=b, act=act)
+    assert Y.shape == (512, 11008)
     rows = np.arange(0, 512, 37)
     pre = O.gemm_f64_rows(X, W, rows, transB=True) + b
     ref = O.act_f64(act, pre)
