@@ -223,7 +223,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default=None, help="comma list of " + ",".join(ALL))
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=512)
+    ap.add_argument("--cpu-rows", type=int, default=4096)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (single-GPU build; the path's "
