@@ -223,7 +223,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default=None, help="comma list of " + ",".join(ALL))
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=4096)
+    ap.add_argument("--cpu-rows", type=int, default=6144)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (single-GPU build; the path's "
@@ -269,7 +269,7 @@ def main():
         roofline = {"bound": "mfma", "achieved": round(head["tflops"], 2), "peak": PEAK_F16_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(head["tflops"] / PEAK_F16_TFLOPS, 4),
                     "traffic": load_traffic("gemm_f16_8192_nn"),
-                    "kernel": "gemm_f16_kernel<256,256,64,2,4,NN>", "flop_per_launch": head["flop"]}
+                    "kernel": "gemm_f16_ring_kernel<256,256,2,4,4,NN>", "flop_per_launch": head["flop"]}
     out = {
         "metric": METRIC,
         "value": round(head["tflops"], 2) if head else None,

@@ -148,6 +148,18 @@ struct TileLoader {
       *reinterpret_cast<u32x4_t *>(lds + r * P + c) = reg[j];
     }
   }
+  // Same-layout store for an MN-contiguous fp16 tile that frag_tr reads: the
+  // 16-half column block is XOR-swizzled by bit 3 of the row (frag_tr undoes it).
+  template <int P>
+  __device__ __forceinline__ void store_sw(T *lds) const {
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int v = threadIdx.x + j * NT;
+      const int r = v / VPR;
+      const int c = (v % VPR) * EPV;
+      *reinterpret_cast<u32x4_t *>(lds + r * P + (c ^ ((r & 8) << 1))) = reg[j];
+    }
+  }
   // Transposed store (fp32 only): element (r, c+e) goes to lds[(c+e)*P + r].
   template <int P>
   __device__ __forceinline__ void store_t(T *lds) const {
@@ -176,7 +188,8 @@ __device__ __forceinline__ half8_t frag_kc(const _Float16 *lds, int P, int row0,
 __device__ __forceinline__ half8_t frag_tr(const _Float16 *lds, int P, int col0, int k0) {
   const int lane = threadIdx.x & 63;
   const int s = lane & 15, g = lane >> 4;
-  const _Float16 *p0 = lds + (k0 + 8 * g + (s >> 2)) * P + col0 + 4 * (s & 3);
+  const int row = k0 + 8 * g + (s >> 2);
+  const _Float16 *p0 = lds + row * P + ((col0 + 4 * (s & 3)) ^ ((row & 8) << 1));
   const _Float16 *p1 = p0 + 4 * P;
   trh4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((LDS_AS trh4_t *)(p0));
   trh4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((LDS_AS trh4_t *)(p1));
@@ -192,9 +205,16 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f16_kernel(GemmParams p) {
   constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
   constexpr int FM = WTM / 16, FN = WTN / 16;  // 16x16 blocks per wave
   static_assert(BK % 32 == 0 && WTM % 16 == 0 && WTN % 16 == 0, "tile shape");
-  // LDS pitches (halves): K-contiguous rows get +8 (16 B); MN-contiguous rows +16.
-  constexpr int PA = TA ? BM + 16 : BK + 8;
-  constexpr int PB = TB ? BK + 8 : BN + 16;
+  // LDS pitches (halves). gfx950's LDS has 64 four-byte banks. K-contiguous rows get
+  // +8 halves: the 16 rows one 16-lane phase of ds_read_b128 touches then start on
+  // distinct 4-bank groups. MN-contiguous rows get +32 halves (pitch = 16 or 48
+  // banks mod 64) plus the row-bit-3 XOR of store_sw / frag_tr: the 8 rows (k0+8g+r,
+  // g < 2, r < 4) one 32-lane phase of ds_read_b64_tr_b16 touches then cover all 64
+  // banks exactly once.
+  constexpr int PA = TA ? BM + 32 : BK + 8;
+  constexpr int PB = TB ? BK + 8 : BN + 32;
+  static_assert(TA ? (PA % 128 == 32 || PA % 128 == 96) : true, "MN-contiguous pitch");
+  static_assert(TB ? true : (PB % 128 == 32 || PB % 128 == 96), "MN-contiguous pitch");
   constexpr int A_ELEMS = TA ? BK * PA : BM * PA;
   constexpr int B_ELEMS = TB ? BN * PB : BK * PB;
   __shared__ __attribute__((aligned(16))) _Float16 smem[2 * (A_ELEMS + B_ELEMS)];
@@ -222,8 +242,8 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f16_kernel(GemmParams p) {
   auto store_tiles = [&](int stage) {
     _Float16 *as = smem + stage * (A_ELEMS + B_ELEMS);
     _Float16 *bs = as + A_ELEMS;
-    la.template store<PA>(as);
-    lb.template store<PB>(bs);
+    if (TA) la.template store_sw<PA>(as); else la.template store<PA>(as);
+    if (TB) lb.template store<PB>(bs); else lb.template store_sw<PB>(bs);
   };
 
   float4_t acc[FM][FN];
@@ -358,6 +378,274 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32_kernel(GemmParams p) {
       store_block(p, C, m0 + wm * WTM + i * 16, n0 + wn * WTN + j * 16, acc[i][j]);
 }
 
+// ------------------------------------------------------------------ fp16 DMA-ring kernel
+// Large aligned fp16 GEMMs. Differences from gemm_f16_kernel:
+//  * global -> LDS copies are buffer loads with the LDS-direct bit (16 bytes per lane
+//    written to M0 + 16*lane): no staging VGPRs and no ds_write instructions, so a
+//    4-stage LDS ring keeps 3 K-tiles in flight (BK = 32, 32 KiB per stage);
+//  * out-of-range lanes (rows past M/N, the K tail) get a buffer offset beyond the
+//    descriptor's range, which the hardware turns into zeros;
+//  * K-contiguous operands are written in MFMA fragment order: each 1 KiB chunk holds
+//    the 16 x 32 fragment block of rows 16c..16c+15 with lane L's 16 bytes at 16*L,
+//    so a fragment is one contiguous 1 KiB ds_read_b128 (measured ~1.5x the
+//    throughput of row-strided b128 reads on gfx950);
+//  * MN-contiguous operands keep their memory layout, rows of 2*BM (or 2*BN) bytes,
+//    with the 32-byte block index XORed by hsw(k) so the 8 rows one 32-lane phase of
+//    ds_read_b64_tr_b16 reads (k0+8g+r, g < 2, r < 4) fall on distinct banks;
+//  * MFMA fragments are double-buffered in registers: tile k+1's fragments are read
+//    while tile k's MFMAs run, one barrier per K-tile.
+// The DMA is issued from inline assembly so the compiler does not track these LDS
+// writes (it would otherwise wait for every outstanding load before each LDS read);
+// the kernel orders them itself with s_waitcnt vmcnt and the per-tile barrier.
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+struct BufRsrc {
+  i32x4_t r;
+};
+
+// Raw buffer descriptor: 48-bit base, stride 0, num_records 0x7ffffff0 (offsets at or
+// beyond it read as zero), gfx9 dword3.
+__device__ __forceinline__ BufRsrc make_rsrc(const void *base) {
+  const unsigned long long b = (unsigned long long)base;
+  BufRsrc s;
+  s.r.x = __builtin_amdgcn_readfirstlane((int)(b & 0xffffffffu));
+  s.r.y = __builtin_amdgcn_readfirstlane((int)(b >> 32) & 0xffff);
+  s.r.z = 0x7ffffff0;
+  s.r.w = 0x00020000;
+  return s;
+}
+
+__device__ __forceinline__ void rsrc_advance(BufRsrc &s, long bytes) {
+  unsigned long long b =
+      ((unsigned long long)(unsigned)s.r.x) | ((unsigned long long)(unsigned)(s.r.y & 0xffff) << 32);
+  b += (unsigned long long)bytes;
+  s.r.x = __builtin_amdgcn_readfirstlane((int)(b & 0xffffffffu));
+  s.r.y = __builtin_amdgcn_readfirstlane((int)(b >> 32) & 0xffff);
+}
+
+// 16 bytes per lane from the buffer at voff into LDS at lds + 16 * lane (lds is
+// wave-uniform). M0 is saved and restored around the load.
+__device__ __forceinline__ void dma16(const BufRsrc &s, unsigned voff, unsigned lds) {
+  int saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(s.r), "s"(lds)
+      : "memory");
+}
+
+constexpr unsigned kOutOfRange = 0x80000000u;
+
+// s_waitcnt immediate that waits for vmcnt <= n only (vmcnt[3:0] in bits 3:0 and
+// vmcnt[5:4] in bits 15:14; expcnt and lgkmcnt at their maxima).
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
+__device__ __forceinline__ unsigned lds_offset(const void *p) {
+  return (unsigned)(unsigned long)(const LDS_AS void *)p;
+}
+
+// 32-byte block XOR of row k of an MN-contiguous tile.
+__device__ __forceinline__ int hsw(int k) { return (k & 3) | ((k >> 1) & 4); }
+
+template <int BM, int BN, int WM, int WN, int S, bool TA, bool TB>
+__global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+gemm_f16_ring_kernel(GemmParams p) {
+  constexpr int BK = 32;
+  constexpr int NW = WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 16, FN = WTN / 16;
+  constexpr int OPA = BM * BK * 2;           // bytes of A per stage
+  constexpr int OPB = BN * BK * 2;           // bytes of B per stage (at offset OPA)
+  constexpr int STB = OPA + OPB;             // bytes per stage
+  constexpr int IPA = BM / 16 / NW;          // 1 KiB DMA chunks per wave per tile, A
+  constexpr int IPB = BN / 16 / NW;          //   ... and B
+  constexpr int RBA = TA ? BM * 2 : BK * 2;  // LDS row bytes of the A / B tiles
+  constexpr int RBB = TB ? BK * 2 : BN * 2;
+  constexpr int LPW = IPA + IPB;             // DMA instructions per wave per tile
+  static_assert(IPA >= 1 && IPB >= 1 && BM % (16 * NW) == 0 && BN % (16 * NW) == 0, "DMA split");
+  static_assert(S >= 3 && (S - 2) * LPW < 64, "ring depth");
+  static_assert((!TA || BM >= 128) && (TB || BN >= 128), "MN-contiguous rows need 8 XOR blocks of 32 B");
+  __shared__ __attribute__((aligned(1024))) char smem[S * STB];
+
+  int tm, tn;
+  tile_coords(p, tm, tn);
+  const long m0 = (long)tm * BM, n0 = (long)tn * BN;
+  const long z = blockIdx.z;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wm = wave / WN, wn = wave % WN;
+
+  // Per-lane DMA plan, fixed for the whole K loop. K-contiguous: chunk c = rows
+  // 16c..16c+15 in fragment order. MN-contiguous: chunk c = k rows c*(1024/RB).. .
+  BufRsrc ra, rb;
+  unsigned voa[IPA], vob[IPB];
+  int kla[IPA], klb[IPB];   // k within the tile that the lane loads
+  bool rva[IPA], rvb[IPB];  // row (K-contiguous) or column block (MN-contiguous) in range
+  {
+    const _Float16 *A = static_cast<const _Float16 *>(p.A) + z * p.strideA;
+    const _Float16 *B = static_cast<const _Float16 *>(p.B) + z * p.strideB;
+    ra = make_rsrc(TA ? (const void *)(A + m0) : (const void *)(A + m0 * p.lda));
+    rb = make_rsrc(TB ? (const void *)(B + n0 * p.ldb) : (const void *)(B + n0));
+#pragma unroll
+    for (int i = 0; i < IPA; ++i) {
+      const int c = wave * IPA + i;
+      if (!TA) {
+        const int r = c * 16 + (lane & 15), q = lane >> 4;
+        kla[i] = 8 * q;
+        rva[i] = m0 + r < p.M;
+        voa[i] = (unsigned)((long)r * p.lda * 2 + 16 * q);
+      } else {
+        constexpr int GPR = RBA / 16;
+        const int k = c * (1024 / RBA) + lane / GPR, qp = lane % GPR;
+        const int q = 2 * ((qp >> 1) ^ hsw(k)) + (qp & 1);
+        kla[i] = k;
+        rva[i] = m0 + 8 * q < p.M;
+        voa[i] = (unsigned)((long)k * p.lda * 2 + 16 * q);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < IPB; ++i) {
+      const int c = wave * IPB + i;
+      if (TB) {
+        const int r = c * 16 + (lane & 15), q = lane >> 4;
+        klb[i] = 8 * q;
+        rvb[i] = n0 + r < p.N;
+        vob[i] = (unsigned)((long)r * p.ldb * 2 + 16 * q);
+      } else {
+        constexpr int GPR = RBB / 16;
+        const int k = c * (1024 / RBB) + lane / GPR, qp = lane % GPR;
+        const int q = 2 * ((qp >> 1) ^ hsw(k)) + (qp & 1);
+        klb[i] = k;
+        rvb[i] = n0 + 8 * q < p.N;
+        vob[i] = (unsigned)((long)k * p.ldb * 2 + 16 * q);
+      }
+    }
+  }
+  const long a_step = TA ? (long)BK * p.lda * 2 : (long)BK * 2;
+  const long b_step = TB ? (long)BK * 2 : (long)BK * p.ldb * 2;
+  const unsigned sbase = lds_offset(smem);
+  const int nk = (int)((p.K + BK - 1) / BK);
+
+  auto issue = [&](int t) {  // DMA of K-tile t into stage t % S (descriptors point at tile t)
+    const unsigned st = sbase + (unsigned)((t % S) * STB);
+    const long krem = p.K - (long)t * BK;
+#pragma unroll
+    for (int i = 0; i < IPA; ++i)
+      dma16(ra, (rva[i] && kla[i] < krem) ? voa[i] : kOutOfRange,
+            __builtin_amdgcn_readfirstlane(st + (wave * IPA + i) * 1024));
+#pragma unroll
+    for (int i = 0; i < IPB; ++i)
+      dma16(rb, (rvb[i] && klb[i] < krem) ? vob[i] : kOutOfRange,
+            __builtin_amdgcn_readfirstlane(st + OPA + (wave * IPB + i) * 1024));
+    rsrc_advance(ra, a_step);
+    rsrc_advance(rb, b_step);
+  };
+
+  auto frag_k = [&](const char *base, int row0) -> half8_t {
+    return *reinterpret_cast<const half8_t *>(base + (row0 >> 4) * 1024 + lane * 16);
+  };
+  auto frag_t = [&](const char *base, int col0, int rowb) -> half8_t {
+    const int s = lane & 15, g = lane >> 4;
+    const int k = 8 * g + (s >> 2);
+    const int col = col0 + 4 * (s & 3);
+    const char *p0 = base + k * rowb + (((col >> 4) ^ hsw(k)) << 5) + ((col & 15) << 1);
+    const trh4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((LDS_AS trh4_t *)(p0));
+    const trh4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((LDS_AS trh4_t *)(p0 + 4 * rowb));
+    const half4_t l4 = __builtin_bit_cast(half4_t, lo);
+    const half4_t h4 = __builtin_bit_cast(half4_t, hi);
+    return __builtin_shufflevector(l4, h4, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+
+  half8_t fa[2][FM], fb[2][FN];
+  auto read_frags = [&](int t, int set) {
+    const char *st = smem + (t % S) * STB;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      fa[set][i] = TA ? frag_t(st, wm * WTM + i * 16, RBA) : frag_k(st, wm * WTM + i * 16);
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      fb[set][j] = TB ? frag_k(st + OPA, wn * WTN + j * 16) : frag_t(st + OPA, wn * WTN + j * 16, RBB);
+  };
+
+  float4_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+  auto mfma_set = [&](int set) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
+  };
+
+  // Prologue: tiles 0..S-2 in flight; wait for tile 0.
+  for (int t = 0; t < S - 1 && t < nk; ++t) issue(t);
+  {
+    const int after = min(nk - 1, S - 2);  // tiles issued after tile 0
+    if (after >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LPW));
+    else if (after == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPW));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  }
+  __syncthreads();
+  if (nk > 0) read_frags(0, 0);
+
+  // Steady state (tiles k+1..k+S-1 exist): tile k+1 has landed (tiles k+2..k+S-2 may
+  // still be in flight); publish it, refill the stage tile k-1 used with tile k+S-1,
+  // read tile k+1's fragments into the other register set, multiply tile k. The
+  // scheduling fences keep tile k's MFMAs ahead of the next barrier, and the group
+  // barriers interleave one LDS read per MFMA.
+  auto steady = [&](int k, int set) {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 3) * LPW));
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(k + S - 1);
+    read_frags(k + 1, set ^ 1);
+    mfma_set(set);
+#pragma unroll
+    for (int g = 0; g < FM + 2 * FN; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - (FM + 2 * FN), 0);
+  };
+  // Last S-1 or fewer tiles: same steps with the waits and refills the tail allows.
+  auto tail = [&](int k, int set) {
+    if (k + 1 < nk) {
+      const int after = min(nk - 1, k + S - 2) - (k + 1);  // tiles issued after k+1
+      if (after >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LPW));
+      else if (after == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPW));
+      else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      __syncthreads();
+      if (k + S - 1 < nk) issue(k + S - 1);
+      read_frags(k + 1, set ^ 1);
+    }
+    mfma_set(set);
+  };
+  int k = 0;
+  for (; k + S < nk; k += 2) {
+    steady(k, 0);
+    steady(k + 1, 1);
+  }
+#pragma unroll
+  for (int u = 0; u < S; u += 2) {
+    if (k + u < nk) tail(k + u, 0);
+    if (k + u + 1 < nk) tail(k + u + 1, 1);
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+
+  float *C = p.C + z * p.strideC;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) store_block(p, C, m0 + wm * WTM + i * 16, n0 + wn * WTN + j * 16, acc[i][j]);
+}
+
 // ------------------------------------------------------------------ dispatch
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VEC>
 hipError_t launch_f16(GemmParams p, long batch, hipStream_t s) {
@@ -377,6 +665,19 @@ hipError_t launch_f32(GemmParams p, long batch, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int BM, int BN, int WM, int WN, int S, bool TA, bool TB>
+hipError_t launch_f16_ring(GemmParams p, long batch, hipStream_t s) {
+  p.tiles_m = (int)((p.M + BM - 1) / BM);
+  p.tiles_n = (int)((p.N + BN - 1) / BN);
+  dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
+  hipLaunchKernelGGL((gemm_f16_ring_kernel<BM, BN, WM, WN, S, TA, TB>), grid, dim3(WM * WN * 64), 0, s, p);
+  return hipGetLastError();
+}
+
+// The ring kernel's 32-bit buffer offsets reach 256 rows (K-contiguous) or 32 k-rows
+// (MN-contiguous) past the tile base.
+bool ring_offsets_fit(const GemmParams &p) { return p.lda < (1L << 21) && p.ldb < (1L << 21); }
+
 template <bool TA, bool TB, bool VEC>
 hipError_t pick_f16(const GemmParams &p, long batch, hipStream_t s) {
   if constexpr (!VEC) {
@@ -384,6 +685,7 @@ hipError_t pick_f16(const GemmParams &p, long batch, hipStream_t s) {
     return launch_f16<64, 64, 64, 2, 2, TA, TB, VEC>(p, batch, s);
   } else {
     const long tiles256 = ((p.M + 255) / 256) * ((p.N + 255) / 256) * batch;
+    if (tiles256 >= 256 && ring_offsets_fit(p)) return launch_f16_ring<256, 256, 2, 4, 4, TA, TB>(p, batch, s);
     if (tiles256 >= 512) return launch_f16<256, 256, 64, 2, 4, TA, TB, VEC>(p, batch, s);
     const long tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
     if (tiles128 >= 128) return launch_f16<128, 128, 64, 2, 2, TA, TB, VEC>(p, batch, s);

@@ -301,3 +301,52 @@ def test_fused_linear_reference_abi(dev):
     rc, msg = G.call_rc("perform_fused_linear_activation", bx.handle, 40, 96, bw.handle, 70, None, 3, 0.0, by.handle,
                         None)
     assert rc == -1
+
+
+# ------------------------------------------------------------------ fp16 ring kernel (large aligned shapes)
+@pytest.mark.parametrize("tA,tB", VARIANTS)
+def test_f16_ring_ragged_all_transposes(dev, tA, tB):
+    """Shapes large enough for the buffer->LDS ring kernel (>= 256 tiles of 256x256) with
+    M, N not multiples of 256 and K not a multiple of the 32-deep K tile: out-of-range
+    rows, columns and the K tail must read as zeros."""
+    rng = np.random.default_rng(31)
+    M, N, K = 4000, 4104, 1000
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
+    C = _gemm_dev(dev, A, B, tA, tB, G.GN_F16)
+    rows = np.concatenate([np.arange(0, 16), rng.choice(M, 24, replace=False), np.arange(M - 16, M)])
+    ref_r = O.gemm_f64_rows(O.round_f16(A[rows], False), O.round_f16(B, False), np.arange(rows.size))
+    err = O.rel_frob(C[rows], ref_r)
+    _say("ring ragged", tA, tB, err)
+    assert err <= 1e-5
+    assert np.isfinite(C).all()
+
+
+def test_f16_ring_transpose_variants_bit_identical(dev):
+    rng = np.random.default_rng(37)
+    A = rng.standard_normal((4096, 512)).astype(np.float32)
+    B = rng.standard_normal((512, 4096)).astype(np.float32)
+    outs = [_gemm_dev(dev, A, B, tA, tB, G.GN_F16) for tA, tB in VARIANTS]
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])
+
+
+def test_f16_ring_batched_and_epilogue(dev):
+    """Batched strides and the bias + GELU epilogue on the ring kernel (4 x 2048^2)."""
+    import torch
+
+    rng = np.random.default_rng(41)
+    bs, M, N, K = 4, 2048, 2048, 512
+    A = rng.standard_normal((bs, M, K)).astype(np.float32)
+    B = (0.05 * rng.standard_normal((bs, K, N))).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    a16 = torch.from_numpy(A).to(dev).half()
+    b16 = torch.from_numpy(B).to(dev).half()
+    C = torch.empty((bs, M, N), dtype=torch.float32, device=dev)
+    G.gemm(a16, b16, C, batch=bs, strideA=M * K, strideB=K * N, strideC=M * N,
+           bias=torch.from_numpy(bias).to(dev), act=G.ACT_GELU)
+    Cn = C.cpu().numpy()
+    rows = rng.choice(M, 12, replace=False)
+    for z in range(bs):
+        pre = O.gemm_f64_rows(O.round_f16(A[z][rows], False), O.round_f16(B[z], False), np.arange(rows.size)) + bias
+        assert O.rel_frob(Cn[z][rows], O.act_f64(G.ACT_GELU, pre)) <= 1e-5, z
