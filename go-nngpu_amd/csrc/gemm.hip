@@ -7,7 +7,10 @@
 // kernels (metal_bridge_kernels.m:28-110) and the fused_linear_activation kernel
 // (default.metal:459-509).
 //
-// Structure (one workgroup per BM x BN output tile, WM x WN waves, 64 lanes each):
+// Two kernel families share the epilogue and the tile order: gemm_f16_ring_kernel
+// (large aligned fp16 problems; described at its definition) and the register-staged
+// gemm_f16_kernel / gemm_f32_kernel for every other shape, structured as follows
+// (one workgroup per BM x BN output tile, WM x WN waves, 64 lanes each):
 //  * global -> VGPR prefetch of the next BK slice overlaps the MFMAs of the current
 //    one; LDS is double buffered, one barrier per BK slice;
 //  * operands whose K index is contiguous in memory are kept K-contiguous in LDS and
