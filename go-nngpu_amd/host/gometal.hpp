@@ -1,0 +1,344 @@
+// gometal.hpp — C++ host API of the MI355X GEMM/SpMM backend, mirroring the Go
+// packages of go-nngpu (module github.com/tsawler/gometal) for the matmul path:
+//
+//   gometal::tensor   tensor/tensor.go, tensor/sparse-tensor.go
+//   gometal::matrix   gpu/matrix/matrix.go (MatMul, Transpose), sparse-matrix.go
+//                     (SparseMatMul, SparseMatVec, SparseTranspose), optimized-kernels.go
+//                     (OptimizedGEMM, OptimizedBatchMatMul), fused-operations.go
+//                     (FusedLinearActivation), mixed-precision.go (FloatMP16,
+//                     MixedPrecisionTrainer), layers.go (LinearLayer), activation.go
+//                     (ActivationType), gonum-compat.go (GPUDense, GPUMatMul),
+//                     sparse-gonum-compat.go (GPUSparse, GPUSparseMatMul)
+//   gometal::mat      the part of gonum's mat package those files use: the Matrix
+//                     interface and a row-major float64 Dense
+//
+// Names, argument meaning and error behaviour follow the Go code. Go's (T, error)
+// returns become Result<T> (usable as `auto [t, err] = ...`); a nil error is an empty
+// Error. Go panics (the gonum-compatible wrappers panic on failure) become a thrown
+// gometal::Panic. Every device operation goes through the C ABI in include/gonngpu.h,
+// exactly as the Go code goes through cgo.
+//
+// Residency: a Tensor's device copy is a GPUPtr from create_gpu_buffer. Unlike the
+// reference's Metal buffers it does not alias Data: EnsureGPU copies Data to the
+// device, RetrieveCPU copies the device copy back into Data and marks the tensor as
+// host-resident (isOnGPU = false, as tensor/tensor.go:182 does), and the next
+// EnsureGPU uploads Data again, so host writes between the two are seen. The device
+// allocation is released when it is replaced or when the tensor is destroyed.
+#pragma once
+
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace gometal {
+
+// ---------------------------------------------------------------- errors
+struct Error {
+  std::string message;
+  explicit operator bool() const { return !message.empty(); }  // true = an error
+};
+Error Errorf(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+
+template <typename T>
+struct Result {
+  T value;
+  Error err;
+};
+
+// A Go panic raised by the gonum-compatible wrappers.
+struct Panic : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+namespace tensor {
+
+class Tensor;
+class SparseTensor;
+using TensorPtr = std::shared_ptr<Tensor>;
+using SparseTensorPtr = std::shared_ptr<SparseTensor>;
+
+// GetGlobalMemoryStats (tensor/tensor.go:74-77): bytes held by tensors' device
+// copies, the peak of that, and the number of live allocations.
+struct MemoryStats {
+  int64_t currentUsage, peakUsage;
+  int numAllocations;
+};
+MemoryStats GetGlobalMemoryStats();
+
+// tensor.Tensor (tensor/tensor.go:80-87): fp32 data with shape, plus a device copy.
+class Tensor {
+ public:
+  std::vector<int> Shape;
+  std::vector<float> Data;
+
+  Tensor() = default;
+  Tensor(const Tensor &) = delete;
+  Tensor &operator=(const Tensor &) = delete;
+  ~Tensor();
+
+  Error EnsureGPU();   // tensor.go:113-150
+  Error RetrieveCPU();  // tensor.go:154-184
+  void ReleaseGPU();   // tensor.go:189-202
+  void *GPUPtr() const { return gpuPtr_; }        // tensor.go:206
+  void *DevicePtr() const { return devicePtr_; }  // tensor.go:211
+  bool IsOnGPU() const { return isOnGPU_; }
+  long Size() const;  // product of Shape
+
+  // Result tensors of GPU operations: Data sized but left zero, a device buffer
+  // allocated without an upload, marked device-resident.
+  static Result<TensorPtr> NewDeviceResult(std::vector<int> shape);
+
+ private:
+  void *gpuPtr_ = nullptr;
+  void *devicePtr_ = nullptr;
+  bool isOnGPU_ = false;
+  bool isOwner_ = true;
+  long gpuBytes_ = 0;
+  void dropDeviceCopy();
+};
+
+// NewTensor (tensor.go:90-109): len(data) must equal the product of shape.
+Result<TensorPtr> NewTensor(std::vector<int> shape, std::vector<float> data);
+
+// tensor.SparseFormat (sparse-tensor.go:18-24).
+enum class SparseFormat { COO = 0, CSR = 1, CSC = 2 };
+std::string String(SparseFormat f);  // sparse-tensor.go:423-434
+
+// tensor.SparseTensor (sparse-tensor.go:27-51): 2-D, int32 indices, fp32 values;
+// explicit zeros and duplicate coordinates are kept.
+class SparseTensor {
+ public:
+  std::vector<int> Shape;
+  SparseFormat Format = SparseFormat::COO;
+  int NNZ = 0;
+  std::vector<int32_t> RowIndices, ColIndices;  // COO
+  std::vector<float> Values;
+  std::vector<int32_t> RowPtr, ColPtr, Indices;  // CSR (RowPtr) / CSC (ColPtr)
+  std::vector<float> Data;
+  bool IsOwner = true;
+
+  SparseTensor() = default;
+  SparseTensor(const SparseTensor &) = delete;
+  SparseTensor &operator=(const SparseTensor &) = delete;
+  ~SparseTensor();
+
+  Error ConvertToCSR();                  // sparse-tensor.go:127-181
+  Error ConvertToCSC();                  // sparse-tensor.go:184-238
+  Result<TensorPtr> ToDense() const;     // sparse-tensor.go:241-272
+  Error EnsureGPU();                     // sparse-tensor.go:275-337 (uploads Data only)
+  Error RetrieveCPU();                   // sparse-tensor.go:340-384
+  void ReleaseGPU();                     // sparse-tensor.go:387-395
+  void *GPUPtr() const { return gpuPtr_; }
+  void *DevicePtr() const { return devicePtr_; }
+  bool IsOnGPU() const { return isOnGPU_; }
+  double GetDensity() const { return density_; }  // :408
+  int GetNNZ() const { return NNZ; }              // :413
+  SparseFormat GetFormat() const { return Format; }
+  Error IsCompatibleWith(const SparseTensor &other) const;  // :437-449
+  Result<SparseTensorPtr> Clone() const;                   // :452-489
+
+  double density_ = 0.0;
+
+ private:
+  void *gpuPtr_ = nullptr;
+  void *devicePtr_ = nullptr;
+  bool isOnGPU_ = false;
+};
+
+// NewSparseTensorCOO (sparse-tensor.go:54-99) and NewSparseTensorFromDense (:102-124,
+// keeps |v| > threshold).
+Result<SparseTensorPtr> NewSparseTensorCOO(std::vector<int> shape, const std::vector<int32_t> &rowIndices,
+                                           const std::vector<int32_t> &colIndices, const std::vector<float> &values);
+Result<SparseTensorPtr> NewSparseTensorFromDense(const Tensor &dense, float threshold);
+
+}  // namespace tensor
+
+namespace mat {
+
+// gonum's mat.Matrix interface (the subset the reference's wrappers implement).
+class Matrix {
+ public:
+  virtual ~Matrix() = default;
+  virtual void Dims(int &r, int &c) const = 0;
+  virtual double At(int i, int j) const = 0;
+  virtual std::shared_ptr<Matrix> T() const = 0;
+};
+using MatrixPtr = std::shared_ptr<Matrix>;
+
+// gonum's mat.Dense: row-major float64; NewDense panics if len(data) != r*c.
+class Dense : public Matrix, public std::enable_shared_from_this<Dense> {
+ public:
+  Dense(int r, int c, std::vector<double> data);
+  void Dims(int &r, int &c) const override { r = rows_; c = cols_; }
+  double At(int i, int j) const override;
+  std::shared_ptr<Matrix> T() const override;  // a transposed view, as gonum's mat.Transpose
+  void Set(int i, int j, double v);
+  const std::vector<double> &RawData() const { return data_; }
+
+ private:
+  int rows_, cols_;
+  std::vector<double> data_;
+};
+std::shared_ptr<Dense> NewDense(int r, int c, std::vector<double> data);
+
+}  // namespace mat
+
+namespace matrix {
+
+using tensor::Tensor;
+using tensor::TensorPtr;
+using tensor::SparseTensor;
+using tensor::SparseTensorPtr;
+
+// ActivationType (gpu/matrix/activation.go:18-29).
+enum ActivationType { ReLU = 0, Sigmoid = 1, Tanh = 2, Softmax = 3, LeakyReLU = 4, ELU = 5, Swish = 6, GELU = 7 };
+
+// Dense ops (gpu/matrix/matrix.go:53-105, :357-404).
+Result<TensorPtr> MatMul(Tensor &A, Tensor &B);
+Result<TensorPtr> Transpose(Tensor &A);
+
+// Custom-kernel GEMMs (gpu/matrix/optimized-kernels.go:21-75, :78-135).
+Result<TensorPtr> OptimizedGEMM(Tensor &A, Tensor &B, float alpha, float beta);
+Result<TensorPtr> OptimizedBatchMatMul(Tensor &A, Tensor &B);
+
+// Sparse ops (gpu/matrix/sparse-matrix.go:20-66, :366-399, :527-583). SparseMatMul
+// dispatches on operand kinds like the Go type switch: sparse x dense runs the CSR
+// SpMM kernel, dense x dense is MatMul; sparse x sparse and dense x sparse are not
+// provided by this backend and return an error.
+Result<TensorPtr> SparseMatMul(SparseTensor &A, Tensor &B);
+Result<TensorPtr> SparseMatMul(Tensor &A, Tensor &B);
+Result<TensorPtr> SparseMatMul(SparseTensor &A, SparseTensor &B);
+Result<TensorPtr> SparseMatMul(Tensor &A, SparseTensor &B);
+Result<TensorPtr> SparseMatVec(SparseTensor &A, Tensor &x);
+Result<SparseTensorPtr> SparseTranspose(const SparseTensor &A);
+
+// Fused linear + activation (gpu/matrix/fused-operations.go:24-54, :380-465).
+struct FusedActivationConfig {
+  gometal::matrix::ActivationType ActivationType = ReLU;
+  float Alpha = 0.0f;
+  bool InPlace = false;
+};
+struct FusedLinearConfig {
+  bool Bias = false;
+  std::shared_ptr<FusedActivationConfig> Activation;  // nil -> ReLU
+  float Dropout = 0.0f;
+};
+class FusedLinearActivation {
+ public:
+  std::string GetName() const { return "linear_activation"; }
+  // inputs = {input [batch,in], weight [in,out], optional bias [out]}.
+  Result<TensorPtr> Forward(const std::vector<Tensor *> &inputs, const FusedLinearConfig *config);
+};
+
+// Mixed precision (gpu/matrix/mixed-precision.go).
+using FloatMP16 = uint16_t;
+FloatMP16 Float32ToFloatMP16(float f);   // :106-151 (truncation, reference bit semantics)
+float FloatMP16ToFloat32(FloatMP16 h);   // :154-189
+struct MixedPrecisionConfig {
+  bool Enabled = true;
+  float LossScale = 65536.0f;
+  float LossScaleGrowthRate = 2.0f;
+  float LossScaleBackoffRate = 0.5f;
+  int GrowthInterval = 2000;
+  float MaxLossScale = 1048576.0f;
+  float MinLossScale = 1.0f;
+  bool SkipOverflowSteps = true;
+};
+std::shared_ptr<MixedPrecisionConfig> DefaultMixedPrecisionConfig();  // :38-49
+class MixedPrecisionTrainer {
+ public:
+  explicit MixedPrecisionTrainer(std::shared_ptr<MixedPrecisionConfig> cfg);
+  // :192-210: fp32 values rounded through FloatMP16 (stored as fp32).
+  Result<TensorPtr> ConvertTensorToFloat16(const Tensor &input) const;
+  // :315-358: input x weights on fp16-rounded operands, plus the fp16-rounded bias
+  // broadcast over rows (bias length must equal the output width). Runs the cast and
+  // an fp16 MFMA GEMM (exact fp16 products, fp32 accumulation) on the device.
+  Result<TensorPtr> ForwardFloat16(Tensor &input, Tensor &weights, Tensor *bias);
+  float GetCurrentLossScale() const { return currentLossScale_; }
+
+ private:
+  std::shared_ptr<MixedPrecisionConfig> config_;
+  float currentLossScale_;
+};
+Result<std::shared_ptr<MixedPrecisionTrainer>> NewMixedPrecisionTrainer(std::shared_ptr<MixedPrecisionConfig> cfg);
+
+// LinearLayer (gpu/matrix/layers.go:11-74): Y = X W + b with W [in, out].
+class LinearLayer {
+ public:
+  TensorPtr Weight, Bias;
+  int InputSize = 0, OutputSize = 0;
+  bool UseBias = false;
+  // Returns a zero output on failure, as the reference does (layers.go:61-67).
+  TensorPtr Forward(TensorPtr input);
+
+ private:
+  TensorPtr input_;
+};
+std::shared_ptr<LinearLayer> NewLinearLayer(int inputSize, int outputSize, bool useBias, uint64_t seed = 1);
+
+// gonum-compatible dense wrapper (gpu/matrix/gonum-compat.go:9-110, :321-367, :744-827).
+class GPUDense : public mat::Matrix {
+ public:
+  explicit GPUDense(TensorPtr t) : tensor_(std::move(t)) {}
+  void Dims(int &r, int &c) const override;
+  double At(int i, int j) const override;         // panics on out-of-range indices
+  std::shared_ptr<mat::Matrix> T() const override;  // materialised GPU transpose
+  void Set(int i, int j, double v);
+  void Mul(const mat::Matrix &a, const mat::Matrix &b);  // receiver := a*b (device-resident)
+  std::shared_ptr<mat::Dense> ToGonum() const;
+  void ReleaseGPU();
+  TensorPtr GetTensor() const { return tensor_; }
+
+ private:
+  TensorPtr tensor_;
+};
+std::shared_ptr<GPUDense> NewGPUDense(int rows, int cols, const std::vector<double> &data);
+std::shared_ptr<GPUDense> FromGonum(const mat::Matrix &m);
+std::shared_ptr<GPUDense> NewGPUDenseFromTensor(TensorPtr t);
+std::shared_ptr<mat::Dense> GPUMatMul(const mat::Matrix &a, const mat::Matrix &b);
+struct MatMulOp {
+  std::shared_ptr<mat::Matrix> A, B;
+};
+std::vector<std::shared_ptr<mat::Dense>> BatchGPUMatMul(const std::vector<MatMulOp> &operations);
+
+// gonum-compatible sparse wrapper (gpu/matrix/sparse-gonum-compat.go:12-382).
+class GPUSparse : public mat::Matrix {
+ public:
+  explicit GPUSparse(SparseTensorPtr s) : sparse_(std::move(s)) {}
+  void Dims(int &r, int &c) const override;
+  double At(int i, int j) const override;  // first stored entry at (i, j), else 0
+  std::shared_ptr<mat::Matrix> T() const override;
+  int GetNNZ() const { return sparse_->GetNNZ(); }
+  double GetDensity() const { return sparse_->GetDensity(); }
+  tensor::SparseFormat GetFormat() const { return sparse_->GetFormat(); }
+  Error ConvertToCSR() { return sparse_->ConvertToCSR(); }
+  Error ConvertToCSC() { return sparse_->ConvertToCSC(); }
+  // (*GPUSparse).SparseMul(a, b) (sparse-gonum-compat.go:147-166): SparseMatMul(a, b)
+  // returned as a mat::Dense; the receiver itself is not an operand.
+  std::shared_ptr<mat::Dense> SparseMul(SparseTensor &a, Tensor &b);
+  std::shared_ptr<mat::Dense> SparseMul(Tensor &a, Tensor &b);
+  std::vector<double> SparseMatVec(const std::vector<double> &x);
+  void ReleaseGPU() { sparse_->ReleaseGPU(); }
+  SparseTensorPtr GetSparseTensor() const { return sparse_; }
+
+ private:
+  SparseTensorPtr sparse_;
+};
+std::shared_ptr<GPUSparse> NewGPUSparse(int rows, int cols, const std::vector<int32_t> &rowIndices,
+                                        const std::vector<int32_t> &colIndices, const std::vector<float> &values);
+std::shared_ptr<GPUSparse> NewGPUSparseFromDense(const mat::Matrix &m, double threshold);
+std::shared_ptr<GPUSparse> FromGonumSparse(int rows, int cols, const std::vector<double> &data, double threshold);
+// GPUSparseMatMul (sparse-gonum-compat.go:253-337): a *GPUSparse operand stays sparse,
+// any other mat::Matrix is densified.
+std::shared_ptr<mat::Dense> GPUSparseMatMul(const mat::Matrix &a, const mat::Matrix &b);
+struct SparseMatMulOp {
+  std::shared_ptr<mat::Matrix> A, B;
+};
+std::vector<std::shared_ptr<mat::Dense>> BatchGPUSparseMatMul(const std::vector<SparseMatMulOp> &operations);
+std::vector<std::vector<double>> BatchGPUSparseMatVec(const std::vector<std::shared_ptr<GPUSparse>> &matrices,
+                                                      const std::vector<std::vector<double>> &vectors);
+
+}  // namespace matrix
+}  // namespace gometal

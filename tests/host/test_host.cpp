@@ -1,0 +1,536 @@
+// Tests of the C++ host API (go-nngpu_amd/host/gometal.hpp), written in the shape of
+// the reference's Go tests: one function per behaviour, checked against the CPU
+// checker in oracle/ (linked as test infrastructure) or against closed forms.
+//
+//   test_host --cpu   host-only behaviour (no device calls)
+//   test_host --gpu   everything, including the device paths through the C ABI
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "../../go-nngpu_amd/host/gometal.hpp"
+#include "../../include/gonngpu.h"
+#include "../../oracle/oracle.h"
+
+using namespace gometal;
+using gometal::tensor::NewSparseTensorCOO;
+using gometal::tensor::NewTensor;
+using gometal::tensor::SparseFormat;
+
+namespace {
+
+int g_failures = 0;
+std::string g_current;
+
+void fail(const char *file, int line, const std::string &what) {
+  ++g_failures;
+  std::printf("  FAIL %s (%s:%d): %s\n", g_current.c_str(), file, line, what.c_str());
+  std::fflush(stdout);
+}
+#define CHECK(cond)                                    \
+  do {                                                 \
+    if (!(cond)) fail(__FILE__, __LINE__, #cond);      \
+  } while (0)
+#define CHECK_NOERR(err)                                                        \
+  do {                                                                          \
+    const gometal::Error &e_ = (err);                                           \
+    if (e_) fail(__FILE__, __LINE__, std::string("unexpected error: ") + e_.message); \
+  } while (0)
+#define CHECK_ERR_HAS(err, sub)                                                                     \
+  do {                                                                                              \
+    const gometal::Error &e_ = (err);                                                               \
+    if (!e_) fail(__FILE__, __LINE__, std::string("expected error containing: ") + (sub));          \
+    else if (e_.message.find(sub) == std::string::npos)                                             \
+      fail(__FILE__, __LINE__, std::string("error '") + e_.message + "' lacks '" + (sub) + "'");    \
+  } while (0)
+#define CHECK_PANICS(stmt)                              \
+  do {                                                  \
+    bool p_ = false;                                    \
+    try {                                               \
+      stmt;                                             \
+    } catch (const gometal::Panic &) {                  \
+      p_ = true;                                        \
+    }                                                   \
+    if (!p_) fail(__FILE__, __LINE__, "expected a panic: " #stmt); \
+  } while (0)
+
+std::vector<float> uniform(size_t n, uint64_t stream, float lo = -1.0f, float hi = 1.0f) {
+  std::vector<float> v(n);
+  orc_fill_uniform_f32(v.data(), n, 42, stream, lo, hi);
+  return v;
+}
+
+// relFrob of fp32 data against a float64 reference.
+double rel(const std::vector<float> &x, const std::vector<double> &r) { return orc_rel_frob(x.data(), r.data(), x.size()); }
+
+std::vector<double> gemm64(const std::vector<float> &A, const std::vector<float> &B, long M, long N, long K) {
+  std::vector<double> C((size_t)(M * N));
+  orc_gemm_f64(0, 0, M, N, K, 1.0, A.data(), K, B.data(), N, 0.0, C.data(), N, 8);
+  return C;
+}
+
+// ============================================================== host-only tests
+void TestNewTensorValidates() {
+  auto [t, err] = NewTensor({2, 3}, std::vector<float>(6, 1.0f));
+  CHECK_NOERR(err);
+  CHECK(t && t->Size() == 6 && !t->IsOnGPU());
+  auto [bad, err2] = NewTensor({2, 3}, std::vector<float>(5));
+  CHECK(!bad);
+  CHECK_ERR_HAS(err2, "does not match shape dimensions");
+}
+
+void TestSparseCOOValidation() {
+  CHECK_ERR_HAS(NewSparseTensorCOO({4, 4}, {0, 1}, {0}, {1.f, 2.f}).err, "length mismatch");
+  CHECK_ERR_HAS(NewSparseTensorCOO({4, 4, 4}, {0}, {0}, {1.f}).err, "only 2D");
+  CHECK_ERR_HAS(NewSparseTensorCOO({4, 4}, {4}, {0}, {1.f}).err, "row index 4 out of bounds");
+  CHECK_ERR_HAS(NewSparseTensorCOO({4, 4}, {0}, {-1}, {1.f}).err, "column index -1 out of bounds");
+  auto [s, err] = NewSparseTensorCOO({4, 5}, {0, 3}, {1, 4}, {1.f, 0.f});  // explicit zero is kept
+  CHECK_NOERR(err);
+  CHECK(s->GetNNZ() == 2 && s->GetFormat() == SparseFormat::COO);
+  CHECK(std::fabs(s->GetDensity() - 2.0 / 20.0) < 1e-12);
+  CHECK(tensor::String(SparseFormat::CSR) == "CSR" && tensor::String(SparseFormat::CSC) == "CSC");
+}
+
+void TestConvertToCSRMatchesOracle() {
+  // COO with duplicates, explicit zeros, empty rows and arbitrary order.
+  const int rows = 50, cols = 40;
+  std::vector<int32_t> ri, ci;
+  std::vector<float> v;
+  uint64_t x = 7;
+  for (int k = 0; k < 400; ++k) {
+    x = x * 6364136223846793005ULL + 1442695040888963407ULL;
+    int r = (int)((x >> 33) % rows);
+    if (r % 7 == 3) continue;  // empty rows
+    ri.push_back(r);
+    ci.push_back((int)((x >> 13) % cols));
+    v.push_back((k % 11 == 0) ? 0.0f : (float)((int)((x >> 40) % 200) - 100) / 8.0f);
+  }
+  ri.push_back(5); ci.push_back(6); v.push_back(1.5f);  // duplicate coordinates
+  ri.push_back(5); ci.push_back(6); v.push_back(-0.25f);
+  auto [s, err] = NewSparseTensorCOO({rows, cols}, ri, ci, v);
+  CHECK_NOERR(err);
+  CHECK_NOERR(s->ConvertToCSR());
+  std::vector<int32_t> rp(rows + 1), idx(v.size());
+  std::vector<float> data(v.size());
+  CHECK(orc_coo_to_csr(rows, cols, (long)v.size(), ri.data(), ci.data(), v.data(), rp.data(), idx.data(),
+                       data.data()) == 0);
+  CHECK(s->Format == SparseFormat::CSR && s->RowPtr == rp && s->Indices == idx && s->Data == data);
+  CHECK_NOERR(s->ConvertToCSR());                          // no-op
+  CHECK_ERR_HAS(s->ConvertToCSC(), "can only convert from COO to CSC");
+  // ToDense: last duplicate wins (sparse-tensor.go:251-258)
+  auto [d, derr] = s->ToDense();
+  CHECK_NOERR(derr);
+  std::vector<float> ref((size_t)rows * cols);
+  orc_csr_to_dense(rows, cols, rp.data(), idx.data(), data.data(), ref.data());
+  CHECK(d->Data == ref);
+  // CSC of the same COO densifies to the same matrix
+  auto [s2, e2] = NewSparseTensorCOO({rows, cols}, ri, ci, v);
+  CHECK_NOERR(e2);
+  CHECK_NOERR(s2->ConvertToCSC());
+  CHECK(s2->ColPtr.size() == (size_t)cols + 1 && s2->ColPtr.back() == (int)v.size());
+  for (int c = 0; c < cols; ++c)
+    for (int k = s2->ColPtr[c] + 1; k < s2->ColPtr[c + 1]; ++k) CHECK(s2->Indices[k - 1] <= s2->Indices[k]);
+  CHECK(s2->ToDense().value->Data == ref);
+  // Clone copies the compressed arrays
+  auto [c, cerr] = s->Clone();
+  CHECK_NOERR(cerr);
+  CHECK(c->RowPtr == s->RowPtr && c->Data == s->Data && c->Format == SparseFormat::CSR);
+  CHECK_NOERR(s->IsCompatibleWith(*c));
+  CHECK_ERR_HAS(s->IsCompatibleWith(*NewSparseTensorCOO({rows, cols + 1}, {}, {}, {}).value), "shape mismatch");
+}
+
+void TestSparseTranspose() {
+  auto [s, err] = NewSparseTensorCOO({3, 5}, {0, 2, 2}, {4, 0, 1}, {1.f, 2.f, 3.f});
+  CHECK_NOERR(err);
+  auto [t, terr] = matrix::SparseTranspose(*s);
+  CHECK_NOERR(terr);
+  CHECK(t->Shape == std::vector<int>({5, 3}) && t->RowIndices == s->ColIndices);
+  CHECK_NOERR(s->ConvertToCSR());
+  auto [tc, tcerr] = matrix::SparseTranspose(*s);
+  CHECK_NOERR(tcerr);
+  CHECK(tc->Format == SparseFormat::CSC && tc->ColPtr == s->RowPtr);
+  matrix::GPUSparse gs(tc);
+  for (int i = 0; i < 5; ++i)
+    for (int j = 0; j < 3; ++j) CHECK(gs.At(i, j) == matrix::GPUSparse(s).At(j, i));
+}
+
+void TestFloatMP16MatchesReferenceBits() {
+  // Float32ToFloatMP16 against the oracle's restatement over a spread of values.
+  uint64_t x = 1;
+  for (int k = 0; k < 200000; ++k) {
+    x = x * 6364136223846793005ULL + 1442695040888963407ULL;
+    uint32_t bits = (uint32_t)(x >> 32);
+    float f;
+    std::memcpy(&f, &bits, 4);
+    CHECK(matrix::Float32ToFloatMP16(f) == orc_f32_to_f16_rtz(f));
+    if (g_failures) return;
+  }
+  for (uint32_t h = 0; h < 65536; ++h) {
+    const float a = matrix::FloatMP16ToFloat32((uint16_t)h), b = orc_f16_to_f32((uint16_t)h);
+    CHECK(std::memcmp(&a, &b, 4) == 0 || (std::isnan(a) && std::isnan(b)));
+  }
+  CHECK(matrix::Float32ToFloatMP16(1.0f) == 0x3C00 && matrix::Float32ToFloatMP16(65520.0f) == 0x7BFF);
+}
+
+void TestMixedPrecisionConfigDefaults() {
+  auto c = matrix::DefaultMixedPrecisionConfig();
+  CHECK(c->Enabled && c->LossScale == 65536.0f && c->MaxLossScale == 1048576.0f && c->GrowthInterval == 2000);
+  auto [mp, err] = matrix::NewMixedPrecisionTrainer(nullptr);
+  CHECK_NOERR(err);
+  CHECK(mp->GetCurrentLossScale() == 65536.0f);
+  auto [t, e2] = NewTensor({4}, {1.0f, 1.0009765625f, 1.00048828125f, 0.1f});
+  CHECK_NOERR(e2);
+  auto [h, e3] = mp->ConvertTensorToFloat16(*t);
+  CHECK_NOERR(e3);
+  CHECK(h->Data[0] == 1.0f && h->Data[1] == 1.0009765625f && h->Data[2] == 1.0f);  // truncation
+  CHECK(h->Data[3] == orc_f16_to_f32(orc_f32_to_f16_rtz(0.1f)));
+}
+
+void TestGonumDense() {
+  auto d = mat::NewDense(2, 3, {1, 2, 3, 4, 5, 6});
+  int r, c;
+  d->Dims(r, c);
+  CHECK(r == 2 && c == 3 && d->At(1, 2) == 6);
+  auto t = d->T();
+  t->Dims(r, c);
+  CHECK(r == 3 && c == 2 && t->At(2, 1) == 6 && t->At(0, 1) == 4);
+  CHECK_PANICS(d->At(2, 0));
+  CHECK_PANICS(mat::NewDense(2, 2, {1, 2, 3}));
+}
+
+void TestGPUSparseAtAndErrors() {
+  auto gs = matrix::NewGPUSparse(3, 3, {0, 1, 1}, {0, 2, 2}, {5.f, 7.f, 9.f});
+  CHECK(gs->At(0, 0) == 5 && gs->At(1, 2) == 7 && gs->At(2, 2) == 0);  // first duplicate wins
+  CHECK_PANICS(gs->At(3, 0));
+  CHECK_PANICS(matrix::NewGPUSparse(3, 3, {0}, {3}, {1.f}));
+  CHECK_NOERR(gs->ConvertToCSR());
+  CHECK(gs->At(1, 2) == 7 && gs->GetNNZ() == 3);
+  auto dense = mat::NewDense(2, 2, {0.5, -0.05, 0, 2});
+  auto fs = matrix::NewGPUSparseFromDense(*dense, 0.1);  // strict |v| > threshold
+  CHECK(fs->GetNNZ() == 2 && fs->At(0, 1) == 0);
+  CHECK_PANICS(matrix::BatchGPUSparseMatVec({fs}, {}));
+}
+
+void TestShapeErrorsBeforeDevice() {
+  auto a = NewTensor({2, 3}, std::vector<float>(6)).value;
+  auto b = NewTensor({2, 3}, std::vector<float>(6)).value;
+  auto v = NewTensor({6}, std::vector<float>(6)).value;
+  CHECK_ERR_HAS(matrix::MatMul(*a, *b).err, "A columns (3) != B rows (2)");
+  CHECK_ERR_HAS(matrix::MatMul(*a, *v).err, "requires 2D tensors");
+  CHECK_ERR_HAS(matrix::Transpose(*v).err, "requires 2D tensor");
+  CHECK_ERR_HAS(matrix::OptimizedGEMM(*a, *b, 1, 0).err, "don't match");
+  CHECK_ERR_HAS(matrix::OptimizedBatchMatMul(*a, *b).err, "requires 3D tensors");
+  auto s = NewSparseTensorCOO({3, 4}, {0}, {0}, {1.f}).value;
+  CHECK_ERR_HAS(matrix::SparseMatMul(*s, *a).err, "A columns (4) != B rows (2)");
+  CHECK_ERR_HAS(matrix::SparseMatVec(*s, *v).err, "matrix cols (4) != vector size (6)");
+  CHECK_ERR_HAS(matrix::SparseMatMul(*s, *s).err, "incompatible matrix dimensions");
+  auto sq = NewSparseTensorCOO({3, 3}, {0}, {0}, {1.f}).value;
+  CHECK_ERR_HAS(matrix::SparseMatMul(*sq, *sq).err, "sparse-sparse");
+  matrix::FusedLinearActivation f;
+  CHECK_ERR_HAS(f.Forward({a.get(), b.get()}, nullptr).err, "invalid config");
+  matrix::FusedLinearConfig cfg;
+  CHECK_ERR_HAS(f.Forward({a.get()}, &cfg).err, "requires at least input and weight");
+}
+
+// ============================================================== device tests
+void TestMatMul() {
+  const int M = 96, K = 130, N = 70;
+  auto A = NewTensor({M, K}, uniform((size_t)M * K, 1)).value;
+  auto B = NewTensor({K, N}, uniform((size_t)K * N, 2)).value;
+  auto [C, err] = matrix::MatMul(*A, *B);
+  CHECK_NOERR(err);
+  CHECK(C->IsOnGPU());
+  CHECK_NOERR(C->RetrieveCPU());
+  CHECK(!C->IsOnGPU());
+  CHECK(rel(C->Data, gemm64(A->Data, B->Data, M, N, K)) <= 1e-5);
+  // 256^3 (config C1)
+  auto A2 = NewTensor({256, 256}, uniform(65536, 3)).value;
+  auto B2 = NewTensor({256, 256}, uniform(65536, 4)).value;
+  auto C2 = matrix::MatMul(*A2, *B2).value;
+  CHECK_NOERR(C2->RetrieveCPU());
+  CHECK(rel(C2->Data, gemm64(A2->Data, B2->Data, 256, 256, 256)) <= 1e-5);
+}
+
+void TestResidencyReuploadsHostWrites() {
+  auto A = NewTensor({2, 2}, {1, 2, 3, 4}).value;
+  auto I = NewTensor({2, 2}, {1, 0, 0, 1}).value;
+  auto C = matrix::MatMul(*A, *I).value;
+  CHECK_NOERR(C->RetrieveCPU());
+  CHECK(C->Data == std::vector<float>({1, 2, 3, 4}));
+  CHECK_NOERR(A->RetrieveCPU());     // host-resident again
+  A->Data[0] = 10.0f;                // host write
+  auto C2 = matrix::MatMul(*A, *I).value;  // EnsureGPU re-uploads
+  CHECK_NOERR(C2->RetrieveCPU());
+  CHECK(C2->Data[0] == 10.0f);
+}
+
+void TestMemoryStatsTrackTensors() {
+  auto before = tensor::GetGlobalMemoryStats();
+  {
+    auto t = NewTensor({1024}, std::vector<float>(1024, 1.0f)).value;
+    CHECK_NOERR(t->EnsureGPU());
+    auto mid = tensor::GetGlobalMemoryStats();
+    CHECK(mid.numAllocations == before.numAllocations + 1 && mid.currentUsage == before.currentUsage + 4096);
+    CHECK(mid.peakUsage >= mid.currentUsage);
+  }
+  auto after = tensor::GetGlobalMemoryStats();
+  CHECK(after.numAllocations == before.numAllocations && after.currentUsage == before.currentUsage);
+}
+
+void TestTranspose() {
+  auto A = NewTensor({3, 70}, uniform(210, 5)).value;
+  auto [T, err] = matrix::Transpose(*A);
+  CHECK_NOERR(err);
+  CHECK(T->Shape == std::vector<int>({70, 3}));
+  CHECK_NOERR(T->RetrieveCPU());
+  std::vector<float> ref(210);
+  orc_transpose_f32(3, 70, A->Data.data(), ref.data());
+  CHECK(T->Data == ref);
+}
+
+void TestOptimizedGEMMAndBatch() {
+  const int M = 33, K = 17, N = 20, bs = 3;
+  auto A = NewTensor({M, K}, uniform((size_t)M * K, 6)).value;
+  auto B = NewTensor({K, N}, uniform((size_t)K * N, 7)).value;
+  auto [C, err] = matrix::OptimizedGEMM(*A, *B, 2.0f, 0.5f);  // beta scales a fresh zero output
+  CHECK_NOERR(err);
+  CHECK_NOERR(C->RetrieveCPU());
+  auto ref = gemm64(A->Data, B->Data, M, N, K);
+  for (double &r : ref) r *= 2.0;
+  CHECK(rel(C->Data, ref) <= 1e-5);
+  auto A3 = NewTensor({bs, M, K}, uniform((size_t)bs * M * K, 8)).value;
+  auto B3 = NewTensor({bs, K, N}, uniform((size_t)bs * K * N, 9)).value;
+  auto [C3, e3] = matrix::OptimizedBatchMatMul(*A3, *B3);
+  CHECK_NOERR(e3);
+  CHECK_NOERR(C3->RetrieveCPU());
+  for (int z = 0; z < bs; ++z) {
+    std::vector<float> a(A3->Data.begin() + (long)z * M * K, A3->Data.begin() + (long)(z + 1) * M * K);
+    std::vector<float> b(B3->Data.begin() + (long)z * K * N, B3->Data.begin() + (long)(z + 1) * K * N);
+    std::vector<float> c(C3->Data.begin() + (long)z * M * N, C3->Data.begin() + (long)(z + 1) * M * N);
+    CHECK(rel(c, gemm64(a, b, M, N, K)) <= 1e-5);
+  }
+}
+
+void TestSparseMatMulAndMatVec() {
+  const int rows = 300, cols = 200, N = 64;
+  std::vector<int32_t> ri, ci;
+  std::vector<float> v;
+  uint64_t x = 99;
+  for (int k = 0; k < 2500; ++k) {
+    x = x * 6364136223846793005ULL + 1442695040888963407ULL;
+    ri.push_back((int)((x >> 33) % rows));
+    ci.push_back((int)((x >> 11) % cols));
+    v.push_back((float)((int)((x >> 45) % 1000) - 500) / 256.0f);
+  }
+  auto S = NewSparseTensorCOO({rows, cols}, ri, ci, v).value;
+  auto D = NewTensor({cols, N}, uniform((size_t)cols * N, 10)).value;
+  auto [C, err] = matrix::SparseMatMul(*S, *D);  // COO converted to CSR on the way
+  CHECK_NOERR(err);
+  CHECK(S->GetFormat() == SparseFormat::CSR);
+  CHECK_NOERR(C->RetrieveCPU());
+  std::vector<float> ref((size_t)rows * N);
+  orc_spmm_csr_f32(rows, N, S->RowPtr.data(), S->Indices.data(), S->Data.data(), D->Data.data(), N, ref.data(), N, 1);
+  CHECK(C->Data == ref);  // CSR-order fma accumulation, bit for bit
+  auto xv = NewTensor({cols}, uniform(cols, 11)).value;
+  auto [y, yerr] = matrix::SparseMatVec(*S, *xv);
+  CHECK_NOERR(yerr);
+  CHECK_NOERR(y->RetrieveCPU());
+  std::vector<double> y64(rows);
+  orc_spmv_csr_f64(rows, S->RowPtr.data(), S->Indices.data(), S->Data.data(), xv->Data.data(), y64.data());
+  CHECK(rel(y->Data, y64) <= 1e-5);
+  // dense x dense through SparseMatMul is MatMul
+  auto A = NewTensor({4, cols}, uniform((size_t)4 * cols, 12)).value;
+  auto [C2, e2] = matrix::SparseMatMul(*A, *D);
+  CHECK_NOERR(e2);
+  CHECK_NOERR(C2->RetrieveCPU());
+  CHECK(rel(C2->Data, gemm64(A->Data, D->Data, 4, N, cols)) <= 1e-5);
+  // nnz = 0 gives zeros (the reference panics on &A.Indices[0])
+  auto E = NewSparseTensorCOO({5, cols}, {}, {}, {}).value;
+  auto [Z, zerr] = matrix::SparseMatMul(*E, *D);
+  CHECK_NOERR(zerr);
+  CHECK_NOERR(Z->RetrieveCPU());
+  for (float z : Z->Data) CHECK(z == 0.0f);
+  // a CSC operand is rejected as in the reference (ConvertToCSR from CSC)
+  auto Cs = NewSparseTensorCOO({rows, cols}, ri, ci, v).value;
+  CHECK_NOERR(Cs->ConvertToCSC());
+  CHECK_ERR_HAS(matrix::SparseMatMul(*Cs, *D).err, "failed to convert A to CSR");
+}
+
+void TestFusedLinearActivation() {
+  const int batch = 40, in = 96, out = 70;
+  auto X = NewTensor({batch, in}, uniform((size_t)batch * in, 13)).value;
+  auto W = NewTensor({in, out}, uniform((size_t)in * out, 14)).value;
+  auto b = NewTensor({out}, uniform(out, 15)).value;
+  matrix::FusedLinearActivation f;
+  matrix::FusedLinearConfig cfg;
+  cfg.Bias = true;  // Activation nil -> ReLU
+  auto [Y, err] = f.Forward({X.get(), W.get(), b.get()}, &cfg);
+  CHECK_NOERR(err);
+  CHECK_NOERR(Y->RetrieveCPU());
+  std::vector<double> ref((size_t)batch * out);
+  orc_linear_f64(batch, in, out, X->Data.data(), W->Data.data(), 0, b->Data.data(), 0, 0.0, ref.data(), 8);
+  CHECK(rel(Y->Data, ref) <= 1e-5);
+  cfg.Activation = std::make_shared<matrix::FusedActivationConfig>();
+  cfg.Activation->ActivationType = matrix::GELU;
+  cfg.Bias = false;  // bias tensor passed but config.Bias false: ignored (fused-operations.go:394-397)
+  auto [Y2, e2] = f.Forward({X.get(), W.get(), b.get()}, &cfg);
+  CHECK_NOERR(e2);
+  CHECK_NOERR(Y2->RetrieveCPU());
+  orc_linear_f64(batch, in, out, X->Data.data(), W->Data.data(), 0, nullptr, 7, 0.0, ref.data(), 8);
+  CHECK(rel(Y2->Data, ref) <= 1e-5);
+  cfg.Activation->ActivationType = matrix::Softmax;  // not an element-wise epilogue
+  CHECK_ERR_HAS(f.Forward({X.get(), W.get()}, &cfg).err, "fused linear+activation failed (code -1)");
+}
+
+void TestForwardFloat16() {
+  const int M = 64, K = 200, N = 48;
+  auto X = NewTensor({M, K}, uniform((size_t)M * K, 16)).value;
+  auto W = NewTensor({K, N}, uniform((size_t)K * N, 17, -0.05f, 0.05f)).value;
+  auto b = NewTensor({N}, uniform(N, 18, -0.01f, 0.01f)).value;
+  auto [mp, merr] = matrix::NewMixedPrecisionTrainer(nullptr);
+  CHECK_NOERR(merr);
+  auto [Y, err] = mp->ForwardFloat16(*X, *W, b.get());
+  CHECK_NOERR(err);
+  CHECK_NOERR(Y->RetrieveCPU());
+  // reference: host RTZ rounding of X, W and b (mixed-precision.go:192-210), float64 GEMM
+  auto Xh = mp->ConvertTensorToFloat16(*X).value, Wh = mp->ConvertTensorToFloat16(*W).value;
+  auto bh = mp->ConvertTensorToFloat16(*b).value;
+  auto ref = gemm64(Xh->Data, Wh->Data, M, N, K);
+  for (int i = 0; i < M; ++i)
+    for (int j = 0; j < N; ++j) ref[(size_t)i * N + j] += bh->Data[j];
+  CHECK(rel(Y->Data, ref) <= 1e-5);
+  auto ref_unrounded = gemm64(X->Data, W->Data, M, N, K);  // unrounded inputs, same bias
+  for (int i = 0; i < M; ++i)
+    for (int j = 0; j < N; ++j) ref_unrounded[(size_t)i * N + j] += b->Data[j];
+  CHECK(rel(Y->Data, ref_unrounded) <= 2e-2);
+  auto wrong = NewTensor({N + 1}, std::vector<float>(N + 1)).value;
+  CHECK_ERR_HAS(mp->ForwardFloat16(*X, *W, wrong.get()).err, "bias length");
+}
+
+void TestLinearLayer() {
+  auto layer = matrix::NewLinearLayer(50, 30, true, 5);
+  for (int j = 0; j < 30; ++j) layer->Bias->Data[j] = 0.01f * (float)j;
+  auto X = NewTensor({8, 50}, uniform(400, 19)).value;
+  auto Y = layer->Forward(X);
+  CHECK(Y->Shape == std::vector<int>({8, 30}));
+  CHECK_NOERR(Y->RetrieveCPU());
+  auto ref = gemm64(X->Data, layer->Weight->Data, 8, 30, 50);
+  for (int i = 0; i < 8; ++i)
+    for (int j = 0; j < 30; ++j) ref[(size_t)i * 30 + j] += layer->Bias->Data[j];
+  CHECK(rel(Y->Data, ref) <= 1e-5);
+  auto bad = NewTensor({8, 49}, std::vector<float>(392)).value;
+  auto Z = layer->Forward(bad);  // zero output on failure (layers.go:61-67)
+  CHECK(Z->Shape == std::vector<int>({8, 30}));
+  for (float z : Z->Data) CHECK(z == 0.0f);
+}
+
+void TestGPUDenseAndGPUMatMul() {
+  const int M = 20, K = 30, N = 10;
+  std::vector<double> a((size_t)M * K), b((size_t)K * N);
+  for (size_t i = 0; i < a.size(); ++i) a[i] = std::sin(0.37 * (double)i);
+  for (size_t i = 0; i < b.size(); ++i) b[i] = std::cos(0.11 * (double)i);
+  auto da = mat::NewDense(M, K, a), db = mat::NewDense(K, N, b);
+  std::vector<float> af(a.begin(), a.end()), bf(b.begin(), b.end());
+  auto ref = gemm64(af, bf, M, N, K);
+  auto C = matrix::GPUMatMul(*da, *db);
+  std::vector<float> cf(C->RawData().begin(), C->RawData().end());
+  CHECK(rel(cf, ref) <= 1e-5);
+  // GPUDense.Mul: receiver becomes the device-resident product; At reads it back
+  auto g = matrix::NewGPUDense(M, N, std::vector<double>((size_t)M * N, 0.0));
+  auto ga = matrix::FromGonum(*da);
+  g->Mul(*ga, *db);
+  CHECK(g->GetTensor()->IsOnGPU());
+  CHECK(std::fabs(g->At(3, 4) - ref[3 * N + 4]) <= 1e-4 * (1.0 + std::fabs(ref[3 * N + 4])));
+  CHECK_PANICS(g->At(M, 0));
+  g->Set(0, 0, 42.0);
+  CHECK(g->At(0, 0) == 42.0);
+  // T() is a materialised GPU transpose
+  auto t = ga->T();
+  int r, c;
+  t->Dims(r, c);
+  CHECK(r == K && c == M && t->At(5, 7) == (double)(float)a[7 * K + 5]);
+  // Batch
+  auto res = matrix::BatchGPUMatMul({{da, db}, {db->T(), da->T()}});
+  CHECK(res.size() == 2);
+  res[1]->Dims(r, c);
+  CHECK(r == N && c == M && std::fabs(res[1]->At(2, 3) - ref[3 * N + 2]) <= 1e-4);
+  auto back = g->ToGonum();
+  CHECK(back->At(0, 0) == 42.0);
+}
+
+void TestGPUSparseMatMulAndMatVec() {
+  auto gs = matrix::NewGPUSparse(4, 3, {0, 1, 3, 3}, {2, 0, 1, 1}, {1.f, 2.f, 3.f, 4.f});  // (3,1) duplicated
+  auto d = mat::NewDense(3, 2, {1, 2, 3, 4, 5, 6});
+  auto C = matrix::GPUSparseMatMul(*gs, *d);
+  // rows: [0,0,1]x -> (5,6); [2,0,0] -> (2,4); 0; [0,7,0] -> (21,28)
+  const double ref[8] = {5, 6, 2, 4, 0, 0, 21, 28};
+  for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 2; ++j) CHECK(C->At(i, j) == ref[i * 2 + j]);
+  auto y = gs->SparseMatVec({1.0, 10.0, 100.0});
+  CHECK(y.size() == 4 && y[0] == 100 && y[1] == 2 && y[2] == 0 && y[3] == 70);
+  auto ys = matrix::BatchGPUSparseMatVec({gs, gs}, {{1, 0, 0}, {0, 1, 0}});
+  CHECK(ys[0][1] == 2 && ys[1][3] == 7);
+  // dense x dense through GPUSparseMatMul, and SparseMul on tensors
+  auto dd = matrix::GPUSparseMatMul(*mat::NewDense(1, 3, {1, 1, 1}), *d);
+  CHECK(dd->At(0, 0) == 9 && dd->At(0, 1) == 12);
+  auto S = gs->GetSparseTensor();
+  auto Dt = NewTensor({3, 2}, {1, 2, 3, 4, 5, 6}).value;
+  auto C2 = gs->SparseMul(*S, *Dt);
+  CHECK(C2->At(3, 1) == 28);
+  CHECK_PANICS(matrix::GPUSparseMatMul(*gs, *gs->T()));  // sparse x sparse not provided
+}
+
+struct Case {
+  const char *name;
+  std::function<void()> fn;
+  bool device;
+};
+
+}  // namespace
+
+int main(int argc, char **argv) {
+  const bool gpu = argc > 1 && std::strcmp(argv[1], "--gpu") == 0;
+  const std::vector<Case> cases = {
+      {"TestNewTensorValidates", TestNewTensorValidates, false},
+      {"TestSparseCOOValidation", TestSparseCOOValidation, false},
+      {"TestConvertToCSRMatchesOracle", TestConvertToCSRMatchesOracle, false},
+      {"TestSparseTranspose", TestSparseTranspose, false},
+      {"TestFloatMP16MatchesReferenceBits", TestFloatMP16MatchesReferenceBits, false},
+      {"TestMixedPrecisionConfigDefaults", TestMixedPrecisionConfigDefaults, false},
+      {"TestGonumDense", TestGonumDense, false},
+      {"TestGPUSparseAtAndErrors", TestGPUSparseAtAndErrors, false},
+      {"TestShapeErrorsBeforeDevice", TestShapeErrorsBeforeDevice, false},
+      {"TestMatMul", TestMatMul, true},
+      {"TestResidencyReuploadsHostWrites", TestResidencyReuploadsHostWrites, true},
+      {"TestMemoryStatsTrackTensors", TestMemoryStatsTrackTensors, true},
+      {"TestTranspose", TestTranspose, true},
+      {"TestOptimizedGEMMAndBatch", TestOptimizedGEMMAndBatch, true},
+      {"TestSparseMatMulAndMatVec", TestSparseMatMulAndMatVec, true},
+      {"TestFusedLinearActivation", TestFusedLinearActivation, true},
+      {"TestForwardFloat16", TestForwardFloat16, true},
+      {"TestLinearLayer", TestLinearLayer, true},
+      {"TestGPUDenseAndGPUMatMul", TestGPUDenseAndGPUMatMul, true},
+      {"TestGPUSparseMatMulAndMatVec", TestGPUSparseMatMulAndMatVec, true},
+  };
+  int run = 0;
+  for (const Case &c : cases) {
+    if (c.device && !gpu) continue;
+    g_current = c.name;
+    const int before = g_failures;
+    std::printf("=== RUN %s\n", c.name);
+    std::fflush(stdout);
+    try {
+      c.fn();
+    } catch (const std::exception &e) {
+      fail(__FILE__, __LINE__, std::string("uncaught exception: ") + e.what());
+    }
+    std::printf("--- %s %s\n", g_failures == before ? "PASS" : "FAIL", c.name);
+    std::fflush(stdout);
+    ++run;
+  }
+  std::printf("%s: %d tests, %d failures\n", g_failures ? "FAIL" : "ok", run, g_failures);
+  return g_failures ? 1 : 0;
+}
