@@ -23,6 +23,8 @@
 //  * a grouped, XCD-aware tile order: hardware dispatches workgroup w to XCD w % 8,
 //    so w is remapped to give each XCD a contiguous band of tiles that share A/B
 //    panels in that XCD's L2.
+#include <utility>
+
 #include "common.h"
 
 namespace gn {
@@ -48,6 +50,7 @@ struct GemmParams {
   float alpha, beta, act_alpha;
   int act;
   int tiles_m, tiles_n;
+  int group_m;  // tile rows per raster group (tile_coords); 0 selects the default of 4
 };
 
 // ------------------------------------------------------------------ epilogue
@@ -95,7 +98,7 @@ __device__ __forceinline__ void tile_coords(const GemmParams &p, int &tm, int &t
     const int per = total >> 3;
     w = (w & 7) * per + (w >> 3);
   }
-  const int GROUP_M = 4;
+  const int GROUP_M = p.group_m > 0 ? p.group_m : 4;
   const int in_group = GROUP_M * p.tiles_n;
   const int group = w / in_group;
   const int first_m = group * GROUP_M;
@@ -453,6 +456,66 @@ __device__ __forceinline__ unsigned lds_offset(const void *p) {
 // 32-byte block XOR of row k of an MN-contiguous tile.
 __device__ __forceinline__ int hsw(int k) { return (k & 3) | ((k >> 1) & 4); }
 
+// Epilogue for one wave's WTM x WTN accumulator tile, staged through a wave-private
+// LDS region so that C is written in row-major 16-byte vectors (a 16x16 MFMA block
+// alone only gives each store instruction 64-byte row pieces). EP rows at a time go
+// to LDS with a pitch of WTN + 4 floats (the 4 row groups of one ds_write_b32 then
+// fall on distinct banks), then each lane reads 4 consecutive columns back and
+// applies alpha, beta*C, bias and the activation before one 16-byte store. vec_ok:
+// ldc, N and C allow aligned 16-byte stores; otherwise elements are stored singly.
+// The pass index is a template parameter so every accumulator index is static (a
+// runtime index would move the whole accumulator array to scratch memory).
+template <int FM, int FN, int EP, int PASS>
+__device__ __forceinline__ void store_pass(const GemmParams &p, float *C, long row0, long col0,
+                                           const float4_t (&acc)[FM][FN], float *region, bool vec_ok) {
+  constexpr int WTN = FN * 16, LDSP = WTN + 4, CPR = WTN / 4;  // float4 per row
+  constexpr int FB = EP / 16;                                   // MFMA block rows per pass
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int ii = 0; ii < FB; ++ii)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) region[(16 * ii + 4 * g + r) * LDSP + 16 * j + c] = acc[PASS * FB + ii][j][r];
+#pragma unroll
+  for (int t = 0; t < EP * CPR / 64; ++t) {
+    const int idx = t * 64 + lane, rr = idx / CPR, c4 = idx % CPR;
+    const float4_t v = *reinterpret_cast<const float4_t *>(region + rr * LDSP + 4 * c4);
+    const long row = row0 + PASS * EP + rr, col = col0 + 4 * c4;
+    if (row < p.M) {
+      float *dst = C + row * p.ldc + col;
+      if (vec_ok && col + 3 < p.N) {
+        float4_t o;
+        const float4_t old =
+            p.beta != 0.0f ? *reinterpret_cast<const float4_t *>(dst) : float4_t{0.f, 0.f, 0.f, 0.f};
+        const float4_t b = p.bias ? *reinterpret_cast<const float4_t *>(p.bias + col) : float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = apply_act(p.act, p.alpha * v[e] + p.beta * old[e] + b[e], p.act_alpha);
+        __builtin_nontemporal_store(o, reinterpret_cast<float4_t *>(dst));  // C is not re-read: keep L2 for A/B
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (col + e < p.N) {
+            float x = p.alpha * v[e];
+            if (p.beta != 0.0f) x += p.beta * dst[e];
+            if (p.bias) x += p.bias[col + e];
+            dst[e] = apply_act(p.act, x, p.act_alpha);
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int FM, int FN, int EP, int... PASS>
+__device__ __forceinline__ void store_tile_coalesced(const GemmParams &p, float *C, long row0, long col0,
+                                                     const float4_t (&acc)[FM][FN], float *region, bool vec_ok,
+                                                     std::integer_sequence<int, PASS...>) {
+  static_assert(FM % (EP / 16) == 0 && (EP * FN * 4) % 64 == 0, "epilogue pass shape");
+  (store_pass<FM, FN, EP, PASS>(p, C, row0, col0, acc, region, vec_ok), ...);
+}
+
 template <int BM, int BN, int WM, int WN, int S, bool TA, bool TB>
 __global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm_f16_ring_kernel(GemmParams p) {
@@ -641,12 +704,15 @@ gemm_f16_ring_kernel(GemmParams p) {
     if (k + u + 1 < nk) tail(k + u + 1, 1);
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  __syncthreads();  // every wave is done with the ring; reuse it to stage C
 
+  constexpr int EP = (NW * 32 * (WTN + 4) * 4 <= S * STB) ? 32 : 16;  // rows per staging pass
+  static_assert(NW * EP * (WTN + 4) * 4 <= S * STB, "epilogue staging exceeds the ring");
   float *C = p.C + z * p.strideC;
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) store_block(p, C, m0 + wm * WTM + i * 16, n0 + wn * WTN + j * 16, acc[i][j]);
+  const bool vec_ok = (p.ldc % 4 == 0) && (((uintptr_t)C & 15) == 0);
+  float *region = reinterpret_cast<float *>(smem) + wave * EP * (WTN + 4);
+  store_tile_coalesced<FM, FN, EP>(p, C, m0 + wm * WTM, n0 + wn * WTN, acc, region, vec_ok,
+                                   std::make_integer_sequence<int, FM / (EP / 16)>{});
 }
 
 // ------------------------------------------------------------------ dispatch
