@@ -516,9 +516,29 @@ __device__ __forceinline__ void store_tile_coalesced(const GemmParams &p, float 
   (store_pass<FM, FN, EP, PASS>(p, C, row0, col0, acc, region, vec_ok), ...);
 }
 
+// Geometry of a ring-kernel instantiation (BK = 32 elements of K per stage).
 template <int BM, int BN, int WM, int WN, int S, bool TA, bool TB>
-__global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-gemm_f16_ring_kernel(GemmParams p) {
+struct RingCfg {
+  static constexpr int BK = 32;
+  static constexpr int NW = WM * WN;
+  static constexpr int WTM = BM / WM, WTN = BN / WN;
+  static constexpr int FM = WTM / 16, FN = WTN / 16;
+  static constexpr int OPA = BM * BK * 2;           // bytes of A per stage
+  static constexpr int OPB = BN * BK * 2;           // bytes of B per stage (at offset OPA)
+  static constexpr int STB = OPA + OPB;             // bytes per stage
+  static constexpr int IPA = BM / 16 / NW;          // 1 KiB DMA chunks per wave per tile, A
+  static constexpr int IPB = BN / 16 / NW;          //   ... and B
+  static constexpr int RBA = TA ? BM * 2 : BK * 2;  // LDS row bytes of the A / B tiles
+  static constexpr int RBB = TB ? BK * 2 : BN * 2;
+  static constexpr int LPW = IPA + IPB;             // DMA instructions per wave per tile
+};
+
+// Main loop of the ring kernel for one output tile (rows m0.., columns n0.., batch z)
+// over K-tiles [kt0, kt1): adds the products into acc. Leaves every DMA complete and
+// every wave past a barrier, so the caller may reuse smem.
+template <int BM, int BN, int WM, int WN, int S, bool TA, bool TB>
+__device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long n0, long z, int kt0, int kt1,
+                                              char *smem, float4_t (&acc)[BM / WM / 16][BN / WN / 16]) {
   constexpr int BK = 32;
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -534,42 +554,35 @@ gemm_f16_ring_kernel(GemmParams p) {
   static_assert(IPA >= 1 && IPB >= 1 && BM % (16 * NW) == 0 && BN % (16 * NW) == 0, "DMA split");
   static_assert(S >= 3 && (S - 2) * LPW < 64, "ring depth");
   static_assert((!TA || BM >= 128) && (TB || BN >= 128), "MN-contiguous rows need 8 XOR blocks of 32 B");
-  __shared__ __attribute__((aligned(1024))) char smem[S * STB];
-
-  int tm, tn;
-  tile_coords(p, tm, tn);
-  const long m0 = (long)tm * BM, n0 = (long)tn * BN;
-  const long z = blockIdx.z;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int wm = wave / WN, wn = wave % WN;
 
   // Per-lane DMA plan, fixed for the whole K loop. K-contiguous: chunk c = rows
   // 16c..16c+15 in fragment order. MN-contiguous: chunk c = k rows c*(1024/RB).. .
+  // Lanes whose row (or column block) lies past M (or N) get the out-of-range offset.
   BufRsrc ra, rb;
   unsigned voa[IPA], vob[IPB];
-  int kla[IPA], klb[IPB];   // k within the tile that the lane loads
-  bool rva[IPA], rvb[IPB];  // row (K-contiguous) or column block (MN-contiguous) in range
+  int kla[IPA], klb[IPB];  // k within the tile that the lane loads
   {
     const _Float16 *A = static_cast<const _Float16 *>(p.A) + z * p.strideA;
     const _Float16 *B = static_cast<const _Float16 *>(p.B) + z * p.strideB;
-    ra = make_rsrc(TA ? (const void *)(A + m0) : (const void *)(A + m0 * p.lda));
-    rb = make_rsrc(TB ? (const void *)(B + n0 * p.ldb) : (const void *)(B + n0));
+    const long k0 = (long)kt0 * BK;
+    ra = make_rsrc(TA ? (const void *)(A + k0 * p.lda + m0) : (const void *)(A + m0 * p.lda + k0));
+    rb = make_rsrc(TB ? (const void *)(B + n0 * p.ldb + k0) : (const void *)(B + k0 * p.ldb + n0));
 #pragma unroll
     for (int i = 0; i < IPA; ++i) {
       const int c = wave * IPA + i;
       if (!TA) {
         const int r = c * 16 + (lane & 15), q = lane >> 4;
         kla[i] = 8 * q;
-        rva[i] = m0 + r < p.M;
-        voa[i] = (unsigned)((long)r * p.lda * 2 + 16 * q);
+        voa[i] = m0 + r < p.M ? (unsigned)((long)r * p.lda * 2 + 16 * q) : kOutOfRange;
       } else {
         constexpr int GPR = RBA / 16;
         const int k = c * (1024 / RBA) + lane / GPR, qp = lane % GPR;
         const int q = 2 * ((qp >> 1) ^ hsw(k)) + (qp & 1);
         kla[i] = k;
-        rva[i] = m0 + 8 * q < p.M;
-        voa[i] = (unsigned)((long)k * p.lda * 2 + 16 * q);
+        voa[i] = m0 + 8 * q < p.M ? (unsigned)((long)k * p.lda * 2 + 16 * q) : kOutOfRange;
       }
     }
 #pragma unroll
@@ -578,33 +591,36 @@ gemm_f16_ring_kernel(GemmParams p) {
       if (TB) {
         const int r = c * 16 + (lane & 15), q = lane >> 4;
         klb[i] = 8 * q;
-        rvb[i] = n0 + r < p.N;
-        vob[i] = (unsigned)((long)r * p.ldb * 2 + 16 * q);
+        vob[i] = n0 + r < p.N ? (unsigned)((long)r * p.ldb * 2 + 16 * q) : kOutOfRange;
       } else {
         constexpr int GPR = RBB / 16;
         const int k = c * (1024 / RBB) + lane / GPR, qp = lane % GPR;
         const int q = 2 * ((qp >> 1) ^ hsw(k)) + (qp & 1);
         klb[i] = k;
-        rvb[i] = n0 + 8 * q < p.N;
-        vob[i] = (unsigned)((long)k * p.ldb * 2 + 16 * q);
+        vob[i] = n0 + 8 * q < p.N ? (unsigned)((long)k * p.ldb * 2 + 16 * q) : kOutOfRange;
       }
     }
   }
   const long a_step = TA ? (long)BK * p.lda * 2 : (long)BK * 2;
   const long b_step = TB ? (long)BK * 2 : (long)BK * p.ldb * 2;
   const unsigned sbase = lds_offset(smem);
-  const int nk = (int)((p.K + BK - 1) / BK);
+  const int nk = kt1 - kt0;
+  const int nk2 = max(2, (nk + 1) & ~1);  // K-tiles the loop runs: tiles nk.. are all zeros
+  const long kend = min(p.K, (long)kt1 * BK) - (long)kt0 * BK;  // K extent of this range
 
-  auto issue = [&](int t) {  // DMA of K-tile t into stage t % S (descriptors point at tile t)
-    const unsigned st = sbase + (unsigned)((t % S) * STB);
-    const long krem = p.K - (long)t * BK;
+  // DMA of K-tile kt0 + t into LDS stage `stage` (the descriptors point at it). Lanes
+  // whose k lies at or past the range's end, which includes every lane of a tile
+  // t >= nk, load zeros.
+  auto issue = [&](int t, int stage) {
+    const unsigned st = sbase + (unsigned)(stage * STB);
+    const long krem_l = kend - (long)t * BK;
+    const int krem = (int)(krem_l < 0 ? 0 : (krem_l > BK ? BK : krem_l));
 #pragma unroll
     for (int i = 0; i < IPA; ++i)
-      dma16(ra, (rva[i] && kla[i] < krem) ? voa[i] : kOutOfRange,
-            __builtin_amdgcn_readfirstlane(st + (wave * IPA + i) * 1024));
+      dma16(ra, kla[i] < krem ? voa[i] : kOutOfRange, __builtin_amdgcn_readfirstlane(st + (wave * IPA + i) * 1024));
 #pragma unroll
     for (int i = 0; i < IPB; ++i)
-      dma16(rb, (rvb[i] && klb[i] < krem) ? vob[i] : kOutOfRange,
+      dma16(rb, klb[i] < krem ? vob[i] : kOutOfRange,
             __builtin_amdgcn_readfirstlane(st + OPA + (wave * IPB + i) * 1024));
     rsrc_advance(ra, a_step);
     rsrc_advance(rb, b_step);
@@ -626,8 +642,8 @@ gemm_f16_ring_kernel(GemmParams p) {
   };
 
   half8_t fa[2][FM], fb[2][FN];
-  auto read_frags = [&](int t, int set) {
-    const char *st = smem + (t % S) * STB;
+  auto read_frags = [&](int stage, int set) {
+    const char *st = smem + stage * STB;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
       fa[set][i] = TA ? frag_t(st, wm * WTM + i * 16, RBA) : frag_k(st, wm * WTM + i * 16);
@@ -636,11 +652,6 @@ gemm_f16_ring_kernel(GemmParams p) {
       fb[set][j] = TB ? frag_k(st + OPA, wn * WTN + j * 16) : frag_t(st + OPA, wn * WTN + j * 16, RBB);
   };
 
-  float4_t acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
   auto mfma_set = [&](int set) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -650,28 +661,26 @@ gemm_f16_ring_kernel(GemmParams p) {
   };
 
   // Prologue: tiles 0..S-2 in flight; wait for tile 0.
-  for (int t = 0; t < S - 1 && t < nk; ++t) issue(t);
-  {
-    const int after = min(nk - 1, S - 2);  // tiles issued after tile 0
-    if (after >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LPW));
-    else if (after == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPW));
-    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-  }
+#pragma unroll
+  for (int t = 0; t < S - 1; ++t) issue(t, t);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 2) * LPW));
   __syncthreads();
-  if (nk > 0) read_frags(0, 0);
 
-  // Steady state (tiles k+1..k+S-1 exist): tile k+1 has landed (tiles k+2..k+S-2 may
-  // still be in flight); publish it, refill the stage tile k-1 used with tile k+S-1,
-  // read tile k+1's fragments into the other register set, multiply tile k. The
-  // scheduling fences keep tile k's MFMAs ahead of the next barrier, and the group
-  // barriers interleave one LDS read per MFMA.
-  auto steady = [&](int k, int set) {
+  // One K-tile per step, the same instructions for every step: tile k+1 has landed
+  // (tiles k+2..k+S-2 may still be in flight); publish it, refill the stage tile k-1
+  // used with tile k+S-1 (zeros past the end of K), read tile k+1's fragments into the
+  // other register set, multiply tile k. The scheduling fences keep tile k's MFMAs
+  // ahead of the next barrier, and the group barriers interleave one LDS read per MFMA.
+  // The loop runs an even number of tiles; a padding tile multiplies zeros.
+  // Stages rotate: tile k+1 is read from stage sr and tile k+S-1 lands in stage si.
+  int sr = 1 % S, si = S - 1;
+  auto step = [&](int k, int set) {
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 3) * LPW));
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
-    issue(k + S - 1);
-    read_frags(k + 1, set ^ 1);
+    issue(k + S - 1, si);
+    read_frags(sr, set ^ 1);
     mfma_set(set);
 #pragma unroll
     for (int g = 0; g < FM + 2 * FN; ++g) {
@@ -679,40 +688,52 @@ gemm_f16_ring_kernel(GemmParams p) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - (FM + 2 * FN), 0);
+    sr = sr + 1 == S ? 0 : sr + 1;
+    si = si + 1 == S ? 0 : si + 1;
   };
-  // Last S-1 or fewer tiles: same steps with the waits and refills the tail allows.
-  auto tail = [&](int k, int set) {
-    if (k + 1 < nk) {
-      const int after = min(nk - 1, k + S - 2) - (k + 1);  // tiles issued after k+1
-      if (after >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LPW));
-      else if (after == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPW));
-      else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-      __syncthreads();
-      if (k + S - 1 < nk) issue(k + S - 1);
-      read_frags(k + 1, set ^ 1);
-    }
-    mfma_set(set);
-  };
-  int k = 0;
-  for (; k + S < nk; k += 2) {
-    steady(k, 0);
-    steady(k + 1, 1);
-  }
-#pragma unroll
-  for (int u = 0; u < S; u += 2) {
-    if (k + u < nk) tail(k + u, 0);
-    if (k + u + 1 < nk) tail(k + u + 1, 1);
+  read_frags(0, 0);
+  for (int k = 0; k < nk2; k += 2) {
+    step(k, 0);
+    step(k + 1, 1);
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-  __syncthreads();  // every wave is done with the ring; reuse it to stage C
+  __syncthreads();
+}
 
-  constexpr int EP = (NW * 32 * (WTN + 4) * 4 <= S * STB) ? 32 : 16;  // rows per staging pass
-  static_assert(NW * EP * (WTN + 4) * 4 <= S * STB, "epilogue staging exceeds the ring");
+// Writes one wave's accumulator tile to C through the LDS staging region (the ring).
+template <int BM, int BN, int WM, int WN, int S>
+__device__ __forceinline__ void ring_epilogue(const GemmParams &p, long m0, long n0, long z, char *smem,
+                                              const float4_t (&acc)[BM / WM / 16][BN / WN / 16]) {
+  constexpr int NW = WM * WN, WTM = BM / WM, WTN = BN / WN, FM = WTM / 16, FN = WTN / 16;
+  constexpr int RING = S * (BM + BN) * 32 * 2;
+  constexpr int EP = (NW * 32 * (WTN + 4) * 4 <= RING) ? 32 : 16;  // rows per staging pass
+  static_assert(NW * EP * (WTN + 4) * 4 <= RING, "epilogue staging exceeds the ring");
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
   float *C = p.C + z * p.strideC;
   const bool vec_ok = (p.ldc % 4 == 0) && (((uintptr_t)C & 15) == 0);
   float *region = reinterpret_cast<float *>(smem) + wave * EP * (WTN + 4);
   store_tile_coalesced<FM, FN, EP>(p, C, m0 + wm * WTM, n0 + wn * WTN, acc, region, vec_ok,
                                    std::make_integer_sequence<int, FM / (EP / 16)>{});
+}
+
+// One workgroup per output tile, the whole K range. WPE: waves per SIMD the register
+// allocation is sized for.
+template <int BM, int BN, int WM, int WN, int S, bool TA, bool TB, int WPE>
+__global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+gemm_f16_ring_kernel(GemmParams p) {
+  using Cfg = RingCfg<BM, BN, WM, WN, S, TA, TB>;
+  __shared__ __attribute__((aligned(1024))) char smem[S * Cfg::STB];
+  int tm, tn;
+  tile_coords(p, tm, tn);
+  float4_t acc[Cfg::FM][Cfg::FN];
+#pragma unroll
+  for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < Cfg::FN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+  const long m0 = (long)tm * BM, n0 = (long)tn * BN, z = blockIdx.z;
+  ring_mainloop<BM, BN, WM, WN, S, TA, TB>(p, m0, n0, z, 0, (int)((p.K + 31) / 32), smem, acc);
+  ring_epilogue<BM, BN, WM, WN, S>(p, m0, n0, z, smem, acc);
 }
 
 // ------------------------------------------------------------------ dispatch
@@ -734,12 +755,12 @@ hipError_t launch_f32(GemmParams p, long batch, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int BM, int BN, int WM, int WN, int S, bool TA, bool TB>
+template <int BM, int BN, int WM, int WN, int S, bool TA, bool TB, int WPE = 2>
 hipError_t launch_f16_ring(GemmParams p, long batch, hipStream_t s) {
   p.tiles_m = (int)((p.M + BM - 1) / BM);
   p.tiles_n = (int)((p.N + BN - 1) / BN);
   dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
-  hipLaunchKernelGGL((gemm_f16_ring_kernel<BM, BN, WM, WN, S, TA, TB>), grid, dim3(WM * WN * 64), 0, s, p);
+  hipLaunchKernelGGL((gemm_f16_ring_kernel<BM, BN, WM, WN, S, TA, TB, WPE>), grid, dim3(WM * WN * 64), 0, s, p);
   return hipGetLastError();
 }
 

@@ -350,3 +350,50 @@ def test_f16_ring_batched_and_epilogue(dev):
     for z in range(bs):
         pre = O.gemm_f64_rows(O.round_f16(A[z][rows], False), O.round_f16(B[z], False), np.arange(rows.size)) + bias
         assert O.rel_frob(Cn[z][rows], O.act_f64(G.ACT_GELU, pre)) <= 1e-5, z
+
+
+# ------------------------------------------------------------------ fp16, fewer 256x256 tiles than CUs
+@pytest.mark.parametrize("tA,tB", VARIANTS)
+def test_f16_few_tiles_ragged_all_transposes(dev, tA, tB):
+    """3 x 12 tiles of 256 (the register-staged kernels take it) with M, N ragged and an
+    8-deep K tail (K = 5000)."""
+    rng = np.random.default_rng(43)
+    M, N, K = 704, 3000, 5000
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
+    C = _gemm_dev(dev, A, B, tA, tB, G.GN_F16)
+    rows = np.concatenate([np.arange(0, 8), rng.choice(M, 16, replace=False), np.arange(M - 8, M)])
+    ref_r = O.gemm_f64_rows(O.round_f16(A[rows], False), O.round_f16(B, False), np.arange(rows.size))
+    err = O.rel_frob(C[rows], ref_r)
+    _say("few tiles ragged", tA, tB, err)
+    assert err <= 1e-5
+    assert np.isfinite(C).all()
+
+
+def test_f16_deterministic_batched_epilogue(dev):
+    """Batched fp16 GEMM with beta*C + bias + GELU: two runs agree bit for bit and the
+    epilogue is applied once."""
+    import torch
+
+    rng = np.random.default_rng(47)
+    bs, M, N, K = 3, 512, 1024, 8192
+    A = rng.standard_normal((bs, M, K)).astype(np.float32)
+    B = (0.02 * rng.standard_normal((bs, K, N))).astype(np.float32)
+    C0 = rng.standard_normal((bs, M, N)).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    a16 = torch.from_numpy(A).to(dev).half()
+    b16 = torch.from_numpy(B).to(dev).half()
+    outs = []
+    for _ in range(2):
+        C = torch.from_numpy(C0).to(dev)
+        G.gemm(a16, b16, C, batch=bs, strideA=M * K, strideB=K * N, strideC=M * N, beta=0.5,
+               bias=torch.from_numpy(bias).to(dev), act=G.ACT_GELU)
+        outs.append(C.cpu().numpy())
+    np.testing.assert_array_equal(outs[0], outs[1])
+    rows = rng.choice(M, 10, replace=False)
+    for z in range(bs):
+        pre = (O.gemm_f64_rows(O.round_f16(A[z][rows], False), O.round_f16(B[z], False), np.arange(rows.size))
+               + 0.5 * C0[z][rows] + bias)
+        err = O.rel_frob(outs[0][z][rows], O.act_f64(G.ACT_GELU, pre))
+        _say("batched epilogue", z, err)
+        assert err <= 1e-5, z
