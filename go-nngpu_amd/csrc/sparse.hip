@@ -13,7 +13,12 @@
 // column skips that entry and raises flags[1]. No access ever leaves its array.
 //
 // SpMV: LPR lanes per row stride over the row's entries and combine their partial
-// sums with an xor-shuffle tree (a different, tolerance-level summation order).
+// sums with an xor-shuffle tree (a different, tolerance-level summation order). Rows
+// of 32 or more entries on average take spmv_wave_kernel: one wave per RW consecutive
+// rows, 64 lanes per row, with the RW rows' loads issued together so that each wave
+// keeps RW independent col/val -> x load chains in flight. Each entry's x gather is a
+// separate L2 request (x stays in L2), and that request rate, not HBM bandwidth, is
+// what bounds SpMV at C5's sparsity.
 #include "common.h"
 
 namespace gn {
@@ -187,6 +192,62 @@ int launch_spmm(long M, long N, long K, long nnz, const int32_t *rowptr, const i
   return e == hipSuccess ? 0 : hip_error(err, -6, "spmm launch", e);
 }
 
+namespace {
+
+// Lane l of a row sums entries s+l, s+l+64, ... in order; the shuffle tree then gives
+// the same result, bit for bit, as spmv_kernel<64>.
+template <int RW>
+__global__ void __launch_bounds__(kBlock) spmv_wave_kernel(long M, long K, long nnz, const int32_t *__restrict__ rowptr,
+                                                           const int32_t *__restrict__ col,
+                                                           const float *__restrict__ val, const float *__restrict__ x,
+                                                           float *__restrict__ y, int *flags) {
+  const int lane = threadIdx.x & 63;
+  const long r0 = (long)__builtin_amdgcn_readfirstlane((int)(blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6))) * RW;
+  if (r0 >= M) return;  // the whole wave
+  int s[RW], e[RW];
+  int maxlen = 0;
+#pragma unroll
+  for (int u = 0; u < RW; ++u) {
+    s[u] = e[u] = 0;
+    if (r0 + u < M) row_bounds(rowptr, r0 + u, nnz, s[u], e[u], flags, lane == 0);
+    maxlen = max(maxlen, e[u] - s[u]);
+  }
+  float acc[RW];
+#pragma unroll
+  for (int u = 0; u < RW; ++u) acc[u] = 0.f;
+  for (int base = 0; base < maxlen; base += 64) {
+    int cc[RW];
+    float vv[RW], xx[RW];
+#pragma unroll
+    for (int u = 0; u < RW; ++u) {
+      const int k = s[u] + base + lane;
+      cc[u] = -1;
+      vv[u] = 0.f;
+      if (k < e[u]) {
+        cc[u] = col[k];
+        vv[u] = val[k];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < RW; ++u) {
+      const bool ok = (unsigned)cc[u] < (unsigned long)K;
+      xx[u] = ok ? x[cc[u]] : 0.f;
+      if (!ok && cc[u] != -1 && flags) flags[1] = 1;
+    }
+#pragma unroll
+    for (int u = 0; u < RW; ++u)
+      if ((unsigned)cc[u] < (unsigned long)K) acc[u] = __builtin_fmaf(vv[u], xx[u], acc[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < RW; ++u) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc[u] += __shfl_xor(acc[u], off, 64);
+    if (lane == 0 && r0 + u < M) y[r0 + u] = acc[u];
+  }
+}
+
+}  // namespace
+
 int launch_spmv(long M, long K, long nnz, const int32_t *rowptr, const int32_t *col, const float *val,
                 const float *x, float *y, int *flags, hipStream_t s, CError *err) {
   if (M < 0 || K < 0 || nnz < 0) return set_error(err, -1, "spmv: negative size");
@@ -197,6 +258,15 @@ int launch_spmv(long M, long K, long nnz, const int32_t *rowptr, const int32_t *
   const long mean = nnz / M;
   int lpr = 4;
   while (lpr < 64 && lpr * 2 <= mean / 2) lpr <<= 1;
+  if (mean >= 32) {
+    constexpr int RW = 2;
+    const long blocks = (M + (kBlock / 64) * RW - 1) / ((kBlock / 64) * RW);
+    if (blocks > 0x7FFFFFFFL / (kBlock / 64)) return set_error(err, -1, "spmv: too many rows");
+    hipLaunchKernelGGL(spmv_wave_kernel<RW>, dim3((unsigned)blocks), dim3(kBlock), 0, s, M, K, nnz, rowptr, col, val, x,
+                       y, flags);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : hip_error(err, -6, "spmv launch", e);
+  }
   const long rows_per_block = (kBlock / 64) * (64 / lpr);
   const long blocks = (M + rows_per_block - 1) / rows_per_block;
   if (blocks > 0x7FFFFFFFL) return set_error(err, -1, "spmv: too many rows");

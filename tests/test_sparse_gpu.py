@@ -132,12 +132,14 @@ def test_spmv_golden_and_random(dev):
     z = np.load(os.path.join(GOLD, "csr_64.npz"))
     y = _spmv_abi(z["rowptr"], z["idx"], z["data"], z["x"], 64, 64)
     assert O.rel_frob(y, z["y64"]) <= 1e-5
-    for mean in (0.5, 3.0, 40.0, 300.0):
-        rp, col, val = O.random_csr(1000, 2000, mean, seed=int(mean * 10))
+    # mean row lengths on both sides of the 32-entry switch to the wave-per-row kernel;
+    # 1003 rows leave a partial group of rows in the last wave, 300 spans 5 chunks of 64
+    for M, mean in ((1000, 0.5), (1000, 3.0), (1003, 31.0), (1003, 40.0), (1000, 300.0)):
+        rp, col, val = O.random_csr(M, 2000, mean, seed=int(mean * 10))
         x = O.normal((2000,), 3, int(mean))
-        y = _spmv_abi(rp, col, val, x, 1000, 2000)
-        assert O.rel_frob(y, O.spmv_f64(rp, col, val, x)) <= 1e-5
-        assert O.rel_frob(y, O.spmv_f32(rp, col, val, x).astype(np.float64)) <= 1e-5
+        y = _spmv_abi(rp, col, val, x, M, 2000)
+        assert O.rel_frob(y, O.spmv_f64(rp, col, val, x)) <= 1e-5, mean
+        assert O.rel_frob(y, O.spmv_f32(rp, col, val, x).astype(np.float64)) <= 1e-5, mean
 
 
 def test_spmv_dimension_and_csr_errors(dev):
@@ -174,3 +176,32 @@ def test_transpose_reference_abi(dev):
         np.testing.assert_array_equal(bo.to_array((c, r)), O.transpose_f32(X))
     rc, _ = G.call_rc("perform_mps_matrix_transpose", bi.handle, 1000, 3, bo.handle, 1000, 3, None)
     assert rc == -2
+
+
+def test_spmv_wave_kernel_empty_rows_and_bad_columns(dev):
+    """Long rows (wave-per-row kernel) mixed with empty rows; an out-of-range column is
+    skipped and reported."""
+    import torch
+
+    rng = np.random.default_rng(61)
+    M, K = 37, 500
+    lens = rng.integers(40, 200, M)
+    lens[[0, 5, 6, 36]] = 0
+    rp = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    col = np.concatenate([np.sort(rng.choice(K, n, replace=False)) for n in lens]).astype(np.int32)
+    val = rng.standard_normal(col.size).astype(np.float32)
+    x = rng.standard_normal(K).astype(np.float32)
+    y = _spmv_abi(rp, col, val, x, M, K)
+    assert np.all(y[[0, 5, 6, 36]] == 0)
+    assert O.rel_frob(y, O.spmv_f64(rp, col, val, x)) <= 1e-5
+    # same answer bit for bit through the device-pointer entry (gn_spmv_csr)
+    d = [torch.from_numpy(a).to(dev) for a in (rp, col, val, x)]
+    yd = torch.empty(M, dtype=torch.float32, device=dev)
+    G.spmv_csr(M, K, val.size, d[0], d[1], d[2], d[3], yd)
+    np.testing.assert_array_equal(yd.cpu().numpy(), y)
+    bad = col.copy()
+    bad[rp[1] + 3] = K + 7
+    bv, bx, by = G.Buffer.from_array(val), G.Buffer.from_array(x), G.Buffer(M * 4)
+    rc, msg = G.call_rc("perform_sparse_matvec", bv.handle, rp.ctypes.data, rp.size, bad.ctypes.data, bad.size, M, K,
+                        val.size, bx.handle, K, by.handle, M, None)
+    assert rc == -3 and "column" in msg
