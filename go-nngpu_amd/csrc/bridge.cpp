@@ -313,6 +313,13 @@ int gn_cast_f16_f32(const uint16_t *in, float *out, size_t n, void *stream, CErr
   return gn::launch_cast_f16_f32(in, out, n, gn::resolve_stream(stream), err);
 }
 
+int gn_activation_backward(const float *grad_out, const float *pre, long rows, long cols, int act, float alpha,
+                           float scale, float *grad_in, float *grad_bias, void *stream, CError *err) {
+  if (!gn::context(err)) return -1;
+  return gn::launch_act_backward(grad_out, pre, rows, cols, act, alpha, scale, grad_in, grad_bias,
+                                 gn::resolve_stream(stream), err);
+}
+
 int gn_transpose_f32(const float *in, long rows, long cols, float *out, void *stream, CError *err) {
   if (!gn::context(err)) return -1;
   return gn::launch_transpose_f32(in, rows, cols, out, gn::resolve_stream(stream), err);

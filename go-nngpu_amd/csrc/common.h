@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstddef>
 #include <cstdint>
+#include <mutex>
 
 #include "../../include/gonngpu.h"
 
@@ -36,6 +37,11 @@ hipStream_t resolve_stream(void *stream);  // NULL -> library stream
 void *dev_alloc(size_t bytes, CError *err);
 void dev_free(void *p);
 void memory_stats(long *cur, long *peak, long *n);
+// Device scratch owned by the library, one block per stream, grown on demand (after
+// synchronising the stream). lk holds a library mutex on return: keep it until every
+// kernel that uses the scratch is enqueued, so that another host thread cannot enqueue
+// work that reuses it in between (kernels on one stream run in order).
+void *stream_scratch(hipStream_t s, size_t bytes, std::unique_lock<std::mutex> &lk, CError *err);
 
 // ---------------------------------------------------------------- host <-> device
 // Synchronous copies of pageable host memory through a pinned staging ring.
@@ -73,6 +79,11 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err);
 int launch_cast_f32_f16(const float *in, uint16_t *out, size_t n, int mode, hipStream_t s, CError *err);
 int launch_cast_f16_f32(const uint16_t *in, float *out, size_t n, hipStream_t s, CError *err);
 int launch_transpose_f32(const float *in, long rows, long cols, float *out, hipStream_t s, CError *err);
+// grad_in = grad_out * act'(pre) * scale element-wise (derivative with respect to the
+// pre-activation), and optionally grad_bias[j] = sum over rows of grad_in[., j].
+int launch_act_backward(const float *grad_out, const float *pre, long rows, long cols, int act, float alpha,
+                        float scale, float *grad_in, float *grad_bias, hipStream_t s, CError *err);
+bool act_grad_supported(int act);
 int launch_spmm(long M, long N, long K, long nnz, const int32_t *rowptr, const int32_t *col, const float *val,
                 const float *D, long ldd, float *C, long ldc, int *flags, hipStream_t s, CError *err);
 int launch_spmv(long M, long K, long nnz, const int32_t *rowptr, const int32_t *col, const float *val,

@@ -1,5 +1,7 @@
 // elementwise.hip — bandwidth-bound helpers: fp32<->fp16 casts, LDS-tiled
 // transpose, synthetic-data generators and a flag-clearing kernel.
+#include <algorithm>
+
 #include "common.h"
 
 namespace gn {
@@ -124,7 +126,105 @@ uint64_t stream_base(uint64_t seed, uint64_t sid) {
   return seed ^ (z ^ (z >> 31));
 }
 
+// ------------------------------------------------------------------ activation backward
+// Derivative of the epilogue activations (apply_act in gemm.hip, Go ActivationType codes)
+// with respect to their input x, evaluated at x.
+__device__ __forceinline__ float act_grad(int act, float x, float a) {
+  switch (act) {
+    case 0: return x > 0.0f ? 1.0f : 0.0f;
+    case 1: {
+      const float sg = 1.0f / (1.0f + __expf(-fmaxf(-88.0f, fminf(88.0f, x))));
+      return sg * (1.0f - sg);
+    }
+    case 2: {
+      const float t = tanhf(x);
+      return 1.0f - t * t;
+    }
+    case 4: return x > 0.0f ? 1.0f : a;
+    case 5: return x > 0.0f ? 1.0f : a * __expf(fmaxf(-88.0f, x));
+    case 6: {
+      const float c = fmaxf(-88.0f, fminf(88.0f, x));
+      const float sg = 1.0f / (1.0f + __expf(-c));
+      return sg + c * sg * (1.0f - sg);
+    }
+    case 7: {
+      const float k = 0.7978845608028654f;
+      const float inner = fmaxf(-88.0f, fminf(88.0f, k * (x + 0.044715f * x * x * x)));
+      const float t = tanhf(inner);
+      return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * k * (1.0f + 3.0f * 0.044715f * x * x);
+    }
+    default: return 1.0f;
+  }
+}
+
+// One thread per column j and chunk of R rows (blockIdx.y): grad_in = (grad_out * act') *
+// scale, and partial[chunk, j] = the chunk's column sum in row order. A wave's 64
+// threads read 64 consecutive columns of a row: one coalesced 256-byte segment.
+__global__ void __launch_bounds__(256) act_backward_kernel(const float *__restrict__ dy, const float *__restrict__ pre,
+                                                           long M, long N, int act, float alpha, float scale,
+                                                           float *dx, float *__restrict__ partial, long R) {
+  const long j = (long)blockIdx.x * 256 + threadIdx.x;
+  if (j >= N) return;
+  const long r0 = (long)blockIdx.y * R;
+  const long r1 = min(M, r0 + R);
+  float sum = 0.0f;
+  for (long r = r0; r < r1; ++r) {
+    const long i = r * N + j;
+    const float g = (dy[i] * act_grad(act, pre[i], alpha)) * scale;
+    dx[i] = g;
+    sum += g;
+  }
+  if (partial) partial[(long)blockIdx.y * N + j] = sum;
+}
+
+// out[j] = sum of partial[c, j] over c = 0, 1, ... (fixed order: deterministic).
+__global__ void __launch_bounds__(256) colsum_finish_kernel(const float *__restrict__ partial, long chunks, long N,
+                                                            float *__restrict__ out) {
+  const long j = (long)blockIdx.x * 256 + threadIdx.x;
+  if (j >= N) return;
+  float sum = 0.0f;
+  for (long c = 0; c < chunks; ++c) sum += partial[c * N + j];
+  out[j] = sum;
+}
+
 }  // namespace
+
+bool act_grad_supported(int act) { return act == -1 || act == 0 || act == 1 || act == 2 || (act >= 4 && act <= 7); }
+
+int launch_act_backward(const float *grad_out, const float *pre, long rows, long cols, int act, float alpha,
+                        float scale, float *grad_in, float *grad_bias, hipStream_t s, CError *err) {
+  if (rows < 0 || cols < 0) return set_error(err, -1, "activation backward: negative size");
+  if (!act_grad_supported(act)) return set_error(err, -1, "activation backward: unsupported activation %d", act);
+  if (cols == 0) return 0;
+  if (rows == 0) {  // an empty column sum is zero (a kernel, not a memset, so it can be captured)
+    if (!grad_bias) return 0;
+    hipLaunchKernelGGL(colsum_finish_kernel, dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, s, nullptr, 0L, cols,
+                       grad_bias);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : hip_error(err, -6, "activation backward launch", e);
+  }
+  if (!grad_out || !pre || !grad_in) return set_error(err, -1, "activation backward: NULL pointer");
+  const long colblocks = (cols + 255) / 256;
+  if (colblocks > 0x7FFFFFFFL) return set_error(err, -1, "activation backward: too many columns");
+  // Enough (column block, row chunk) workgroups to fill the GPU, at least 8 rows each.
+  long chunks = (4096 + colblocks - 1) / colblocks;
+  chunks = std::max(1L, std::min(chunks, (rows + 7) / 8));
+  const long R = (rows + chunks - 1) / chunks;
+  chunks = (rows + R - 1) / R;
+  float *partial = nullptr;
+  std::unique_lock<std::mutex> lk;
+  if (grad_bias) {
+    partial = static_cast<float *>(stream_scratch(s, (size_t)chunks * cols * sizeof(float), lk, err));
+    if (!partial) return -3;
+  }
+  hipLaunchKernelGGL(act_backward_kernel, dim3((unsigned)colblocks, (unsigned)chunks), dim3(256), 0, s, grad_out, pre,
+                     rows, cols, act, alpha, scale, grad_in, partial, R);
+  if (grad_bias)
+    hipLaunchKernelGGL(colsum_finish_kernel, dim3((unsigned)colblocks), dim3(256), 0, s, partial, chunks, cols,
+                       grad_bias);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : hip_error(err, -6, "activation backward launch", e);
+}
 
 int launch_cast_f32_f16(const float *in, uint16_t *out, size_t n, int mode, hipStream_t s, CError *err) {
   if (mode != GN_ROUND_NEAREST_EVEN && mode != GN_ROUND_TOWARD_ZERO)

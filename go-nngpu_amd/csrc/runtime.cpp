@@ -286,4 +286,35 @@ bool unregister_buffer(Buffer *b) {
   return true;
 }
 
+// ---------------------------------------------------------------- per-stream scratch
+static std::mutex g_scratch_mu;
+struct StreamScratch {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+};
+static std::unordered_map<hipStream_t, StreamScratch> g_scratch;
+
+void *stream_scratch(hipStream_t s, size_t bytes, std::unique_lock<std::mutex> &lk, CError *err) {
+  lk = std::unique_lock<std::mutex>(g_scratch_mu);
+  StreamScratch &w = g_scratch[s];
+  if (w.bytes < bytes) {
+    if (w.ptr) {
+      // Kernels already enqueued on s may still read the old block.
+      hipError_t e = hipStreamSynchronize(s);
+      if (e != hipSuccess) {
+        hip_error(err, -6, "scratch: synchronize", e);
+        return nullptr;
+      }
+      dev_free(w.ptr);
+      w = StreamScratch{};
+    }
+    const size_t nb = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+    void *p = dev_alloc(nb, err);
+    if (!p) return nullptr;
+    w.ptr = p;
+    w.bytes = nb;
+  }
+  return w.ptr;
+}
+
 }  // namespace gn

@@ -71,6 +71,7 @@ SIGNATURES = {
                      _ERR]),
     "gn_cast_f32_f16": (_I, [_VP, _VP, _SZ, _I, _VP, _ERR]),
     "gn_cast_f16_f32": (_I, [_VP, _VP, _SZ, _VP, _ERR]),
+    "gn_activation_backward": (_I, [_VP, _VP, _L, _L, _I, _F, _F, _VP, _VP, _VP, _ERR]),
     "gn_transpose_f32": (_I, [_VP, _L, _L, _VP, _VP, _ERR]),
     "gn_spmm_csr": (_I, [_L, _L, _L, _L, _VP, _VP, _VP, _VP, _L, _VP, _L, _VP, _VP, _ERR]),
     "gn_spmv_csr": (_I, [_L, _L, _L, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _ERR]),
@@ -244,6 +245,13 @@ def cast_f32_f16(x, out, round_mode=ROUND_NEAREST_EVEN, stream_ptr=None):
 
 def cast_f16_f32(x, out, stream_ptr=None):
     _dispatch(stream_ptr, "gn_cast_f16_f32", _ptr(x), _ptr(out), x.numel())
+
+
+def activation_backward(grad_out, pre, act, grad_in, grad_bias=None, alpha=0.0, scale=1.0, stream_ptr=None):
+    """grad_in = grad_out * act'(pre) * scale; grad_bias = column sums of grad_in (optional)."""
+    rows, cols = pre.shape
+    _dispatch(stream_ptr, "gn_activation_backward", _ptr(grad_out), _ptr(pre), rows, cols, act, alpha, scale,
+              _ptr(grad_in), _ptr(grad_bias))
 
 
 def transpose(x, out, stream_ptr=None):

@@ -230,7 +230,19 @@ class FusedLinearActivation {
   std::string GetName() const { return "linear_activation"; }
   // inputs = {input [batch,in], weight [in,out], optional bias [out]}.
   Result<TensorPtr> Forward(const std::vector<Tensor *> &inputs, const FusedLinearConfig *config);
+  // FusedLinearActivation.Backward (fused-operations.go:467-578). savedTensors =
+  // {input [batch,in], weight [in,out], pre-activation [batch,out] (needed by ReLU,
+  // LeakyReLU, Sigmoid, Tanh and GELU)}. Returns {grad_input [batch,in],
+  // grad_weight [in,out]} plus grad_bias [1,out] when config->Bias and three tensors
+  // were saved. A nil activation, and Softmax / ELU / Swish, pass the gradient through
+  // unchanged, as the reference's switch does.
+  Result<std::vector<TensorPtr>> Backward(Tensor &gradOutput, const std::vector<Tensor *> &savedTensors,
+                                          const FusedLinearConfig *config);
 };
+
+// matmulBackward of gpu/matrix/gradient.go:601-637 for C = A * B:
+// {grad_A = grad_output * B^T, grad_B = A^T * grad_output} (device-resident).
+Result<std::vector<TensorPtr>> MatMulBackward(Tensor &gradOutput, Tensor &A, Tensor &B);
 
 // Mixed precision (gpu/matrix/mixed-precision.go).
 using FloatMP16 = uint16_t;

@@ -218,6 +218,103 @@ Result<TensorPtr> FusedLinearActivation::Forward(const std::vector<Tensor *> &in
   return {output, {}};
 }
 
+namespace {
+
+// C[M,N] = op(A) * op(B) in fp32 on device pointers (row-major, packed), synchronised.
+Error gemm_f32(bool ta, bool tb, long M, long N, long K, const float *A, const float *B, float *C, const char *what) {
+  CError ce{nullptr};
+  int rc = gn_gemm(GN_F32, ta ? 1 : 0, tb ? 1 : 0, M, N, K, 1.0f, A, ta ? M : K, 0, B, tb ? K : N, 0, 0.0f, C, N, 0,
+                   1, nullptr, GN_ACT_NONE, 0.0f, nullptr, &ce);
+  if (rc == 0) rc = gn_synchronize(nullptr, &ce);
+  return rc == 0 ? Error{} : op_error(what, rc, ce);
+}
+
+}  // namespace
+
+Result<std::vector<TensorPtr>> FusedLinearActivation::Backward(Tensor &gradOutput,
+                                                               const std::vector<Tensor *> &savedTensors,
+                                                               const FusedLinearConfig *config) {
+  if (!config) return {{}, Errorf("invalid config type for FusedLinearActivation backward")};
+  if (savedTensors.size() < 2 || !savedTensors[0] || !savedTensors[1])
+    return {{}, Errorf("insufficient saved tensors for FusedLinearActivation backward")};
+  Tensor &input = *savedTensors[0];
+  Tensor &weight = *savedTensors[1];
+  Tensor *pre = savedTensors.size() > 2 ? savedTensors[2] : nullptr;
+  if (input.Shape.size() != 2 || weight.Shape.size() != 2 || gradOutput.Shape.size() != 2 ||
+      input.Shape[1] != weight.Shape[0] || gradOutput.Shape[0] != input.Shape[0] ||
+      gradOutput.Shape[1] != weight.Shape[1])
+    return {{}, Errorf("FusedLinearActivation backward needs input [batch,in], weight [in,out], grad [batch,out]")};
+  const long batch = input.Shape[0], in = input.Shape[1], out = weight.Shape[1];
+  // Step 1: activation backward at the pre-activation (the reference switch, :489-523).
+  int act = GN_ACT_NONE;
+  float alpha = 0.0f;
+  if (config->Activation) {
+    switch (config->Activation->ActivationType) {
+      case ReLU: case LeakyReLU: case Sigmoid: case Tanh: case GELU:
+        act = config->Activation->ActivationType;
+        alpha = config->Activation->Alpha;
+        break;
+      default: break;  // the reference's default branch: gradient passes through
+    }
+  }
+  if (act != GN_ACT_NONE && (!pre || pre->Shape != gradOutput.Shape))
+    return {{}, Errorf("failed to apply activation backward: pre-activation tensor [batch,out] required")};
+  // Step 2: dropout scaling (:528-537).
+  const float scale = config->Dropout > 0.0f ? (float)(1.0 / (1.0 - (double)config->Dropout)) : 1.0f;
+  const bool want_bias = config->Bias && savedTensors.size() >= 3;
+  if (Error e = gradOutput.EnsureGPU()) return {{}, wrap("failed to move gradient to GPU", e)};
+  if (Error e = input.EnsureGPU()) return {{}, wrap("failed to move input to GPU", e)};
+  if (Error e = weight.EnsureGPU()) return {{}, wrap("failed to move weight to GPU", e)};
+  if (pre && act != GN_ACT_NONE)
+    if (Error e = pre->EnsureGPU()) return {{}, wrap("failed to move pre-activation to GPU", e)};
+  DeviceScratch g;
+  if (Error e = g.alloc((size_t)(batch * out) * 4)) return {{}, e};
+  TensorPtr gradBias;
+  if (want_bias) {
+    auto [gb, berr] = Tensor::NewDeviceResult({1, (int)out});
+    if (berr) return {{}, wrap("failed to create bias gradient", berr)};
+    gradBias = gb;
+  }
+  CError ce{nullptr};
+  int rc = gn_activation_backward(dptr(gradOutput), act != GN_ACT_NONE ? dptr(*pre) : dptr(gradOutput), batch, out,
+                                  act, alpha, scale, (float *)g.p, gradBias ? dptr(*gradBias) : nullptr, nullptr, &ce);
+  if (rc != 0) return {{}, op_error("activation backward", rc, ce)};
+  // Step 3: grad_input = G W^T, grad_weight = X^T G (:540-563).
+  auto [gradInput, ierr] = Tensor::NewDeviceResult({(int)batch, (int)in});
+  if (ierr) return {{}, wrap("failed to compute input gradient", ierr)};
+  auto [gradWeight, werr] = Tensor::NewDeviceResult({(int)in, (int)out});
+  if (werr) return {{}, wrap("failed to compute weight gradient", werr)};
+  if (Error e = gemm_f32(false, true, batch, in, out, (const float *)g.p, dptr(weight), dptr(*gradInput),
+                         "input gradient"))
+    return {{}, e};
+  if (Error e = gemm_f32(true, false, in, out, batch, dptr(input), (const float *)g.p, dptr(*gradWeight),
+                         "weight gradient"))
+    return {{}, e};
+  std::vector<TensorPtr> results{gradInput, gradWeight};
+  if (gradBias) results.push_back(gradBias);
+  return {results, {}};
+}
+
+Result<std::vector<TensorPtr>> MatMulBackward(Tensor &gradOutput, Tensor &A, Tensor &B) {
+  if (A.Shape.size() != 2 || B.Shape.size() != 2 || gradOutput.Shape.size() != 2 || A.Shape[1] != B.Shape[0] ||
+      gradOutput.Shape[0] != A.Shape[0] || gradOutput.Shape[1] != B.Shape[1])
+    return {{}, Errorf("insufficient or mismatched tensors for matmul backward")};
+  const long M = A.Shape[0], K = A.Shape[1], N = B.Shape[1];
+  if (Error e = gradOutput.EnsureGPU()) return {{}, e};
+  if (Error e = A.EnsureGPU()) return {{}, e};
+  if (Error e = B.EnsureGPU()) return {{}, e};
+  auto [gradA, aerr] = Tensor::NewDeviceResult({(int)M, (int)K});
+  if (aerr) return {{}, wrap("failed to compute gradient for first input", aerr)};
+  auto [gradB, berr] = Tensor::NewDeviceResult({(int)K, (int)N});
+  if (berr) return {{}, wrap("failed to compute gradient for second input", berr)};
+  if (Error e = gemm_f32(false, true, M, K, N, dptr(gradOutput), dptr(B), dptr(*gradA),
+                         "gradient for first input"))
+    return {{}, e};
+  if (Error e = gemm_f32(true, false, K, N, M, dptr(A), dptr(gradOutput), dptr(*gradB), "gradient for second input"))
+    return {{}, e};
+  return {{gradA, gradB}, {}};
+}
+
 // ------------------------------------------------------------------ mixed precision
 // Float32ToFloatMP16 (mixed-precision.go:106-151): truncation toward zero, fp32
 // subnormals to signed zero, overflow to infinity, NaN keeps the top mantissa bits.

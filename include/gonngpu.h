@@ -165,6 +165,20 @@ int gn_gemm(int dtype, int transA, int transB, long M, long N, long K, float alp
 int gn_cast_f32_f16(const float *in, uint16_t *out, size_t n, int round_mode, void *stream, CError *err);
 int gn_cast_f16_f32(const uint16_t *in, float *out, size_t n, void *stream, CError *err);
 
+/* Backward of an element-wise activation applied to a [rows, cols] fp32 pre-activation:
+ *   grad_in = (grad_out * act'(pre)) * scale,   grad_bias[j] = sum_i grad_in[i, j]
+ * act'(x) is the derivative with respect to the activation's input x, evaluated at pre
+ * (codes and formulas as the gn_gemm epilogue; GN_ACT_NONE gives 1). scale carries the
+ * dropout factor 1/(1-p) of FusedLinearActivation.Backward (gpu/matrix/fused-operations.go:
+ * 528-537; 1 for none). This is steps 1, 2 and 4 of that function (:486-575): the ReLU mask
+ * (:491-500), LeakyReLU/Sigmoid/Tanh/GELU backward (:501-520) and the bias gradient
+ * ReduceSum(grad, axis 0) (:566-572); step 3 is two gn_gemm calls (NT for grad_input,
+ * TN for grad_weight). grad_bias may be NULL; grad_in may alias grad_out. The column sums
+ * are added in a fixed order (deterministic). Codes: -1 invalid argument, -3 scratch
+ * allocation, -6 launch error. */
+int gn_activation_backward(const float *grad_out, const float *pre, long rows, long cols, int act, float alpha,
+                           float scale, float *grad_in, float *grad_bias, void *stream, CError *err);
+
 /* out[cols,rows] = in[rows,cols]^T, fp32, LDS-tiled. */
 int gn_transpose_f32(const float *in, long rows, long cols, float *out, void *stream, CError *err);
 

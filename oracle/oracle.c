@@ -355,6 +355,32 @@ float orc_act_f32(int code, float alpha, float x) {
   }
 }
 
+double orc_act_grad_f64(int code, double alpha, double x) {
+  switch (code) {
+    case -1: return 1.0;
+    case 0: return x > 0.0 ? 1.0 : 0.0;
+    case 1: { double s = 1.0 / (1.0 + exp(-clampd(x, -88.0, 88.0))); return s * (1.0 - s); }
+    case 2: { double t = tanh(x); return 1.0 - t * t; }
+    case 4: return x > 0.0 ? 1.0 : alpha;
+    case 5: return x > 0.0 ? 1.0 : alpha * exp(x < -88.0 ? -88.0 : x);
+    case 6: {
+      double c = clampd(x, -88.0, 88.0), s = 1.0 / (1.0 + exp(-c));
+      return s + c * s * (1.0 - s);
+    }
+    case 7: {
+      const double k = 0.7978845608028654, a3 = 0.044715;
+      double t = tanh(clampd(k * (x + a3 * x * x * x), -88.0, 88.0));
+      return 0.5 * (1.0 + t) + 0.5 * x * (1.0 - t * t) * k * (1.0 + 3.0 * a3 * x * x);
+    }
+    default: return NAN;
+  }
+}
+
+void orc_act_backward_f64(int code, double alpha, double scale, const float *dy, const float *pre, long n,
+                          double *g) {
+  for (long i = 0; i < n; ++i) g[i] = (double)dy[i] * orc_act_grad_f64(code, alpha, (double)pre[i]) * scale;
+}
+
 void orc_linear_f64(long batch, long in, long out, const float *X, const float *W, int w_out_in,
                     const float *bias, int act, double alpha, double *Y, int threads) {
   /* op(B)[k][j] = W(i=k, o=j): reference layout W[in,out] is transB=0 with ldb=out;

@@ -106,6 +106,23 @@ float orc_act_f32(int code, float alpha, float x);
 void orc_linear_f64(long batch, long in, long out, const float *X, const float *W, int w_out_in,
                     const float *bias, int act, double alpha, double *Y, int threads);
 
+/* d act(x)/dx at x, float64, for the codes above (-1 gives 1). The derivatives of the
+ * formulas of orc_act_f64: ReLU [x>0]; Sigmoid s(1-s); Tanh 1-t^2; LeakyReLU x>0 ? 1 : a;
+ * ELU x>0 ? 1 : a*e^x; Swish s + c*s*(1-s) at c = clamp(x); GELU
+ * 0.5(1+t) + 0.5x(1-t^2)*sqrt(2/pi)(1+3*0.044715x^2), t = tanh(clamped inner) (the
+ * derivative expression of metal_bridge_activation.m:689-697 at the input x).
+ * The reference's FusedLinearActivation.Backward (fused-operations.go:486-523) hands
+ * the PRE-activation to helpers whose formulas expect the activation OUTPUT
+ * (metal_bridge_activation.m:131-134, :192-195, :667-698); for ReLU and LeakyReLU the
+ * two agree, for Sigmoid, Tanh and GELU this restatement follows the mathematics
+ * (derivative at the input), which the build implements. Pins: central finite
+ * differences of orc_act_f64 (tests/test_oracle.py) and closed forms (GELU'(0) = 1/2,
+ * sigmoid'(0) = 1/4, tanh'(0) = 1, Swish'(0) = 1/2). */
+double orc_act_grad_f64(int code, double alpha, double x);
+/* g[i] = dy[i] * orc_act_grad_f64(code, alpha, pre[i]) * scale, i < n. */
+void orc_act_backward_f64(int code, double alpha, double scale, const float *dy, const float *pre, long n,
+                          double *g);
+
 /* ---- transpose ----------------------------------------------------------- */
 /* out[j,i] = in[i,j]; restates metal_bridge_matrix.m:162-166. */
 void orc_transpose_f32(long rows, long cols, const float *in, float *out);

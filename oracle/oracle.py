@@ -57,6 +57,8 @@ def lib():
         "orc_spmv_csr_f64": (None, [_L, _i32p, _i32p, _f32p, _f32p, _f64p]),
         "orc_act_f64": (ctypes.c_double, [ctypes.c_int, ctypes.c_double, ctypes.c_double]),
         "orc_act_f32": (ctypes.c_float, [ctypes.c_int, ctypes.c_float, ctypes.c_float]),
+        "orc_act_grad_f64": (ctypes.c_double, [ctypes.c_int, ctypes.c_double, ctypes.c_double]),
+        "orc_act_backward_f64": (None, [ctypes.c_int, ctypes.c_double, ctypes.c_double, _f32p, _f32p, _L, _f64p]),
         "orc_linear_f64": (None, [_L, _L, _L, _f32p, _f32p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
                                   ctypes.c_double, _f64p, ctypes.c_int]),
         "orc_transpose_f32": (None, [_L, _L, _f32p, _f32p]),
@@ -235,6 +237,33 @@ def random_csr(M, K, mean_row, seed, stream=7, distinct=True):
 def act_f64(code, x, alpha=0.0):
     f = lib().orc_act_f64
     return np.array([f(code, alpha, float(v)) for v in np.asarray(x, dtype=np.float64).reshape(-1)]).reshape(np.shape(x))
+
+
+def act_grad_f64(code, x, alpha=0.0):
+    """d act / dx at x (orc_act_grad_f64), element-wise, float64."""
+    f = lib().orc_act_grad_f64
+    return np.array([f(code, alpha, float(v)) for v in np.asarray(x, dtype=np.float64).reshape(-1)]).reshape(np.shape(x))
+
+
+def act_backward_f64(code, dy, pre, alpha=0.0, scale=1.0):
+    """dy * act'(pre) * scale in float64 (orc_act_backward_f64)."""
+    dy = np.ascontiguousarray(dy, dtype=np.float32)
+    pre = np.ascontiguousarray(pre, dtype=np.float32)
+    g = np.empty(pre.shape, dtype=np.float64)
+    lib().orc_act_backward_f64(code, alpha, scale, dy.reshape(-1), pre.reshape(-1), pre.size, g.reshape(-1))
+    return g
+
+
+def linear_backward_f64(X, W, pre, dY, act, alpha=0.0, scale=1.0, act_applied=True):
+    """Backward of Y = act(X W + b), W [in, out] (FusedLinearActivation.Backward,
+    gpu/matrix/fused-operations.go:467-578): returns (dX = G W^T, dW = X^T G,
+    db = column sums of G) with G = dY * act'(pre) * scale (G = dY * scale when the
+    activation backward is skipped)."""
+    G = act_backward_f64(act if act_applied else -1, dY, pre, alpha, scale)
+    G32 = G.astype(np.float64)
+    dX = G32 @ np.asarray(W, dtype=np.float64).T
+    dW = np.asarray(X, dtype=np.float64).T @ G32
+    return dX, dW, G32.sum(axis=0), G
 
 
 def act_f32(code, x, alpha=0.0):

@@ -385,6 +385,82 @@ void TestFusedLinearActivation() {
   CHECK_ERR_HAS(f.Forward({X.get(), W.get()}, &cfg).err, "fused linear+activation failed (code -1)");
 }
 
+// FusedLinearActivation.Backward (fused-operations.go:467-578) against the float64
+// restatement: G = dY * act'(pre) * scale, grad_input = G W^T, grad_weight = X^T G,
+// grad_bias = column sums of G (shape [1, out]).
+void TestFusedLinearBackward() {
+  const int batch = 33, in = 50, out = 70;
+  auto X = NewTensor({batch, in}, uniform((size_t)batch * in, 21)).value;
+  auto W = NewTensor({in, out}, uniform((size_t)in * out, 22)).value;
+  auto pre = NewTensor({batch, out}, uniform((size_t)batch * out, 23, -2.0f, 2.0f)).value;
+  auto dY = NewTensor({batch, out}, uniform((size_t)batch * out, 24)).value;
+  matrix::FusedLinearActivation f;
+  for (int act : {(int)matrix::ReLU, (int)matrix::GELU, (int)matrix::Sigmoid}) {
+    matrix::FusedLinearConfig cfg;
+    cfg.Bias = true;
+    cfg.Dropout = 0.25f;
+    cfg.Activation = std::make_shared<matrix::FusedActivationConfig>();
+    cfg.Activation->ActivationType = (matrix::ActivationType)act;
+    auto [grads, err] = f.Backward(*dY, {X.get(), W.get(), pre.get()}, &cfg);
+    CHECK_NOERR(err);
+    CHECK(grads.size() == 3);
+    if (grads.size() != 3) return;
+    std::vector<double> G((size_t)batch * out), dX((size_t)batch * in), dW((size_t)in * out), db(out, 0.0);
+    orc_act_backward_f64(act, 0.0, 1.0 / 0.75, dY->Data.data(), pre->Data.data(), (long)G.size(), G.data());
+    for (int i = 0; i < batch; ++i)
+      for (int k = 0; k < in; ++k) {
+        double s = 0;
+        for (int o = 0; o < out; ++o) s += G[(size_t)i * out + o] * (double)W->Data[(size_t)k * out + o];
+        dX[(size_t)i * in + k] = s;
+      }
+    for (int k = 0; k < in; ++k)
+      for (int o = 0; o < out; ++o) {
+        double s = 0;
+        for (int i = 0; i < batch; ++i) s += (double)X->Data[(size_t)i * in + k] * G[(size_t)i * out + o];
+        dW[(size_t)k * out + o] = s;
+      }
+    for (int i = 0; i < batch; ++i)
+      for (int o = 0; o < out; ++o) db[o] += G[(size_t)i * out + o];
+    for (auto &t : grads) CHECK_NOERR(t->RetrieveCPU());
+    CHECK(grads[0]->Shape == std::vector<int>({batch, in}));
+    CHECK(grads[1]->Shape == std::vector<int>({in, out}));
+    CHECK(grads[2]->Shape == std::vector<int>({1, out}));
+    CHECK(rel(grads[0]->Data, dX) <= 1e-5);
+    CHECK(rel(grads[1]->Data, dW) <= 1e-5);
+    CHECK(rel(grads[2]->Data, db) <= 1e-5);
+  }
+  // nil activation: the gradient passes through; no bias gradient with two saved tensors
+  matrix::FusedLinearConfig plain;
+  plain.Bias = true;
+  auto [g2, e2] = f.Backward(*dY, {X.get(), W.get()}, &plain);
+  CHECK_NOERR(e2);
+  CHECK(g2.size() == 2);
+  // ReLU without the pre-activation is an error
+  matrix::FusedLinearConfig relu;
+  relu.Activation = std::make_shared<matrix::FusedActivationConfig>();
+  CHECK_ERR_HAS(f.Backward(*dY, {X.get(), W.get()}, &relu).err, "pre-activation tensor");
+  CHECK_ERR_HAS(f.Backward(*dY, {X.get()}, &relu).err, "insufficient saved tensors");
+}
+
+// matmulBackward (gradient.go:601-637): grad_A = dC B^T, grad_B = A^T dC.
+void TestMatMulBackward() {
+  const int M = 37, K = 45, N = 29;
+  auto A = NewTensor({M, K}, uniform((size_t)M * K, 31)).value;
+  auto B = NewTensor({K, N}, uniform((size_t)K * N, 32)).value;
+  auto dC = NewTensor({M, N}, uniform((size_t)M * N, 33)).value;
+  auto [g, err] = matrix::MatMulBackward(*dC, *A, *B);
+  CHECK_NOERR(err);
+  CHECK(g.size() == 2);
+  if (g.size() != 2) return;
+  std::vector<double> gA((size_t)M * K), gB((size_t)K * N);
+  orc_gemm_f64(0, 1, M, K, N, 1.0, dC->Data.data(), N, B->Data.data(), N, 0.0, gA.data(), K, 8);
+  orc_gemm_f64(1, 0, K, N, M, 1.0, A->Data.data(), K, dC->Data.data(), N, 0.0, gB.data(), N, 8);
+  for (auto &t : g) CHECK_NOERR(t->RetrieveCPU());
+  CHECK(rel(g[0]->Data, gA) <= 1e-5);
+  CHECK(rel(g[1]->Data, gB) <= 1e-5);
+  CHECK_ERR_HAS(matrix::MatMulBackward(*dC, *B, *A).err, "matmul backward");
+}
+
 void TestForwardFloat16() {
   const int M = 64, K = 200, N = 48;
   auto X = NewTensor({M, K}, uniform((size_t)M * K, 16)).value;
@@ -510,6 +586,8 @@ int main(int argc, char **argv) {
       {"TestOptimizedGEMMAndBatch", TestOptimizedGEMMAndBatch, true},
       {"TestSparseMatMulAndMatVec", TestSparseMatMulAndMatVec, true},
       {"TestFusedLinearActivation", TestFusedLinearActivation, true},
+      {"TestFusedLinearBackward", TestFusedLinearBackward, true},
+      {"TestMatMulBackward", TestMatMulBackward, true},
       {"TestForwardFloat16", TestForwardFloat16, true},
       {"TestLinearLayer", TestLinearLayer, true},
       {"TestGPUDenseAndGPUMatMul", TestGPUDenseAndGPUMatMul, true},

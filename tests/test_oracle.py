@@ -316,3 +316,68 @@ def test_rel_frob():
     R = np.array([3.0, 4.0])
     assert O.rel_frob(np.array([3.0, 4.0], np.float32), R) == 0.0
     assert O.rel_frob(np.array([3.0, 4.5], np.float32), R) == pytest.approx(0.1)
+
+
+# ------------------------------------------------------------------ activation / linear backward
+GRAD_CODES = [-1, 0, 1, 2, 4, 5, 6, 7]
+
+
+@pytest.mark.parametrize("code", GRAD_CODES)
+def test_act_grad_matches_finite_differences(code):
+    """orc_act_grad_f64 against central differences of the forward restatement
+    orc_act_f64 (an independent check: a dropped term or wrong sign fails)."""
+    rng = np.random.default_rng(71 + code)
+    x = rng.uniform(-4, 4, 200)
+    x = x[np.abs(x) > 1e-2]  # away from the ReLU / LeakyReLU / ELU kink at 0
+    h = 1e-6
+    fd = (O.act_f64(code, x + h, 0.1) - O.act_f64(code, x - h, 0.1)) / (2 * h)
+    g = O.act_grad_f64(code, x, 0.1)
+    np.testing.assert_allclose(g, fd, rtol=1e-6, atol=1e-8)
+
+
+def test_act_grad_closed_forms():
+    assert O.act_grad_f64(7, 0.0) == 0.5     # GELU'(0)
+    assert O.act_grad_f64(1, 0.0) == 0.25    # sigmoid'(0)
+    assert O.act_grad_f64(2, 0.0) == 1.0     # tanh'(0)
+    assert O.act_grad_f64(6, 0.0) == 0.5     # swish'(0)
+    assert O.act_grad_f64(0, 2.0) == 1.0 and O.act_grad_f64(0, -2.0) == 0.0
+    assert O.act_grad_f64(4, -2.0, 0.2) == 0.2
+    assert abs(O.act_grad_f64(5, -1.0, 0.5) - 0.5 * np.exp(-1.0)) < 1e-15
+    assert abs(O.act_grad_f64(7, 50.0) - 1.0) < 1e-12 and abs(O.act_grad_f64(7, -50.0)) < 1e-12
+
+
+@pytest.mark.parametrize("code", [0, 1, 2, 4, 7])
+def test_linear_backward_matches_finite_differences(code):
+    """(dX, dW, db) of L = sum(G * act(X W + b)) by central differences, W [in, out]:
+    pins the transposes and the bias reduction of the backward restatement."""
+    rng = np.random.default_rng(91 + code)
+    B_, I_, O_ = 3, 4, 5
+    X = rng.standard_normal((B_, I_))
+    W = rng.standard_normal((I_, O_))
+    b = rng.standard_normal(O_)
+    Gout = rng.standard_normal((B_, O_))
+
+    def loss(X_, W_, b_):
+        return float((Gout * O.act_f64(code, X_ @ W_ + b_, 0.1)).sum())
+
+    pre = (X @ W + b)
+    # the restatement works on fp32 storage: feed values exactly representable in fp32
+    X32, W32, pre32, G32 = (a.astype(np.float32) for a in (X, W, pre, Gout))
+    dX, dW, db, _ = O.linear_backward_f64(X32, W32, pre32, G32, code, alpha=0.1)
+    h = 1e-6
+
+    def fd(arr, idx, which):
+        a_p, a_m = arr.copy(), arr.copy()
+        a_p[idx] += h
+        a_m[idx] -= h
+        args_p = {"X": (a_p, W, b), "W": (X, a_p, b), "b": (X, W, a_p)}[which]
+        args_m = {"X": (a_m, W, b), "W": (X, a_m, b), "b": (X, W, a_m)}[which]
+        return (loss(*args_p) - loss(*args_m)) / (2 * h)
+
+    fdX = np.array([[fd(X, (i, j), "X") for j in range(I_)] for i in range(B_)])
+    fdW = np.array([[fd(W, (i, j), "W") for j in range(O_)] for i in range(I_)])
+    fdb = np.array([fd(b, (j,), "b") for j in range(O_)])
+    # tolerance covers the fp32 rounding of the restatement's inputs
+    np.testing.assert_allclose(dX, fdX, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(dW, fdW, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(db, fdb, rtol=1e-5, atol=1e-5)
