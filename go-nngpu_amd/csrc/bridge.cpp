@@ -3,6 +3,7 @@
 // (internal/cgo/metal_bridge*.m); Part 2 is the device-pointer API.
 #include <cstdlib>
 #include <cstring>
+#include <vector>
 
 #include "common.h"
 
@@ -52,6 +53,50 @@ int with_csr(const int *rowptr, long rows, const int *cols, long nnz, hipStream_
   if (flags[0]) return set_error(err, -3, "malformed CSR: row pointers are not monotone within [0, nnz]");
   if (flags[1]) return set_error(err, -3, "malformed CSR: column index outside [0, cols)");
   return 0;
+}
+
+// Device copy of a host array (n elements of T), released on scope exit.
+template <typename T>
+int upload_array(Scratch &dst, const T *src, long n, hipStream_t s, CError *err) {
+  if (n <= 0) return 0;
+  dst.p = gn::dev_alloc(sizeof(T) * (size_t)n, err);
+  if (!dst.p) return -3;
+  return gn::upload(dst.p, src, sizeof(T) * (size_t)n, s, err);
+}
+
+int alloc_scratch(Scratch &dst, size_t bytes, CError *err) {
+  if (bytes == 0) return 0;
+  dst.p = gn::dev_alloc(bytes, err);
+  return dst.p ? 0 : -3;
+}
+
+// Reads back the kernels' validation flags (after everything on s has run).
+int check_flags(const Scratch &flags, hipStream_t s, CError *err, const char *ptrs_msg, const char *index_msg) {
+  int f[2] = {0, 0};
+  if (int rc = gn::download(f, flags.p, sizeof(f), s, err)) return rc;
+  if (f[0]) return set_error(err, -3, "%s", ptrs_msg);
+  if (f[1]) return set_error(err, -3, "%s", index_msg);
+  return 0;
+}
+
+// Exclusive prefix sum of per-row counts on the host; returns the total.
+long exclusive_scan(std::vector<long> &v) {
+  long run = 0;
+  for (long &x : v) {
+    const long c = x;
+    x = run;
+    run += c;
+  }
+  return run;
+}
+
+// Copies a device COO result (n entries) into the caller's host arrays.
+int download_coo(const Scratch &ri, const Scratch &ci, const Scratch &vv, long n, int *rows, int *cols, float *vals,
+                 hipStream_t s, CError *err) {
+  if (n <= 0) return 0;
+  if (int rc = gn::download(rows, ri.p, sizeof(int) * (size_t)n, s, err)) return rc;
+  if (int rc = gn::download(cols, ci.p, sizeof(int) * (size_t)n, s, err)) return rc;
+  return gn::download(vals, vv.p, sizeof(float) * (size_t)n, s, err);
 }
 
 }  // namespace
@@ -250,6 +295,248 @@ int perform_sparse_matvec(GPUPtr aValuesPtr, int *aRowPtr, long aRowPtrLen, int 
 }
 
 void free_c_error_message(char *message) { free(message); }
+
+// ---------------------------------------------------------------- remaining sparse entries
+// perform_sparse_sparse_matmul (metal_bridge.h:169-176): CSR A x CSC B -> dense.
+int perform_sparse_sparse_matmul(GPUPtr aValuesPtr, int *aRowPtr, long aRowPtrLen, int *aColIndices,
+                                 long aColIndicesLen, long aRows, long aCols, long aNNZ, GPUPtr bValuesPtr,
+                                 int *bColPtr, long bColPtrLen, int *bRowIndices, long bRowIndicesLen, long bRows,
+                                 long bCols, long bNNZ, GPUPtr resultMatrixPtr, long resultRows, long resultCols,
+                                 DevicePtr mtlDevicePtr, CError *err) {
+  (void)mtlDevicePtr;
+  gn::Context *ctx = gn::context(err);
+  if (!ctx) return -1;
+  Buffer *av = aValuesPtr ? gn::as_buffer(aValuesPtr) : nullptr;
+  Buffer *bv = bValuesPtr ? gn::as_buffer(bValuesPtr) : nullptr;
+  Buffer *c = gn::as_buffer(resultMatrixPtr);
+  if (!c || (aNNZ > 0 && !av) || (aValuesPtr && !av) || (bNNZ > 0 && !bv) || (bValuesPtr && !bv))
+    return set_error(err, -1, "Invalid buffer pointers for sparse-sparse multiplication.");
+  if (aRows < 0 || aCols < 0 || aNNZ < 0 || bRows < 0 || bCols < 0 || bNNZ < 0 || aRowPtrLen != aRows + 1 ||
+      bColPtrLen != bCols + 1 || aColIndicesLen < aNNZ || bRowIndicesLen < bNNZ || aCols != bRows ||
+      resultRows != aRows || resultCols != bCols || !aRowPtr || !bColPtr || (aNNZ > 0 && !aColIndices) ||
+      (bNNZ > 0 && !bRowIndices))
+    return set_error(err, -2, "Incompatible dimensions for sparse-sparse multiplication.");
+  if (!fits(c, resultRows, resultCols, 4) || (av && !fits(av, 1, aNNZ, 4)) || (bv && !fits(bv, 1, bNNZ, 4)))
+    return set_error(err, -2, "Buffer smaller than the matrix it describes.");
+  const hipStream_t s = ctx->stream;
+  Scratch arp, acol, bcp, brow, flags;
+  int rc = upload_array(arp, aRowPtr, aRows + 1, s, err);
+  if (!rc) rc = upload_array(acol, aColIndices, aNNZ, s, err);
+  if (!rc) rc = upload_array(bcp, bColPtr, bCols + 1, s, err);
+  if (!rc) rc = upload_array(brow, bRowIndices, bNNZ, s, err);
+  if (!rc) rc = alloc_scratch(flags, 2 * sizeof(int), err);
+  if (!rc) rc = gn::launch_zero_i32(static_cast<int *>(flags.p), 2, s, err);
+  if (!rc)
+    rc = gn::launch_spgemm_csr_csc(aRows, bCols, aNNZ, bNNZ, static_cast<const int32_t *>(arp.p),
+                                   static_cast<const int32_t *>(acol.p),
+                                   av ? static_cast<const float *>(av->dptr) : nullptr,
+                                   static_cast<const int32_t *>(bcp.p), static_cast<const int32_t *>(brow.p),
+                                   bv ? static_cast<const float *>(bv->dptr) : nullptr, static_cast<float *>(c->dptr),
+                                   resultCols, static_cast<int *>(flags.p), s, err);
+  if (rc) return rc;
+  return check_flags(flags, s, err, "malformed sparse operand: row/column pointers are not monotone within [0, nnz]",
+                     "malformed sparse operand");
+}
+
+// perform_dense_sparse_matmul (metal_bridge.h:190-197): dense A x CSC B -> dense. Runs
+// as C^T = B^T A^T: B's CSC arrays are the CSR arrays of B^T, so the CSR SpMM kernel
+// computes C^T from A^T, accumulating each output over B's column entries in order
+// (the reference's order, metal_bridge_sparse.m:163-176), and C is transposed back.
+int perform_dense_sparse_matmul(GPUPtr aMatrixPtr, long aRows, long aCols, GPUPtr bValuesPtr, int *bColPtr,
+                                long bColPtrLen, int *bRowIndices, long bRowIndicesLen, long bRows, long bCols,
+                                long bNNZ, GPUPtr resultMatrixPtr, long resultRows, long resultCols,
+                                DevicePtr mtlDevicePtr, CError *err) {
+  (void)mtlDevicePtr;
+  gn::Context *ctx = gn::context(err);
+  if (!ctx) return -1;
+  Buffer *a = gn::as_buffer(aMatrixPtr), *c = gn::as_buffer(resultMatrixPtr);
+  Buffer *bv = bValuesPtr ? gn::as_buffer(bValuesPtr) : nullptr;
+  if (!a || !c || (bNNZ > 0 && !bv) || (bValuesPtr && !bv))
+    return set_error(err, -1, "Invalid buffer pointers for dense-sparse multiplication.");
+  if (aRows < 0 || aCols < 0 || bRows < 0 || bCols < 0 || bNNZ < 0 || bColPtrLen != bCols + 1 ||
+      bRowIndicesLen < bNNZ || aCols != bRows || resultRows != aRows || resultCols != bCols || !bColPtr ||
+      (bNNZ > 0 && !bRowIndices))
+    return set_error(err, -2, "Incompatible dimensions for dense-sparse multiplication.");
+  if (!fits(a, aRows, aCols, 4) || !fits(c, resultRows, resultCols, 4) || (bv && !fits(bv, 1, bNNZ, 4)))
+    return set_error(err, -2, "Buffer smaller than the matrix it describes.");
+  if (aRows == 0 || bCols == 0) return 0;
+  const hipStream_t s = ctx->stream;
+  Scratch at, ct;
+  int rc = alloc_scratch(at, sizeof(float) * (size_t)aRows * (size_t)std::max(aCols, 1L), err);
+  if (!rc) rc = alloc_scratch(ct, sizeof(float) * (size_t)aRows * (size_t)bCols, err);
+  if (!rc && aCols > 0)
+    rc = gn::launch_transpose_f32(static_cast<const float *>(a->dptr), aRows, aCols, static_cast<float *>(at.p), s,
+                                  err);
+  if (rc) return rc;
+  const float *vals = bv ? static_cast<const float *>(bv->dptr) : nullptr;
+  rc = with_csr(bColPtr, bCols, bRowIndices, bNNZ, s, err,
+                [&](const int32_t *cp, const int32_t *rows, int *flags) -> int {
+                  int r = gn::launch_spmm(bCols, aRows, aCols, bNNZ, cp, rows, vals, static_cast<const float *>(at.p),
+                                          aRows, static_cast<float *>(ct.p), aRows, flags, s, err);
+                  if (!r) r = gn::launch_transpose_f32(static_cast<const float *>(ct.p), bCols, aRows,
+                                                       static_cast<float *>(c->dptr), s, err);
+                  return r ? (r == -1 ? -2 : r) : sync(s, err, -6);
+                });
+  return rc;
+}
+
+// perform_sparse_add (metal_bridge.h:200-209): CSR + CSR -> COO in host arrays.
+int perform_sparse_add(GPUPtr aValuesPtr, int *aRowPtr, long aRowPtrLen, int *aColIndices, long aColIndicesLen,
+                       long aRows, long aCols, long aNNZ, GPUPtr bValuesPtr, int *bRowPtr, long bRowPtrLen,
+                       int *bColIndices, long bColIndicesLen, long bRows, long bCols, long bNNZ,
+                       int *resultRowIndices, int *resultColIndices, float *resultValues, long *actualNNZ,
+                       long maxResultNNZ, DevicePtr mtlDevicePtr, CError *err) {
+  (void)mtlDevicePtr;
+  if (aRows != bRows || aCols != bCols)  // metal_bridge_sparse.m:196-199
+    return set_error(err, -1, "Matrix dimensions must match for addition.");
+  gn::Context *ctx = gn::context(err);
+  if (!ctx) return -1;
+  Buffer *av = aValuesPtr ? gn::as_buffer(aValuesPtr) : nullptr;
+  Buffer *bv = bValuesPtr ? gn::as_buffer(bValuesPtr) : nullptr;
+  if ((aNNZ > 0 && !av) || (aValuesPtr && !av) || (bNNZ > 0 && !bv) || (bValuesPtr && !bv))
+    return set_error(err, -1, "Invalid buffer pointers for sparse addition.");
+  if (aRows < 0 || aCols < 0 || aNNZ < 0 || bNNZ < 0 || aRowPtrLen != aRows + 1 || bRowPtrLen != bRows + 1 ||
+      aColIndicesLen < aNNZ || bColIndicesLen < bNNZ || !aRowPtr || !bRowPtr || (aNNZ > 0 && !aColIndices) ||
+      (bNNZ > 0 && !bColIndices) || !actualNNZ || maxResultNNZ < 0 ||
+      (maxResultNNZ > 0 && (!resultRowIndices || !resultColIndices || !resultValues)))
+    return set_error(err, -1, "Invalid arguments for sparse addition.");
+  if ((av && !fits(av, 1, aNNZ, 4)) || (bv && !fits(bv, 1, bNNZ, 4)))
+    return set_error(err, -1, "Buffer smaller than the values it describes.");
+  *actualNNZ = 0;
+  if (aRows == 0) return 0;
+  const hipStream_t s = ctx->stream;
+  Scratch arp, acol, brp, bcol, flags, counts, offs, ri, ci, vv;
+  int rc = upload_array(arp, aRowPtr, aRows + 1, s, err);
+  if (!rc) rc = upload_array(acol, aColIndices, aNNZ, s, err);
+  if (!rc) rc = upload_array(brp, bRowPtr, bRows + 1, s, err);
+  if (!rc) rc = upload_array(bcol, bColIndices, bNNZ, s, err);
+  if (!rc) rc = alloc_scratch(flags, 2 * sizeof(int), err);
+  if (!rc) rc = alloc_scratch(counts, sizeof(long) * (size_t)aRows, err);
+  if (!rc) rc = gn::launch_zero_i32(static_cast<int *>(flags.p), 2, s, err);
+  const float *a_vals = av ? static_cast<const float *>(av->dptr) : nullptr;
+  const float *b_vals = bv ? static_cast<const float *>(bv->dptr) : nullptr;
+  auto pass = [&](bool write) {
+    return gn::launch_spadd(write, aRows, aCols, aNNZ, bNNZ, static_cast<const int32_t *>(arp.p),
+                            static_cast<const int32_t *>(acol.p), a_vals, static_cast<const int32_t *>(brp.p),
+                            static_cast<const int32_t *>(bcol.p), b_vals, static_cast<long *>(counts.p),
+                            static_cast<const long *>(offs.p), static_cast<int32_t *>(ri.p),
+                            static_cast<int32_t *>(ci.p), static_cast<float *>(vv.p), static_cast<int *>(flags.p), s,
+                            err);
+  };
+  if (!rc) rc = pass(false);
+  if (rc) return rc;
+  if (int f = check_flags(flags, s, err, "malformed CSR: row pointers are not monotone within [0, nnz]",
+                          "malformed CSR: column index outside [0, cols)"))
+    return f;
+  std::vector<long> off((size_t)aRows);
+  if (int r = gn::download(off.data(), counts.p, sizeof(long) * (size_t)aRows, s, err)) return r;
+  const long total = exclusive_scan(off);
+  if (total > maxResultNNZ) return set_error(err, -2, "Result matrix exceeds maximum allocated space.");
+  if (total > 0) {
+    rc = upload_array(offs, off.data(), aRows, s, err);
+    if (!rc) rc = alloc_scratch(ri, sizeof(int32_t) * (size_t)total, err);
+    if (!rc) rc = alloc_scratch(ci, sizeof(int32_t) * (size_t)total, err);
+    if (!rc) rc = alloc_scratch(vv, sizeof(float) * (size_t)total, err);
+    if (!rc) rc = pass(true);
+    if (!rc) rc = download_coo(ri, ci, vv, total, resultRowIndices, resultColIndices, resultValues, s, err);
+    if (rc) return rc;
+  }
+  *actualNNZ = total;
+  return 0;
+}
+
+// perform_sparse_scalar_multiply (metal_bridge.h:212-218): values *= scalar in place.
+int perform_sparse_scalar_multiply(GPUPtr valuesPtr, int *rowPtr, long rowPtrLen, int *colIndices,
+                                   long colIndicesLen, long rows, long cols, long nnz, float scalar,
+                                   DevicePtr mtlDevicePtr, CError *err) {
+  (void)mtlDevicePtr;
+  (void)rowPtr;
+  (void)rowPtrLen;
+  (void)colIndices;
+  (void)colIndicesLen;
+  (void)rows;
+  (void)cols;
+  gn::Context *ctx = gn::context(err);
+  if (!ctx) return -1;
+  Buffer *v = valuesPtr ? gn::as_buffer(valuesPtr) : nullptr;
+  if (nnz < 0 || (nnz > 0 && !v) || (valuesPtr && !v))
+    return set_error(err, -1, "Invalid buffer pointer for sparse scalar multiplication.");
+  if (v && !fits(v, 1, nnz, 4)) return set_error(err, -1, "Buffer smaller than the values it describes.");
+  if (nnz == 0) return 0;
+  int rc = gn::launch_scale_f32(static_cast<float *>(v->dptr), nnz, scalar, ctx->stream, err);
+  return rc ? rc : sync(ctx->stream, err, -6);
+}
+
+// perform_sparse_to_dense (metal_bridge.h:231-236): CSR -> dense (later duplicates win).
+int perform_sparse_to_dense(GPUPtr valuesPtr, int *rowPtr, long rowPtrLen, int *colIndices, long colIndicesLen,
+                            long rows, long cols, long nnz, GPUPtr denseMatrixPtr, long denseRows, long denseCols,
+                            DevicePtr mtlDevicePtr, CError *err) {
+  (void)mtlDevicePtr;
+  if (rows != denseRows || cols != denseCols)  // metal_bridge_sparse.m:353-356
+    return set_error(err, -1, "Dimension mismatch in sparse to dense conversion.");
+  gn::Context *ctx = gn::context(err);
+  if (!ctx) return -1;
+  Buffer *v = valuesPtr ? gn::as_buffer(valuesPtr) : nullptr;
+  Buffer *d = gn::as_buffer(denseMatrixPtr);
+  if (!d || (nnz > 0 && !v) || (valuesPtr && !v))
+    return set_error(err, -1, "Invalid buffer pointers for sparse to dense conversion.");
+  if (rows < 0 || cols < 0 || nnz < 0 || rowPtrLen != rows + 1 || colIndicesLen < nnz || !rowPtr ||
+      (nnz > 0 && !colIndices))
+    return set_error(err, -1, "Incompatible CSR arrays for sparse to dense conversion.");
+  if (!fits(d, rows, cols, 4) || (v && !fits(v, 1, nnz, 4)))
+    return set_error(err, -1, "Buffer smaller than the matrix it describes.");
+  if (rows == 0 || cols == 0) return 0;
+  const float *vals = v ? static_cast<const float *>(v->dptr) : nullptr;
+  return with_csr(rowPtr, rows, colIndices, nnz, ctx->stream, err,
+                  [&](const int32_t *rp, const int32_t *col, int *flags) -> int {
+                    int rc = gn::launch_csr_to_dense(rows, cols, nnz, rp, col, vals, static_cast<float *>(d->dptr),
+                                                     flags, ctx->stream, err);
+                    return rc ? rc : sync(ctx->stream, err, -6);
+                  });
+}
+
+// perform_dense_to_sparse (metal_bridge.h:240-246): dense -> COO (|v| > threshold) in
+// host arrays, row-major order.
+int perform_dense_to_sparse(GPUPtr denseMatrixPtr, long rows, long cols, float threshold, int *rowIndices,
+                            int *colIndices, float *values, long *actualNNZ, long maxNNZ, DevicePtr mtlDevicePtr,
+                            CError *err) {
+  (void)mtlDevicePtr;
+  gn::Context *ctx = gn::context(err);
+  if (!ctx) return -1;
+  Buffer *d = gn::as_buffer(denseMatrixPtr);
+  if (!d) return set_error(err, -1, "Invalid buffer pointer for dense to sparse conversion.");
+  if (rows < 0 || cols < 0 || !actualNNZ || maxNNZ < 0 || (maxNNZ > 0 && (!rowIndices || !colIndices || !values)))
+    return set_error(err, -1, "Invalid arguments for dense to sparse conversion.");
+  if (!fits(d, rows, cols, 4)) return set_error(err, -1, "Buffer smaller than the matrix it describes.");
+  *actualNNZ = 0;
+  if (rows == 0 || cols == 0) return 0;
+  const hipStream_t s = ctx->stream;
+  const float *D = static_cast<const float *>(d->dptr);
+  Scratch counts, offs, ri, ci, vv;
+  int rc = alloc_scratch(counts, sizeof(long) * (size_t)rows, err);
+  if (!rc)
+    rc = gn::launch_dense_to_coo(false, rows, cols, D, threshold, static_cast<long *>(counts.p), nullptr, nullptr,
+                                 nullptr, nullptr, s, err);
+  if (rc) return rc;
+  std::vector<long> off((size_t)rows);
+  if (int r = gn::download(off.data(), counts.p, sizeof(long) * (size_t)rows, s, err)) return r;
+  const long total = exclusive_scan(off);
+  if (total > maxNNZ) return set_error(err, -2, "Too many non-zero elements, exceeds allocated space.");
+  if (total > 0) {
+    rc = upload_array(offs, off.data(), rows, s, err);
+    if (!rc) rc = alloc_scratch(ri, sizeof(int32_t) * (size_t)total, err);
+    if (!rc) rc = alloc_scratch(ci, sizeof(int32_t) * (size_t)total, err);
+    if (!rc) rc = alloc_scratch(vv, sizeof(float) * (size_t)total, err);
+    if (!rc)
+      rc = gn::launch_dense_to_coo(true, rows, cols, D, threshold, nullptr, static_cast<const long *>(offs.p),
+                                   static_cast<int32_t *>(ri.p), static_cast<int32_t *>(ci.p),
+                                   static_cast<float *>(vv.p), s, err);
+    if (!rc) rc = download_coo(ri, ci, vv, total, rowIndices, colIndices, values, s, err);
+    if (rc) return rc;
+  }
+  *actualNNZ = total;
+  return 0;
+}
 
 // =========================================================================== Part 2
 

@@ -93,6 +93,18 @@ int launch_fill_uniform(float *out, size_t n, uint64_t seed, uint64_t sid, float
 int launch_fill_normal(float *out, size_t n, uint64_t seed, uint64_t sid, float mean, float sd, hipStream_t s,
                        CError *err);
 int launch_zero_i32(int *p, long n, hipStream_t s, CError *err);
+// sparse_ops.hip (flags as launch_spmm: [0] bad row/column pointers, [1] index out of range)
+int launch_spgemm_csr_csc(long M, long N, long annz, long bnnz, const int32_t *arp, const int32_t *acol,
+                          const float *aval, const int32_t *bcp, const int32_t *brow, const float *bval, float *C,
+                          long ldc, int *flags, hipStream_t s, CError *err);
+int launch_spadd(bool write, long M, long N, long annz, long bnnz, const int32_t *arp, const int32_t *acol,
+                 const float *aval, const int32_t *brp, const int32_t *bcol, const float *bval, long *count,
+                 const long *out_off, int32_t *ri, int32_t *ci, float *vv, int *flags, hipStream_t s, CError *err);
+int launch_scale_f32(float *v, long n, float scalar, hipStream_t s, CError *err);
+int launch_csr_to_dense(long M, long N, long nnz, const int32_t *rp, const int32_t *col, const float *val, float *D,
+                        int *flags, hipStream_t s, CError *err);
+int launch_dense_to_coo(bool write, long M, long N, const float *D, float thr, long *count, const long *out_off,
+                        int32_t *ri, int32_t *ci, float *vv, hipStream_t s, CError *err);
 
 bool act_supported(int act);
 

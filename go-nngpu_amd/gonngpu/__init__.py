@@ -57,6 +57,14 @@ SIGNATURES = {
     "perform_fused_linear_activation": (_I, [_VP, _L, _L, _VP, _L, _VP, _I, _F, _VP, _VP, _ERR]),
     "perform_sparse_dense_matmul": (_I, [_VP, _VP, _L, _VP, _L, _L, _L, _L, _VP, _L, _L, _VP, _L, _L, _VP, _ERR]),
     "perform_sparse_matvec": (_I, [_VP, _VP, _L, _VP, _L, _L, _L, _L, _VP, _L, _VP, _L, _VP, _ERR]),
+    "perform_sparse_sparse_matmul": (_I, [_VP, _VP, _L, _VP, _L, _L, _L, _L, _VP, _VP, _L, _VP, _L, _L, _L, _L, _VP,
+                                          _L, _L, _VP, _ERR]),
+    "perform_dense_sparse_matmul": (_I, [_VP, _L, _L, _VP, _VP, _L, _VP, _L, _L, _L, _L, _VP, _L, _L, _VP, _ERR]),
+    "perform_sparse_add": (_I, [_VP, _VP, _L, _VP, _L, _L, _L, _L, _VP, _VP, _L, _VP, _L, _L, _L, _L, _VP, _VP, _VP,
+                                ctypes.POINTER(_L), _L, _VP, _ERR]),
+    "perform_sparse_scalar_multiply": (_I, [_VP, _VP, _L, _VP, _L, _L, _L, _L, _F, _VP, _ERR]),
+    "perform_sparse_to_dense": (_I, [_VP, _VP, _L, _VP, _L, _L, _L, _L, _VP, _L, _L, _VP, _ERR]),
+    "perform_dense_to_sparse": (_I, [_VP, _L, _L, _F, _VP, _VP, _VP, ctypes.POINTER(_L), _L, _VP, _ERR]),
     "free_c_error_message": (None, [_VP]),
     "gn_version": (ctypes.c_char_p, []),
     "gn_init": (_I, [_ERR]),

@@ -117,6 +117,66 @@ int perform_sparse_matvec(GPUPtr aValuesPtr, int *aRowPtr, long aRowPtrLen, int 
                           long aRows, long aCols, long aNNZ, GPUPtr xVectorPtr, long xSize, GPUPtr resultVectorPtr,
                           long resultSize, DevicePtr mtlDevicePtr, CError *err);
 
+/* metal_bridge.h:168-176. C = A*B, A in CSR (host row pointers / column indices),
+ * B in CSC (host column pointers / row indices), C dense row-major fp32
+ * (sparseSparseMatMul, sparse-matrix.go:69-131). Every output runs the reference's
+ * merge of A's row with B's column (metal_bridge_sparse.m:56-84): equal indices pair
+ * up and both advance, one fma per match; a zero sum stores +0. Either nnz may be 0.
+ * Codes: -1 NULL buffer, -2 inconsistent dimensions, -3 malformed row/column
+ * pointers, -6 execution error. */
+int perform_sparse_sparse_matmul(GPUPtr aValuesPtr, int *aRowPtr, long aRowPtrLen, int *aColIndices,
+                                 long aColIndicesLen, long aRows, long aCols, long aNNZ, GPUPtr bValuesPtr,
+                                 int *bColPtr, long bColPtrLen, int *bRowIndices, long bRowIndicesLen, long bRows,
+                                 long bCols, long bNNZ, GPUPtr resultMatrixPtr, long resultRows, long resultCols,
+                                 DevicePtr mtlDevicePtr, CError *err);
+
+/* metal_bridge.h:189-197. C = A*B, A dense row-major, B in CSC (denseSparseMatMul,
+ * sparse-matrix.go:193-250). Each output accumulates over B's column entries in
+ * order with one fma each (metal_bridge_sparse.m:163-176).
+ * Codes: -1 NULL buffer, -2 inconsistent dimensions, -3 malformed CSC (column
+ * pointers, or a row index outside [0, bRows)), -6 execution error. */
+int perform_dense_sparse_matmul(GPUPtr aMatrixPtr, long aRows, long aCols, GPUPtr bValuesPtr, int *bColPtr,
+                                long bColPtrLen, int *bRowIndices, long bRowIndicesLen, long bRows, long bCols,
+                                long bNNZ, GPUPtr resultMatrixPtr, long resultRows, long resultCols,
+                                DevicePtr mtlDevicePtr, CError *err);
+
+/* metal_bridge.h:199-209. A + B for two CSR matrices into host COO arrays
+ * (SparseAdd, sparse-matrix.go:252-320): the reference's per-row merge
+ * (metal_bridge_sparse.m:221-259); coinciding entries are added and dropped when the
+ * sum is 0, the others are kept as they are. *actualNNZ receives the entry count.
+ * Codes: -1 dimension mismatch (:196-199), NULL buffer or bad arguments, -2 more
+ * than maxResultNNZ entries (the arrays' contents are then unspecified), -3
+ * malformed CSR (including a column index outside [0, aCols)), -6 execution error. */
+int perform_sparse_add(GPUPtr aValuesPtr, int *aRowPtr, long aRowPtrLen, int *aColIndices, long aColIndicesLen,
+                       long aRows, long aCols, long aNNZ, GPUPtr bValuesPtr, int *bRowPtr, long bRowPtrLen,
+                       int *bColIndices, long bColIndicesLen, long bRows, long bCols, long bNNZ,
+                       int *resultRowIndices, int *resultColIndices, float *resultValues, long *actualNNZ,
+                       long maxResultNNZ, DevicePtr mtlDevicePtr, CError *err);
+
+/* metal_bridge.h:211-218. values[0..nnz) *= scalar in place (SparseScalarMul,
+ * sparse-matrix.go:322-364; metal_bridge_sparse.m:286-289). The index arrays are not
+ * read. Codes: -1 NULL or too small buffer, -6 execution error. */
+int perform_sparse_scalar_multiply(GPUPtr valuesPtr, int *rowPtr, long rowPtrLen, int *colIndices,
+                                   long colIndicesLen, long rows, long cols, long nnz, float scalar,
+                                   DevicePtr mtlDevicePtr, CError *err);
+
+/* metal_bridge.h:230-236. Dense = CSR (SparseToDense, sparse-matrix.go:425-473):
+ * zeros, then each row's entries in CSR order, so a later duplicate overwrites an
+ * earlier one (metal_bridge_sparse.m:366-377). Codes: -1 dimension mismatch
+ * (:353-356), NULL buffer or bad arrays, -3 malformed CSR (including a column index
+ * outside [0, cols)), -6 execution error. */
+int perform_sparse_to_dense(GPUPtr valuesPtr, int *rowPtr, long rowPtrLen, int *colIndices, long colIndicesLen,
+                            long rows, long cols, long nnz, GPUPtr denseMatrixPtr, long denseRows, long denseCols,
+                            DevicePtr mtlDevicePtr, CError *err);
+
+/* metal_bridge.h:239-246. COO of the entries with |v| > threshold, in row-major order,
+ * into host arrays (DenseToSparse, sparse-matrix.go:475-525; metal_bridge_sparse.m:
+ * 405-424; NaN is never kept). Codes: -1 NULL buffer or bad arguments, -2 more than
+ * maxNNZ entries (contents then unspecified), -6 execution error. */
+int perform_dense_to_sparse(GPUPtr denseMatrixPtr, long rows, long cols, float threshold, int *rowIndices,
+                            int *colIndices, float *values, long *actualNNZ, long maxNNZ, DevicePtr mtlDevicePtr,
+                            CError *err);
+
 /* metal_bridge.h:250. */
 void free_c_error_message(char *message);
 

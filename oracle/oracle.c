@@ -9,6 +9,7 @@
  */
 #include "oracle.h"
 
+#include <limits.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -311,6 +312,111 @@ void orc_spmv_csr_f64(long M, const int32_t *rowptr, const int32_t *col, const f
     for (long k = rowptr[i]; k < rowptr[i + 1]; ++k) s += (double)val[k] * (double)x[col[k]];
     y[i] = s;
   }
+}
+
+/* ------------------------------------------------------------------------- */
+/* remaining sparse entry points                                             */
+/* ------------------------------------------------------------------------- */
+void orc_spgemm_csr_csc_f32(long M, long N, const int32_t *arp, const int32_t *acol, const float *aval,
+                            const int32_t *bcp, const int32_t *brow, const float *bval, float *C, long ldc, int fma) {
+  for (long i = 0; i < M; ++i)
+    for (long j = 0; j < N; ++j) C[i * ldc + j] = 0.0f; /* :50 memset */
+  for (long i = 0; i < M; ++i)
+    for (long j = 0; j < N; ++j) {
+      long ai = arp[i], ae = arp[i + 1], bi = bcp[j], be = bcp[j + 1];
+      float sum = 0.0f;
+      while (ai < ae && bi < be) { /* :66-78 */
+        int ac = acol[ai], br = brow[bi];
+        if (ac == br) {
+          sum = fma ? fmaf(aval[ai], bval[bi], sum) : sum + aval[ai] * bval[bi];
+          ++ai;
+          ++bi;
+        } else if (ac < br) {
+          ++ai;
+        } else {
+          ++bi;
+        }
+      }
+      if (sum != 0.0f) C[i * ldc + j] = sum; /* :80-82 */
+    }
+}
+
+void orc_dense_csc_f32(long M, long K, long N, const float *A, long lda, const int32_t *bcp, const int32_t *brow,
+                       const float *bval, float *C, long ldc, int fma) {
+  (void)K;
+  for (long i = 0; i < M; ++i)
+    for (long j = 0; j < N; ++j) C[i * ldc + j] = 0.0f; /* :161 */
+  for (long j = 0; j < N; ++j)                          /* :164-176 */
+    for (long k = bcp[j]; k < bcp[j + 1]; ++k) {
+      const int r = brow[k];
+      const float v = bval[k];
+      for (long i = 0; i < M; ++i) {
+        float *c = C + i * ldc + j;
+        *c = fma ? fmaf(A[i * lda + r], v, *c) : *c + A[i * lda + r] * v;
+      }
+    }
+}
+
+int orc_sparse_add(long M, const int32_t *arp, const int32_t *acol, const float *aval, const int32_t *brp,
+                   const int32_t *bcol, const float *bval, int32_t *ri, int32_t *ci, float *vv, long max_nnz,
+                   long *actual) {
+  long n = 0;
+  for (long i = 0; i < M; ++i) { /* :214-259 */
+    long ai = arp[i], ae = arp[i + 1], bi = brp[i], be = brp[i + 1];
+    while (ai < ae || bi < be) {
+      if (n >= max_nnz) {
+        *actual = n;
+        return -2;
+      }
+      int ac = ai < ae ? acol[ai] : INT_MAX, bc = bi < be ? bcol[bi] : INT_MAX;
+      if (ac == bc && ac != INT_MAX) {
+        float sum = aval[ai] + bval[bi];
+        if (sum != 0.0f) {
+          ri[n] = (int32_t)i;
+          ci[n] = ac;
+          vv[n] = sum;
+          ++n;
+        }
+        ++ai;
+        ++bi;
+      } else if (ac < bc) {
+        ri[n] = (int32_t)i;
+        ci[n] = ac;
+        vv[n] = aval[ai];
+        ++n;
+        ++ai;
+      } else {
+        ri[n] = (int32_t)i;
+        ci[n] = bc;
+        vv[n] = bval[bi];
+        ++n;
+        ++bi;
+      }
+    }
+  }
+  *actual = n;
+  return 0;
+}
+
+int orc_dense_to_coo(long M, long N, const float *D, float threshold, int32_t *ri, int32_t *ci, float *vv,
+                     long max_nnz, long *actual) {
+  long n = 0;
+  for (long i = 0; i < M; ++i) /* :407-423 */
+    for (long j = 0; j < N; ++j) {
+      const float v = D[i * N + j];
+      if (fabsf(v) > threshold) {
+        if (n >= max_nnz) {
+          *actual = n;
+          return -2;
+        }
+        ri[n] = (int32_t)i;
+        ci[n] = (int32_t)j;
+        vv[n] = v;
+        ++n;
+      }
+    }
+  *actual = n;
+  return 0;
 }
 
 /* ------------------------------------------------------------------------- */

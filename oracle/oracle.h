@@ -68,8 +68,8 @@ void orc_cast_f16_f32(const uint16_t *in, float *out, size_t n);
  * Pins: numpy lexsort (stable) + bincount/cumsum. */
 int orc_coo_to_csr(long rows, long cols, long nnz, const int32_t *ri, const int32_t *ci,
                    const float *v, int32_t *rowptr, int32_t *idx, float *data);
-/* Restates SparseTensor.ToDense for CSR (tensor/sparse-tensor.go:251-258): last
- * duplicate written wins. */
+/* Restates SparseTensor.ToDense for CSR (tensor/sparse-tensor.go:251-258) and
+ * perform_sparse_to_dense (metal_bridge_sparse.m:366-377): last duplicate written wins. */
 void orc_csr_to_dense(long rows, long cols, const int32_t *rowptr, const int32_t *idx,
                       const float *data, float *out);
 
@@ -89,6 +89,34 @@ void orc_spmv_csr_f32(long M, const int32_t *rowptr, const int32_t *col, const f
                       const float *x, float *y, int fma);
 void orc_spmv_csr_f64(long M, const int32_t *rowptr, const int32_t *col, const float *val,
                       const float *x, double *y);
+
+/* ---- remaining sparse entry points ---------------------------------------- */
+/* Restates perform_sparse_sparse_matmul, metal_bridge_sparse.m:49-84: C = 0; for each
+ * (i, j) merge A's CSR row i with B's CSC column j, equal indices pair up and both
+ * advance, sum += a*b (fma=1: fmaf); store only a nonzero sum. Pins: equals the float64
+ * dense product of ToDense(A) and ToDense(B) for distinct sorted indices; brute force on
+ * tiny shapes; a hand-worked duplicate-pairing case. */
+void orc_spgemm_csr_csc_f32(long M, long N, const int32_t *arp, const int32_t *acol, const float *aval,
+                            const int32_t *bcp, const int32_t *brow, const float *bval, float *C, long ldc, int fma);
+/* Restates perform_dense_sparse_matmul, metal_bridge_sparse.m:160-176: C = 0; for each
+ * column j of the CSC B, for each entry k, for each row i: C[i,j] += A[i,row_k]*v_k
+ * (fma=1: fmaf). Pins: numpy float64 A @ ToDense(B). */
+void orc_dense_csc_f32(long M, long K, long N, const float *A, long lda, const int32_t *bcp, const int32_t *brow,
+                       const float *bval, float *C, long ldc, int fma);
+/* Restates perform_sparse_add, metal_bridge_sparse.m:212-266: per row, merge the two
+ * CSR rows by column (INT_MAX marks an exhausted row); equal columns are added and
+ * dropped when the sum is 0; the others are copied. Writes COO triplets in that order.
+ * Returns 0, or -2 (and stops) once max_nnz would be exceeded. *actual = count.
+ * Pins: ToDense(A) + ToDense(B) equals the COO result scattered; hand-worked merge cases
+ * (cancellation, one-sided entries, empty rows). */
+int orc_sparse_add(long M, const int32_t *arp, const int32_t *acol, const float *aval, const int32_t *brp,
+                   const int32_t *bcol, const float *bval, int32_t *ri, int32_t *ci, float *vv, long max_nnz,
+                   long *actual);
+/* Restates perform_dense_to_sparse, metal_bridge_sparse.m:403-424: row-major scan,
+ * keep fabsf(v) > threshold. Returns 0 or -2 past max_nnz. Pins: numpy nonzero of
+ * |D| > threshold (row-major order). */
+int orc_dense_to_coo(long M, long N, const float *D, float threshold, int32_t *ri, int32_t *ci, float *vv,
+                     long max_nnz, long *actual);
 
 /* ---- activations / fused linear ----------------------------------------- */
 /* Activation codes follow the Go ActivationType enum, gpu/matrix/activation.go:20-29:

@@ -57,6 +57,12 @@ def lib():
         "orc_spmv_csr_f64": (None, [_L, _i32p, _i32p, _f32p, _f32p, _f64p]),
         "orc_act_f64": (ctypes.c_double, [ctypes.c_int, ctypes.c_double, ctypes.c_double]),
         "orc_act_f32": (ctypes.c_float, [ctypes.c_int, ctypes.c_float, ctypes.c_float]),
+        "orc_spgemm_csr_csc_f32": (None, [_L, _L, _i32p, _i32p, _f32p, _i32p, _i32p, _f32p, _f32p, _L, ctypes.c_int]),
+        "orc_dense_csc_f32": (None, [_L, _L, _L, _f32p, _L, _i32p, _i32p, _f32p, _f32p, _L, ctypes.c_int]),
+        "orc_sparse_add": (ctypes.c_int, [_L, _i32p, _i32p, _f32p, _i32p, _i32p, _f32p, _i32p, _i32p, _f32p, _L,
+                                          ctypes.POINTER(_L)]),
+        "orc_dense_to_coo": (ctypes.c_int, [_L, _L, _f32p, ctypes.c_float, _i32p, _i32p, _f32p, _L,
+                                            ctypes.POINTER(_L)]),
         "orc_act_grad_f64": (ctypes.c_double, [ctypes.c_int, ctypes.c_double, ctypes.c_double]),
         "orc_act_backward_f64": (None, [ctypes.c_int, ctypes.c_double, ctypes.c_double, _f32p, _f32p, _L, _f64p]),
         "orc_linear_f64": (None, [_L, _L, _L, _f32p, _f32p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
@@ -183,6 +189,66 @@ def spmm_f64(rowptr, col, val, D, nthreads=None):
     lib().orc_spmm_csr_f64(M, N, np.ascontiguousarray(rowptr, np.int32), pad(col, np.int32), pad(val, np.float32),
                            D.reshape(-1), N, C.reshape(-1), N, nthreads or threads())
     return C
+
+
+def _pad(a, dt):
+    a = np.ascontiguousarray(a, dtype=dt)
+    return a if a.size else np.zeros(1, dt)
+
+
+def spgemm_csr_csc_f32(arp, acol, aval, bcp, brow, bval, use_fma=True):
+    """perform_sparse_sparse_matmul restated: A CSR [M, K] x B CSC [K, N] -> dense fp32."""
+    M, N = len(arp) - 1, len(bcp) - 1
+    C = np.empty((max(M, 1), max(N, 1)), dtype=np.float32)
+    lib().orc_spgemm_csr_csc_f32(M, N, _pad(arp, np.int32), _pad(acol, np.int32), _pad(aval, np.float32),
+                                 _pad(bcp, np.int32), _pad(brow, np.int32), _pad(bval, np.float32), C.reshape(-1),
+                                 C.shape[1], int(use_fma))
+    return C[:M, :N]
+
+
+def dense_csc_f32(A, bcp, brow, bval, use_fma=True):
+    """perform_dense_sparse_matmul restated: A dense [M, K] x B CSC [K, N] -> dense fp32."""
+    A = np.ascontiguousarray(A, dtype=np.float32)
+    M, K = A.shape
+    N = len(bcp) - 1
+    C = np.empty((max(M, 1), max(N, 1)), dtype=np.float32)
+    lib().orc_dense_csc_f32(M, K, N, _pad(A.reshape(-1), np.float32), max(K, 1), _pad(bcp, np.int32),
+                            _pad(brow, np.int32), _pad(bval, np.float32), C.reshape(-1), C.shape[1], int(use_fma))
+    return C[:M, :N]
+
+
+def sparse_add(arp, acol, aval, brp, bcol, bval, max_nnz=None):
+    """perform_sparse_add restated: returns (rc, rows, cols, vals) of the COO result."""
+    M = len(arp) - 1
+    cap = len(aval) + len(bval) if max_nnz is None else max_nnz
+    ri, ci, vv = np.zeros(max(cap, 1), np.int32), np.zeros(max(cap, 1), np.int32), np.zeros(max(cap, 1), np.float32)
+    n = ctypes.c_long(0)
+    rc = lib().orc_sparse_add(M, _pad(arp, np.int32), _pad(acol, np.int32), _pad(aval, np.float32),
+                              _pad(brp, np.int32), _pad(bcol, np.int32), _pad(bval, np.float32), ri, ci, vv, cap,
+                              ctypes.byref(n))
+    return rc, ri[:n.value], ci[:n.value], vv[:n.value]
+
+
+def dense_to_coo(D, threshold, max_nnz=None):
+    """perform_dense_to_sparse restated: returns (rc, rows, cols, vals)."""
+    D = np.ascontiguousarray(D, dtype=np.float32)
+    M, N = D.shape
+    cap = M * N if max_nnz is None else max_nnz
+    ri, ci, vv = np.zeros(max(cap, 1), np.int32), np.zeros(max(cap, 1), np.int32), np.zeros(max(cap, 1), np.float32)
+    n = ctypes.c_long(0)
+    rc = lib().orc_dense_to_coo(M, N, _pad(D.reshape(-1), np.float32), threshold, ri, ci, vv, cap, ctypes.byref(n))
+    return rc, ri[:n.value], ci[:n.value], vv[:n.value]
+
+
+def csr_to_csc(rows, cols, rowptr, idx, data):
+    """CSR -> CSC by a stable sort on column (ConvertToCSC order, tensor/sparse-tensor.go:184-238):
+    returns (colptr, row indices, values)."""
+    rowptr = np.asarray(rowptr, np.int64)
+    r = np.repeat(np.arange(rows), np.diff(rowptr))
+    order = np.lexsort((r, np.asarray(idx)))  # by column, then row
+    colptr = np.zeros(cols + 1, np.int32)
+    np.cumsum(np.bincount(np.asarray(idx, np.int64), minlength=cols), out=colptr[1:])
+    return colptr, r[order].astype(np.int32), np.asarray(data, np.float32)[order]
 
 
 def spmv_f32(rowptr, col, val, x, use_fma=True):

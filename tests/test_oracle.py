@@ -381,3 +381,88 @@ def test_linear_backward_matches_finite_differences(code):
     np.testing.assert_allclose(dX, fdX, rtol=1e-5, atol=1e-5)
     np.testing.assert_allclose(dW, fdW, rtol=1e-5, atol=1e-5)
     np.testing.assert_allclose(db, fdb, rtol=1e-5, atol=1e-5)
+
+
+# ------------------------------------------------------------------ remaining sparse entry points
+def _rand_csr(rng, M, K, density):
+    D = np.where(rng.random((M, K)) < density, rng.standard_normal((M, K)), 0.0).astype(np.float32)
+    rows, cols = np.nonzero(D)
+    rp = np.zeros(M + 1, np.int32)
+    np.cumsum(np.bincount(rows, minlength=M), out=rp[1:])
+    return D, rp, cols.astype(np.int32), D[rows, cols]
+
+
+def test_csr_to_csc_round_trip():
+    rng = np.random.default_rng(201)
+    D, rp, ci, v = _rand_csr(rng, 30, 41, 0.2)
+    cp, ri, cv = O.csr_to_csc(30, 41, rp, ci, v)
+    back = np.zeros_like(D)
+    for j in range(41):
+        back[ri[cp[j]:cp[j + 1]], j] = cv[cp[j]:cp[j + 1]]
+    np.testing.assert_array_equal(back, D)
+
+
+def test_spgemm_matches_dense_product_and_merge_pairing():
+    rng = np.random.default_rng(203)
+    A, arp, acol, aval = _rand_csr(rng, 40, 60, 0.15)
+    Bd, brp, bcol, bval = _rand_csr(rng, 60, 35, 0.15)
+    bcp, brow, bv = O.csr_to_csc(60, 35, brp, bcol, bval)
+    C = O.spgemm_csr_csc_f32(arp, acol, aval, bcp, brow, bv)
+    ref = A.astype(np.float64) @ Bd.astype(np.float64)
+    assert O.rel_frob(C, ref) <= 1e-6
+    # duplicates pair up in merge order: A row (col 1: 2, col 1: 3), B column (row 1: 5, row 1: 7)
+    C2 = O.spgemm_csr_csc_f32(np.array([0, 2], np.int32), np.array([1, 1], np.int32), np.array([2, 3], np.float32),
+                              np.array([0, 2], np.int32), np.array([1, 1], np.int32), np.array([5, 7], np.float32))
+    assert C2[0, 0] == 2 * 5 + 3 * 7
+    # a zero sum leaves +0 (the reference stores only nonzero sums)
+    C3 = O.spgemm_csr_csc_f32(np.array([0, 2], np.int32), np.array([0, 1], np.int32), np.array([1, -1], np.float32),
+                              np.array([0, 2], np.int32), np.array([0, 1], np.int32), np.array([1, 1], np.float32))
+    assert C3[0, 0] == 0.0 and not np.signbit(C3[0, 0])
+
+
+def test_dense_csc_matches_dense_product():
+    rng = np.random.default_rng(205)
+    A = rng.standard_normal((23, 50)).astype(np.float32)
+    Bd, brp, bcol, bval = _rand_csr(rng, 50, 31, 0.2)
+    bcp, brow, bv = O.csr_to_csc(50, 31, brp, bcol, bval)
+    C = O.dense_csc_f32(A, bcp, brow, bv)
+    assert O.rel_frob(C, A.astype(np.float64) @ Bd.astype(np.float64)) <= 1e-6
+
+
+def test_sparse_add_merge_cases():
+    rng = np.random.default_rng(207)
+    A, arp, acol, aval = _rand_csr(rng, 25, 33, 0.3)
+    B, brp, bcol, bval = _rand_csr(rng, 25, 33, 0.3)
+    # force some exact cancellations
+    both = np.argwhere((A != 0) & (B != 0))[:5]
+    for i, j in both:
+        B[i, j] = -A[i, j]
+    rows, cols = np.nonzero(B)
+    brp = np.zeros(26, np.int32)
+    np.cumsum(np.bincount(rows, minlength=25), out=brp[1:])
+    bcol, bval = cols.astype(np.int32), B[rows, cols]
+    rc, ri, ci, vv = O.sparse_add(arp, acol, aval, brp, bcol, bval)
+    assert rc == 0
+    S = np.zeros((25, 33), np.float32)
+    S[ri, ci] = vv
+    np.testing.assert_array_equal(S, A + B)
+    # order: rows non-decreasing, columns increasing within a row; cancelled entries dropped
+    key = ri.astype(np.int64) * 33 + ci
+    assert np.all(np.diff(key) > 0)
+    assert not np.any(vv == 0)
+    assert ri.size == np.count_nonzero(A + B)
+    rc2, *_ = O.sparse_add(arp, acol, aval, brp, bcol, bval, max_nnz=ri.size - 1)
+    assert rc2 == -2
+
+
+def test_dense_to_coo_threshold_order_nan():
+    rng = np.random.default_rng(209)
+    D = rng.standard_normal((17, 29)).astype(np.float32)
+    D[3, 4] = np.nan
+    rc, ri, ci, vv = O.dense_to_coo(D, 0.5)
+    assert rc == 0
+    rr, cc = np.nonzero(np.abs(np.nan_to_num(D, nan=0.0)) > 0.5)
+    np.testing.assert_array_equal(ri, rr)
+    np.testing.assert_array_equal(ci, cc)
+    np.testing.assert_array_equal(vv, D[rr, cc])
+    assert O.dense_to_coo(D, 0.5, max_nnz=3)[0] == -2
