@@ -203,16 +203,26 @@ Result<TensorPtr> Transpose(Tensor &A);
 Result<TensorPtr> OptimizedGEMM(Tensor &A, Tensor &B, float alpha, float beta);
 Result<TensorPtr> OptimizedBatchMatMul(Tensor &A, Tensor &B);
 
-// Sparse ops (gpu/matrix/sparse-matrix.go:20-66, :366-399, :527-583). SparseMatMul
-// dispatches on operand kinds like the Go type switch: sparse x dense runs the CSR
-// SpMM kernel, dense x dense is MatMul; sparse x sparse and dense x sparse are not
-// provided by this backend and return an error.
+// Sparse ops (gpu/matrix/sparse-matrix.go). SparseMatMul dispatches on operand kinds
+// like the Go type switch (:20-66): sparse x dense is the CSR SpMM kernel (:134-190),
+// sparse x sparse converts A to CSR and B to CSC (:69-131), dense x sparse converts B
+// to CSC (:193-250), dense x dense is MatMul. Conversions follow the reference: only
+// COO converts, so a CSR operand where CSC is needed is an error.
 Result<TensorPtr> SparseMatMul(SparseTensor &A, Tensor &B);
 Result<TensorPtr> SparseMatMul(Tensor &A, Tensor &B);
 Result<TensorPtr> SparseMatMul(SparseTensor &A, SparseTensor &B);
 Result<TensorPtr> SparseMatMul(Tensor &A, SparseTensor &B);
 Result<TensorPtr> SparseMatVec(SparseTensor &A, Tensor &x);
 Result<SparseTensorPtr> SparseTranspose(const SparseTensor &A);
+// SparseAdd (:252-320): A + B as a new COO tensor (coinciding entries summed, zero
+// sums dropped).
+Result<SparseTensorPtr> SparseAdd(SparseTensor &A, SparseTensor &B);
+// SparseScalarMul (:322-364): a CSR clone with its values scaled on the GPU (the
+// clone's host Data is refreshed by RetrieveCPU, as in the reference).
+Result<SparseTensorPtr> SparseScalarMul(SparseTensor &A, float scalar);
+// SparseToDense (:425-473) and DenseToSparse (:475-525; keeps |v| > threshold, COO).
+Result<TensorPtr> SparseToDense(SparseTensor &A);
+Result<SparseTensorPtr> DenseToSparse(Tensor &A, float threshold);
 
 // Fused linear + activation (gpu/matrix/fused-operations.go:24-54, :380-465).
 struct FusedActivationConfig {

@@ -135,14 +135,112 @@ Result<TensorPtr> SparseMatMul(Tensor &A, Tensor &B) {  // both dense: MatMul (s
   return MatMul(A, B);
 }
 
-Result<TensorPtr> SparseMatMul(SparseTensor &A, SparseTensor &B) {
+namespace {
+template <typename T>
+T *data_or_null(std::vector<T> &v) {
+  return v.empty() ? nullptr : v.data();
+}
+}  // namespace
+
+Result<TensorPtr> SparseMatMul(SparseTensor &A, SparseTensor &B) {  // sparseSparseMatMul, sparse-matrix.go:69-131
   if (Error e = check_matmul_shapes(A.Shape, B.Shape)) return {nullptr, e};
-  return {nullptr, Errorf("sparse-sparse matrix multiplication is not provided by the MI355X backend")};
+  if (Error e = A.ConvertToCSR()) return {nullptr, wrap("failed to convert A to CSR", e)};
+  if (Error e = B.ConvertToCSC()) return {nullptr, wrap("failed to convert B to CSC", e)};
+  if (Error e = A.EnsureGPU()) return {nullptr, wrap("failed to move sparse tensor A to GPU", e)};
+  if (Error e = B.EnsureGPU()) return {nullptr, wrap("failed to move sparse tensor B to GPU", e)};
+  auto [result, rerr] = Tensor::NewDeviceResult({A.Shape[0], B.Shape[1]});
+  if (rerr) return {nullptr, wrap("failed to create result tensor", rerr)};
+  CError ce{nullptr};
+  int rc = perform_sparse_sparse_matmul(A.GPUPtr(), A.RowPtr.data(), (long)A.RowPtr.size(), data_or_null(A.Indices),
+                                        (long)A.Indices.size(), A.Shape[0], A.Shape[1], A.NNZ, B.GPUPtr(),
+                                        B.ColPtr.data(), (long)B.ColPtr.size(), data_or_null(B.Indices),
+                                        (long)B.Indices.size(), B.Shape[0], B.Shape[1], B.NNZ, result->GPUPtr(),
+                                        result->Shape[0], result->Shape[1], A.DevicePtr(), &ce);
+  if (rc != 0) return {nullptr, op_error("GPU sparse-sparse matrix multiplication", rc, ce)};
+  return {result, {}};
 }
 
-Result<TensorPtr> SparseMatMul(Tensor &A, SparseTensor &B) {
+Result<TensorPtr> SparseMatMul(Tensor &A, SparseTensor &B) {  // denseSparseMatMul, sparse-matrix.go:193-250
   if (Error e = check_matmul_shapes(A.Shape, B.Shape)) return {nullptr, e};
-  return {nullptr, Errorf("dense-sparse matrix multiplication is not provided by the MI355X backend")};
+  if (Error e = B.ConvertToCSC()) return {nullptr, wrap("failed to convert B to CSC", e)};
+  if (Error e = A.EnsureGPU()) return {nullptr, wrap("failed to move tensor A to GPU", e)};
+  if (Error e = B.EnsureGPU()) return {nullptr, wrap("failed to move sparse tensor B to GPU", e)};
+  auto [result, rerr] = Tensor::NewDeviceResult({A.Shape[0], B.Shape[1]});
+  if (rerr) return {nullptr, wrap("failed to create result tensor", rerr)};
+  CError ce{nullptr};
+  int rc = perform_dense_sparse_matmul(A.GPUPtr(), A.Shape[0], A.Shape[1], B.GPUPtr(), B.ColPtr.data(),
+                                       (long)B.ColPtr.size(), data_or_null(B.Indices), (long)B.Indices.size(),
+                                       B.Shape[0], B.Shape[1], B.NNZ, result->GPUPtr(), result->Shape[0],
+                                       result->Shape[1], A.DevicePtr(), &ce);
+  if (rc != 0) return {nullptr, op_error("GPU dense-sparse matrix multiplication", rc, ce)};
+  return {result, {}};
+}
+
+Result<SparseTensorPtr> SparseAdd(SparseTensor &A, SparseTensor &B) {  // sparse-matrix.go:252-320
+  if (Error e = A.IsCompatibleWith(B)) return {nullptr, wrap("incompatible tensors for addition", e)};
+  if (Error e = A.ConvertToCSR()) return {nullptr, wrap("failed to convert A to CSR", e)};
+  if (Error e = B.ConvertToCSR()) return {nullptr, wrap("failed to convert B to CSR", e)};
+  if (Error e = A.EnsureGPU()) return {nullptr, wrap("failed to move sparse tensor A to GPU", e)};
+  if (Error e = B.EnsureGPU()) return {nullptr, wrap("failed to move sparse tensor B to GPU", e)};
+  const long maxResultNNZ = (long)A.NNZ + (long)B.NNZ;
+  std::vector<int32_t> ri((size_t)maxResultNNZ), ci((size_t)maxResultNNZ);
+  std::vector<float> vv((size_t)maxResultNNZ);
+  long actual = 0;
+  CError ce{nullptr};
+  int rc = perform_sparse_add(A.GPUPtr(), A.RowPtr.data(), (long)A.RowPtr.size(), data_or_null(A.Indices),
+                              (long)A.Indices.size(), A.Shape[0], A.Shape[1], A.NNZ, B.GPUPtr(), B.RowPtr.data(),
+                              (long)B.RowPtr.size(), data_or_null(B.Indices), (long)B.Indices.size(), B.Shape[0],
+                              B.Shape[1], B.NNZ, data_or_null(ri), data_or_null(ci), data_or_null(vv), &actual,
+                              maxResultNNZ, A.DevicePtr(), &ce);
+  if (rc != 0) return {nullptr, op_error("GPU sparse addition", rc, ce)};
+  ri.resize((size_t)actual);
+  ci.resize((size_t)actual);
+  vv.resize((size_t)actual);
+  return tensor::NewSparseTensorCOO(A.Shape, ri, ci, vv);
+}
+
+Result<SparseTensorPtr> SparseScalarMul(SparseTensor &A, float scalar) {  // sparse-matrix.go:322-364
+  if (Error e = A.ConvertToCSR()) return {nullptr, wrap("failed to convert A to CSR", e)};
+  auto [result, cerr] = A.Clone();
+  if (cerr) return {nullptr, wrap("failed to clone sparse tensor", cerr)};
+  if (Error e = result->EnsureGPU()) return {nullptr, wrap("failed to move sparse tensor to GPU", e)};
+  CError ce{nullptr};
+  int rc = perform_sparse_scalar_multiply(result->GPUPtr(), result->RowPtr.data(), (long)result->RowPtr.size(),
+                                          data_or_null(result->Indices), (long)result->Indices.size(),
+                                          result->Shape[0], result->Shape[1], result->NNZ, scalar,
+                                          result->DevicePtr(), &ce);
+  if (rc != 0) return {nullptr, op_error("GPU sparse scalar multiplication", rc, ce)};
+  return {result, {}};
+}
+
+Result<TensorPtr> SparseToDense(SparseTensor &A) {  // sparse-matrix.go:425-473
+  if (Error e = A.ConvertToCSR()) return {nullptr, wrap("failed to convert to CSR", e)};
+  auto [result, rerr] = Tensor::NewDeviceResult(A.Shape);
+  if (rerr) return {nullptr, wrap("failed to create dense result tensor", rerr)};
+  if (Error e = A.EnsureGPU()) return {nullptr, wrap("failed to move sparse tensor to GPU", e)};
+  CError ce{nullptr};
+  int rc = perform_sparse_to_dense(A.GPUPtr(), A.RowPtr.data(), (long)A.RowPtr.size(), data_or_null(A.Indices),
+                                   (long)A.Indices.size(), A.Shape[0], A.Shape[1], A.NNZ, result->GPUPtr(),
+                                   result->Shape[0], result->Shape[1], A.DevicePtr(), &ce);
+  if (rc != 0) return {nullptr, op_error("GPU sparse to dense conversion", rc, ce)};
+  return {result, {}};
+}
+
+Result<SparseTensorPtr> DenseToSparse(Tensor &A, float threshold) {  // sparse-matrix.go:475-525
+  if (A.Shape.size() != 2) return {nullptr, Errorf("dense to sparse conversion requires 2D tensor")};
+  const long maxNNZ = (long)A.Shape[0] * A.Shape[1];
+  std::vector<int32_t> ri((size_t)maxNNZ), ci((size_t)maxNNZ);
+  std::vector<float> vv((size_t)maxNNZ);
+  if (Error e = A.EnsureGPU()) return {nullptr, wrap("failed to move tensor to GPU", e)};
+  long actual = 0;
+  CError ce{nullptr};
+  int rc = perform_dense_to_sparse(A.GPUPtr(), A.Shape[0], A.Shape[1], threshold, data_or_null(ri),
+                                   data_or_null(ci), data_or_null(vv), &actual, maxNNZ, A.DevicePtr(), &ce);
+  if (rc != 0) return {nullptr, op_error("GPU dense to sparse conversion", rc, ce)};
+  ri.resize((size_t)actual);
+  ci.resize((size_t)actual);
+  vv.resize((size_t)actual);
+  return tensor::NewSparseTensorCOO(A.Shape, ri, ci, vv);
 }
 
 Result<TensorPtr> SparseMatVec(SparseTensor &A, Tensor &x) {  // sparse-matrix.go:527-583

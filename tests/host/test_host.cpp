@@ -228,7 +228,9 @@ void TestShapeErrorsBeforeDevice() {
   CHECK_ERR_HAS(matrix::SparseMatVec(*s, *v).err, "matrix cols (4) != vector size (6)");
   CHECK_ERR_HAS(matrix::SparseMatMul(*s, *s).err, "incompatible matrix dimensions");
   auto sq = NewSparseTensorCOO({3, 3}, {0}, {0}, {1.f}).value;
-  CHECK_ERR_HAS(matrix::SparseMatMul(*sq, *sq).err, "sparse-sparse");
+  // the same tensor as both operands: A goes to CSR, then B (already CSR) cannot become
+  // CSC, as in sparseSparseMatMul (sparse-matrix.go:71-76, sparse-tensor.go:189-191)
+  CHECK_ERR_HAS(matrix::SparseMatMul(*sq, *sq).err, "can only convert from COO to CSC format");
   matrix::FusedLinearActivation f;
   CHECK_ERR_HAS(f.Forward({a.get(), b.get()}, nullptr).err, "invalid config");
   matrix::FusedLinearConfig cfg;
@@ -556,7 +558,84 @@ void TestGPUSparseMatMulAndMatVec() {
   auto Dt = NewTensor({3, 2}, {1, 2, 3, 4, 5, 6}).value;
   auto C2 = gs->SparseMul(*S, *Dt);
   CHECK(C2->At(3, 1) == 28);
-  CHECK_PANICS(matrix::GPUSparseMatMul(*gs, *gs->T()));  // sparse x sparse not provided
+  // sparse x sparse: CSR x CSC merge, duplicates pair up in order ((3,1): 3*3 + 4*4)
+  auto G2 = matrix::GPUSparseMatMul(*gs, *gs->T());
+  CHECK(G2->At(0, 0) == 1 && G2->At(1, 1) == 4 && G2->At(0, 1) == 0 && G2->At(3, 3) == 25);
+}
+
+// A random COO tensor (distinct or duplicate coordinates) from the splitmix generator.
+tensor::SparseTensorPtr random_coo(int rows, int cols, int n, uint64_t seed) {
+  std::vector<int32_t> ri, ci;
+  std::vector<float> v;
+  uint64_t x = seed;
+  for (int k = 0; k < n; ++k) {
+    x = x * 6364136223846793005ULL + 1442695040888963407ULL;
+    ri.push_back((int)((x >> 33) % rows));
+    ci.push_back((int)((x >> 13) % cols));
+    v.push_back((float)((int)((x >> 45) % 1000) - 500) / 128.0f);
+  }
+  return NewSparseTensorCOO({rows, cols}, ri, ci, v).value;
+}
+
+// The remaining sparse-matrix.go entry points against the oracle restatements.
+void TestSparseOps() {
+  // sparse x sparse (sparse-matrix.go:69-131): A to CSR, B to CSC, bit-exact merge
+  auto A = random_coo(60, 80, 500, 7), B = random_coo(80, 50, 400, 8);
+  auto [C, err] = matrix::SparseMatMul(*A, *B);
+  CHECK_NOERR(err);
+  CHECK(A->GetFormat() == SparseFormat::CSR && B->GetFormat() == SparseFormat::CSC);
+  CHECK_NOERR(C->RetrieveCPU());
+  std::vector<float> ref(60 * 50);
+  orc_spgemm_csr_csc_f32(60, 50, A->RowPtr.data(), A->Indices.data(), A->Data.data(), B->ColPtr.data(),
+                         B->Indices.data(), B->Data.data(), ref.data(), 50, 1);
+  CHECK(C->Data == ref);
+  // dense x sparse (:193-250): B to CSC, accumulated over B's column entries in order
+  auto X = NewTensor({30, 60}, uniform(30 * 60, 40)).value;
+  auto S = random_coo(60, 80, 700, 9);
+  auto [D, derr] = matrix::SparseMatMul(*X, *S);
+  CHECK_NOERR(derr);
+  CHECK_NOERR(D->RetrieveCPU());
+  std::vector<float> ref2(30 * 80);
+  orc_dense_csc_f32(30, 60, 80, X->Data.data(), 60, S->ColPtr.data(), S->Indices.data(), S->Data.data(), ref2.data(),
+                    80, 1);
+  CHECK(D->Data == ref2);
+  // a CSR operand where CSC is needed is rejected, as ConvertToCSC does (:184-191)
+  CHECK_ERR_HAS(matrix::SparseMatMul(*X, *A).err, "can only convert from COO to CSC format");
+  // SparseAdd (:252-320)
+  auto P = random_coo(40, 50, 300, 10), Q = random_coo(40, 50, 300, 11);
+  auto [Sum, aerr] = matrix::SparseAdd(*P, *Q);
+  CHECK_NOERR(aerr);
+  std::vector<int32_t> ri(600), ci(600);
+  std::vector<float> vv(600);
+  long n = 0;
+  CHECK(orc_sparse_add(40, P->RowPtr.data(), P->Indices.data(), P->Data.data(), Q->RowPtr.data(), Q->Indices.data(),
+                       Q->Data.data(), ri.data(), ci.data(), vv.data(), 600, &n) == 0);
+  ri.resize(n), ci.resize(n), vv.resize(n);
+  CHECK(Sum->GetFormat() == SparseFormat::COO && Sum->NNZ == n);
+  CHECK(Sum->RowIndices == ri && Sum->ColIndices == ci && Sum->Values == vv);
+  CHECK_ERR_HAS(matrix::SparseAdd(*P, *A).err, "incompatible tensors for addition");
+  // SparseScalarMul (:322-364): a scaled clone, the original untouched
+  auto [Sc, serr] = matrix::SparseScalarMul(*P, -2.5f);
+  CHECK_NOERR(serr);
+  CHECK_NOERR(Sc->RetrieveCPU());
+  CHECK(Sc->Data.size() == P->Data.size());
+  for (size_t k = 0; k < P->Data.size(); ++k) CHECK(Sc->Data[k] == P->Data[k] * -2.5f);
+  // SparseToDense (:425-473): later duplicates win
+  auto [Pd, pderr] = matrix::SparseToDense(*P);
+  CHECK_NOERR(pderr);
+  CHECK_NOERR(Pd->RetrieveCPU());
+  std::vector<float> dref(40 * 50);
+  orc_csr_to_dense(40, 50, P->RowPtr.data(), P->Indices.data(), P->Data.data(), dref.data());
+  CHECK(Pd->Data == dref);
+  // DenseToSparse (:475-525)
+  auto [Xs, xerr] = matrix::DenseToSparse(*X, 0.5f);
+  CHECK_NOERR(xerr);
+  std::vector<int32_t> r2(1800), c2(1800);
+  std::vector<float> v2(1800);
+  long n2 = 0;
+  CHECK(orc_dense_to_coo(30, 60, X->Data.data(), 0.5f, r2.data(), c2.data(), v2.data(), 1800, &n2) == 0);
+  r2.resize(n2), c2.resize(n2), v2.resize(n2);
+  CHECK(Xs->RowIndices == r2 && Xs->ColIndices == c2 && Xs->Values == v2);
 }
 
 struct Case {
@@ -592,6 +671,7 @@ int main(int argc, char **argv) {
       {"TestLinearLayer", TestLinearLayer, true},
       {"TestGPUDenseAndGPUMatMul", TestGPUDenseAndGPUMatMul, true},
       {"TestGPUSparseMatMulAndMatVec", TestGPUSparseMatMulAndMatVec, true},
+      {"TestSparseOps", TestSparseOps, true},
   };
   int run = 0;
   for (const Case &c : cases) {
