@@ -63,9 +63,13 @@ __device__ __forceinline__ float apply_act(int act, float x, float a) {
     case 5: return x > 0.0f ? x : a * (__expf(fmaxf(-88.0f, x)) - 1.0f);
     case 6: { float c = fmaxf(-88.0f, fminf(88.0f, x)); return c / (1.0f + __expf(-c)); }
     case 7: {
+      // tanh(u) = 1 - 2 / (e^(2u) + 1): one exp and one divide instead of tanhf; the
+      // limits are exact (e -> 0 gives -1, e -> inf gives +1), and near u = 0 the
+      // absolute error stays at fp32 rounding level, far below the GEMM's own.
       float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
       inner = fmaxf(-88.0f, fminf(88.0f, inner));
-      return 0.5f * x * (1.0f + tanhf(inner));
+      const float t = 1.0f - 2.0f / (__expf(2.0f * inner) + 1.0f);
+      return 0.5f * x * (1.0f + t);
     }
     default: return x;
   }
@@ -778,7 +782,19 @@ hipError_t pick_f16(const GemmParams &p, long batch, hipStream_t s) {
     if (tiles256 >= 256 && ring_offsets_fit(p)) return launch_f16_ring<256, 256, 2, 4, 4, TA, TB>(p, batch, s);
     if (tiles256 >= 512) return launch_f16<256, 256, 64, 2, 4, TA, TB, VEC>(p, batch, s);
     const long tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
-    if (tiles128 >= 128) return launch_f16<128, 128, 64, 2, 2, TA, TB, VEC>(p, batch, s);
+    if (tiles128 >= 128) {
+      if constexpr (TB) {
+        // Fewer tiles than two rounds of the 256 CUs: the busiest CU's work decides the
+        // time. 128x96 tiles (measured at ~0.89x the per-CU efficiency of 128x128)
+        // often balance better, e.g. the 512 x 11008 linear layer: 460 tiles, at most
+        // two per CU of 128*96, against 344 tiles, two per CU of 128*128 (79 vs 94 us).
+        const long tiles96 = ((p.M + 127) / 128) * ((p.N + 95) / 96) * batch;
+        const double c128 = (double)((tiles128 + 255) / 256) * (128.0 * 128.0);
+        const double c96 = (double)((tiles96 + 255) / 256) * (128.0 * 96.0) / 0.89;
+        if (c96 < c128) return launch_f16<128, 96, 64, 2, 2, TA, TB, VEC>(p, batch, s);
+      }
+      return launch_f16<128, 128, 64, 2, 2, TA, TB, VEC>(p, batch, s);
+    }
     return launch_f16<64, 64, 64, 2, 2, TA, TB, VEC>(p, batch, s);
   }
 }

@@ -397,3 +397,21 @@ def test_f16_deterministic_batched_epilogue(dev):
         err = O.rel_frob(outs[0][z][rows], O.act_f64(G.ACT_GELU, pre))
         _say("batched epilogue", z, err)
         assert err <= 1e-5, z
+
+
+@pytest.mark.parametrize("tA", [False, True])
+def test_f16_128x96_tiles_ragged(dev, tA):
+    """K-contiguous B with a tile count that favours 128x96 tiles (the linear-layer shape
+    class): N = 5000 leaves a partial 96-wide tile, M = 520 a partial 128-row tile."""
+    rng = np.random.default_rng(59)
+    M, N, K = 520, 5000, 1032
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
+    C = _gemm_dev(dev, A, B, tA, True, G.GN_F16)
+    rows = np.concatenate([np.arange(0, 4), rng.choice(M, 12, replace=False), np.arange(M - 4, M)])
+    ref_r = O.gemm_f64_rows(O.round_f16(A[rows], False), O.round_f16(B, False), np.arange(rows.size))
+    err = O.rel_frob(C[rows], ref_r)
+    _say("128x96 tiles", tA, err)
+    assert err <= 1e-5
+    assert np.isfinite(C).all()
+
