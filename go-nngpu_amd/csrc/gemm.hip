@@ -18,8 +18,8 @@
 //    their memory layout and read with ds_read_b64_tr_b16, which transposes 4x16
 //    blocks across a 16-lane group (out lane i, element e <- source lane 4e+i/4,
 //    element i%4), giving the MFMA K-contiguous operand directly;
-//  * fp32 operands are always stored K-contiguous; an M/N-contiguous fp32 tile is
-//    transposed on its way into LDS;
+//  * fp32 operands keep their memory layout in LDS too; an M/N-contiguous fp32 operand
+//    is read one float per lane and MFMA step (see gemm_f32_kernel);
 //  * a grouped, XCD-aware tile order: hardware dispatches workgroup w to XCD w % 8,
 //    so w is remapped to give each XCD a contiguous band of tiles that share A/B
 //    panels in that XCD's L2.
@@ -170,19 +170,6 @@ struct TileLoader {
       *reinterpret_cast<u32x4_t *>(lds + r * P + (c ^ ((r & 8) << 1))) = reg[j];
     }
   }
-  // Transposed store (fp32 only): element (r, c+e) goes to lds[(c+e)*P + r].
-  template <int P>
-  __device__ __forceinline__ void store_t(T *lds) const {
-#pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      const int v = threadIdx.x + j * NT;
-      const int r = v / VPR;
-      const int c = (v % VPR) * EPV;
-      const T *e4 = reinterpret_cast<const T *>(&reg[j]);
-#pragma unroll
-      for (int e = 0; e < EPV; ++e) lds[(c + e) * P + r] = e4[e];
-    }
-  }
 };
 
 // ------------------------------------------------------------------ fp16 fragments
@@ -302,16 +289,24 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f16_kernel(GemmParams p) {
 
 // ------------------------------------------------------------------ fp32 kernel
 // v_mfma_f32_16x16x4_f32: lane (i, g) supplies A[i][k_g], B[k_g][j]. Within a
-// 16-wide K chunk, MFMA step s uses k = 4g + s, so each lane's 4 steps read one
-// 16-byte K-contiguous vector of A and of B.
+// 16-wide K chunk, MFMA step s uses k = 4g + s (the same K order for A and B):
+//  * a K-contiguous operand is stored K-contiguous (pitch BK + 4) and each lane reads
+//    its 4 steps as one 16-byte vector;
+//  * an M/N-contiguous operand keeps its memory layout (k rows of BM or BN floats,
+//    pitch + 4, so the 4 rows 4g + s of one step fall on distinct banks) and each lane
+//    reads one float per step. Storing it transposed instead would turn every 16-byte
+//    tile store into four 4-byte LDS writes.
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VEC>
 __global__ void __launch_bounds__(WM * WN * 64) gemm_f32_kernel(GemmParams p) {
   constexpr int NT = WM * WN * 64;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 16, FN = WTN / 16;
   static_assert(BK % 16 == 0, "tile shape");
-  constexpr int P = BK + 4;  // K-contiguous rows, 16 B pad
-  __shared__ __attribute__((aligned(16))) float smem[2 * (BM + BN) * P];
+  constexpr int PA = TA ? BM + 4 : BK + 4;  // LDS pitches (floats)
+  constexpr int PB = TB ? BK + 4 : BN + 4;
+  constexpr int A_ELEMS = TA ? BK * PA : BM * PA;
+  constexpr int B_ELEMS = TB ? BN * PB : BK * PB;
+  __shared__ __attribute__((aligned(16))) float smem[2 * (A_ELEMS + B_ELEMS)];
 
   int tm, tn;
   tile_coords(p, tm, tn);
@@ -335,10 +330,10 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32_kernel(GemmParams p) {
     else    lb.load(B + k0 * p.ldb + n0, p.ldb, p.K - k0, p.N - n0);
   };
   auto store_tiles = [&](int stage) {
-    float *as = smem + stage * (BM + BN) * P;
-    float *bs = as + BM * P;
-    if (TA) la.template store_t<P>(as); else la.template store<P>(as);
-    if (TB) lb.template store<P>(bs); else lb.template store_t<P>(bs);
+    float *as = smem + stage * (A_ELEMS + B_ELEMS);
+    float *bs = as + A_ELEMS;
+    la.template store<PA>(as);
+    lb.template store<PB>(bs);
   };
 
   float4_t acc[FM][FN];
@@ -358,17 +353,31 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32_kernel(GemmParams p) {
   for (int kt = 0; kt < nk; ++kt) {
     const bool more = kt + 1 < nk;
     if (more) load_tiles((long)(kt + 1) * BK);
-    const float *as = smem + (kt & 1) * (BM + BN) * P;
-    const float *bs = as + BM * P;
+    const float *as = smem + (kt & 1) * (A_ELEMS + B_ELEMS);
+    const float *bs = as + A_ELEMS;
 #pragma unroll
     for (int kc = 0; kc < BK; kc += 16) {
       float4_t af[FM], bf[FN];
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
-        af[i] = *reinterpret_cast<const float4_t *>(as + (wm * WTM + i * 16 + li) * P + kc + 4 * lg);
+      for (int i = 0; i < FM; ++i) {
+        const int r = wm * WTM + i * 16 + li;
+        if (TA) {
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
-        bf[j] = *reinterpret_cast<const float4_t *>(bs + (wn * WTN + j * 16 + li) * P + kc + 4 * lg);
+          for (int s = 0; s < 4; ++s) af[i][s] = as[(kc + 4 * lg + s) * PA + r];
+        } else {
+          af[i] = *reinterpret_cast<const float4_t *>(as + r * PA + kc + 4 * lg);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int c = wn * WTN + j * 16 + li;
+        if (TB) {
+          bf[j] = *reinterpret_cast<const float4_t *>(bs + c * PB + kc + 4 * lg);
+        } else {
+#pragma unroll
+          for (int s = 0; s < 4; ++s) bf[j][s] = bs[(kc + 4 * lg + s) * PB + c];
+        }
+      }
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
