@@ -96,11 +96,13 @@ __device__ __forceinline__ void store_block(const GemmParams &p, float *C, long 
 
 // Grouped + XCD-aware mapping of the linear workgroup id to a (tile_m, tile_n) pair.
 __device__ __forceinline__ void tile_coords(const GemmParams &p, int &tm, int &tn) {
+  // Workgroup w runs on XCD w % 8; give XCD x the contiguous tile range
+  // [x*base + min(x, rem), ...) of base (+1 for the first rem XCDs) tiles.
   const int total = p.tiles_m * p.tiles_n;
   int w = blockIdx.x;
-  if ((total & 7) == 0) {
-    const int per = total >> 3;
-    w = (w & 7) * per + (w >> 3);
+  {
+    const int base = total >> 3, rem = total & 7, x = w & 7;
+    w = x * base + min(x, rem) + (w >> 3);
   }
   const int GROUP_M = p.group_m > 0 ? p.group_m : 4;
   const int in_group = GROUP_M * p.tiles_n;
