@@ -269,7 +269,7 @@ def main():
         roofline = {"bound": "mfma", "achieved": round(head["tflops"], 2), "peak": PEAK_F16_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(head["tflops"] / PEAK_F16_TFLOPS, 4),
                     "traffic": load_traffic("gemm_f16_8192_nn"),
-                    "kernel": "gemm_f16_ring_kernel<256,256,2,4,4,NN>", "flop_per_launch": head["flop"]}
+                    "kernel": "gemm_f16_ring_kernel<256,256,2,4,NN>", "flop_per_launch": head["flop"]}
     out = {
         "metric": METRIC,
         "value": round(head["tflops"], 2) if head else None,

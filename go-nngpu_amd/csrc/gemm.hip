@@ -402,22 +402,23 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32_kernel(GemmParams p) {
 // ------------------------------------------------------------------ fp16 DMA-ring kernel
 // Large aligned fp16 GEMMs. Differences from gemm_f16_kernel:
 //  * global -> LDS copies are buffer loads with the LDS-direct bit (16 bytes per lane
-//    written to M0 + 16*lane): no staging VGPRs and no ds_write instructions, so a
-//    4-stage LDS ring keeps 3 K-tiles in flight (BK = 32, 32 KiB per stage);
+//    written to M0 + 16*lane): no staging VGPRs and no ds_write instructions;
+//  * the LDS ring holds two slots of two consecutive K-tiles each (BK = 32, 64 KiB per
+//    slot at 256 x 256): one DMA burst fills a slot while the other is multiplied, and
+//    only one barrier per pair of K-tiles is needed;
 //  * out-of-range lanes (rows past M/N, the K tail) get a buffer offset beyond the
 //    descriptor's range, which the hardware turns into zeros;
-//  * K-contiguous operands are written in MFMA fragment order: each 1 KiB chunk holds
-//    the 16 x 32 fragment block of rows 16c..16c+15 with lane L's 16 bytes at 16*L,
-//    so a fragment is one contiguous 1 KiB ds_read_b128 (measured ~1.5x the
-//    throughput of row-strided b128 reads on gfx950);
+//  * K-contiguous operands are stored in 1 KiB chunks of 16 rows x 32 k, each MFMA
+//    fragment one ds_read_b128 within a chunk (lane quads copy whole 64-byte row
+//    pieces; see kq_slot);
 //  * MN-contiguous operands keep their memory layout, rows of 2*BM (or 2*BN) bytes,
 //    with the 32-byte block index XORed by hsw(k) so the 8 rows one 32-lane phase of
 //    ds_read_b64_tr_b16 reads (k0+8g+r, g < 2, r < 4) fall on distinct banks;
 //  * MFMA fragments are double-buffered in registers: tile k+1's fragments are read
-//    while tile k's MFMAs run, one barrier per K-tile.
+//    while tile k's MFMAs run.
 // The DMA is issued from inline assembly so the compiler does not track these LDS
 // writes (it would otherwise wait for every outstanding load before each LDS read);
-// the kernel orders them itself with s_waitcnt vmcnt and the per-tile barrier.
+// the kernel orders them itself with s_waitcnt vmcnt and the barriers.
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
 struct BufRsrc {
@@ -531,196 +532,23 @@ __device__ __forceinline__ void store_tile_coalesced(const GemmParams &p, float 
   (store_pass<FM, FN, EP, PASS>(p, C, row0, col0, acc, region, vec_ok), ...);
 }
 
-// Geometry of a ring-kernel instantiation (BK = 32 elements of K per stage).
-template <int BM, int BN, int WM, int WN, int S, bool TA, bool TB>
-struct RingCfg {
-  static constexpr int BK = 32;
-  static constexpr int NW = WM * WN;
-  static constexpr int WTM = BM / WM, WTN = BN / WN;
-  static constexpr int FM = WTM / 16, FN = WTN / 16;
-  static constexpr int OPA = BM * BK * 2;           // bytes of A per stage
-  static constexpr int OPB = BN * BK * 2;           // bytes of B per stage (at offset OPA)
-  static constexpr int STB = OPA + OPB;             // bytes per stage
-  static constexpr int IPA = BM / 16 / NW;          // 1 KiB DMA chunks per wave per tile, A
-  static constexpr int IPB = BN / 16 / NW;          //   ... and B
-  static constexpr int RBA = TA ? BM * 2 : BK * 2;  // LDS row bytes of the A / B tiles
-  static constexpr int RBB = TB ? BK * 2 : BN * 2;
-  static constexpr int LPW = IPA + IPB;             // DMA instructions per wave per tile
-};
+// K-contiguous tiles: a 1 KiB DMA chunk holds rows 16c..16c+15 (32 k each). Lane L
+// copies 16 bytes of row 16c + (L >> 2), so each lane quad reads one row's 64
+// contiguous bytes (a quad spread over four rows stalled the address unit on the L1
+// cache, measured 14% slower for NT). The hardware writes lane L's bytes to slot L of
+// the chunk, so the k octet it loads is permuted, q = (L & 3) ^ g(row), such that an
+// MFMA fragment read (lane l: row l & 15, octet l >> 4, slot kq_slot) hits 16 distinct
+// 16-byte bank groups in every 16 lanes and 8 distinct ones in every 8.
+__device__ __forceinline__ int kq_swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+__device__ __forceinline__ int kq_slot(int r, int q) { return 4 * r + (q ^ kq_swz(r)); }
+__device__ __forceinline__ int kq_octet(int lane) { return (lane & 3) ^ kq_swz(lane >> 2); }
 
-// Main loop of the ring kernel for one output tile (rows m0.., columns n0.., batch z)
-// over K-tiles [kt0, kt1): adds the products into acc. Leaves every DMA complete and
-// every wave past a barrier, so the caller may reuse smem.
-template <int BM, int BN, int WM, int WN, int S, bool TA, bool TB>
-__device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long n0, long z, int kt0, int kt1,
-                                              char *smem, float4_t (&acc)[BM / WM / 16][BN / WN / 16]) {
-  constexpr int BK = 32;
-  constexpr int NW = WM * WN;
-  constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int FM = WTM / 16, FN = WTN / 16;
-  constexpr int OPA = BM * BK * 2;           // bytes of A per stage
-  constexpr int OPB = BN * BK * 2;           // bytes of B per stage (at offset OPA)
-  constexpr int STB = OPA + OPB;             // bytes per stage
-  constexpr int IPA = BM / 16 / NW;          // 1 KiB DMA chunks per wave per tile, A
-  constexpr int IPB = BN / 16 / NW;          //   ... and B
-  constexpr int RBA = TA ? BM * 2 : BK * 2;  // LDS row bytes of the A / B tiles
-  constexpr int RBB = TB ? BK * 2 : BN * 2;
-  constexpr int LPW = IPA + IPB;             // DMA instructions per wave per tile
-  static_assert(IPA >= 1 && IPB >= 1 && BM % (16 * NW) == 0 && BN % (16 * NW) == 0, "DMA split");
-  static_assert(S >= 3 && (S - 2) * LPW < 64, "ring depth");
-  static_assert((!TA || BM >= 128) && (TB || BN >= 128), "MN-contiguous rows need 8 XOR blocks of 32 B");
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int wm = wave / WN, wn = wave % WN;
-
-  // Per-lane DMA plan, fixed for the whole K loop. K-contiguous: chunk c = rows
-  // 16c..16c+15 in fragment order. MN-contiguous: chunk c = k rows c*(1024/RB).. .
-  // Lanes whose row (or column block) lies past M (or N) get the out-of-range offset.
-  BufRsrc ra, rb;
-  unsigned voa[IPA], vob[IPB];
-  int kla[IPA], klb[IPB];  // k within the tile that the lane loads
-  {
-    const _Float16 *A = static_cast<const _Float16 *>(p.A) + z * p.strideA;
-    const _Float16 *B = static_cast<const _Float16 *>(p.B) + z * p.strideB;
-    const long k0 = (long)kt0 * BK;
-    ra = make_rsrc(TA ? (const void *)(A + k0 * p.lda + m0) : (const void *)(A + m0 * p.lda + k0));
-    rb = make_rsrc(TB ? (const void *)(B + n0 * p.ldb + k0) : (const void *)(B + k0 * p.ldb + n0));
-#pragma unroll
-    for (int i = 0; i < IPA; ++i) {
-      const int c = wave * IPA + i;
-      if (!TA) {
-        const int r = c * 16 + (lane & 15), q = lane >> 4;
-        kla[i] = 8 * q;
-        voa[i] = m0 + r < p.M ? (unsigned)((long)r * p.lda * 2 + 16 * q) : kOutOfRange;
-      } else {
-        constexpr int GPR = RBA / 16;
-        const int k = c * (1024 / RBA) + lane / GPR, qp = lane % GPR;
-        const int q = 2 * ((qp >> 1) ^ hsw(k)) + (qp & 1);
-        kla[i] = k;
-        voa[i] = m0 + 8 * q < p.M ? (unsigned)((long)k * p.lda * 2 + 16 * q) : kOutOfRange;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < IPB; ++i) {
-      const int c = wave * IPB + i;
-      if (TB) {
-        const int r = c * 16 + (lane & 15), q = lane >> 4;
-        klb[i] = 8 * q;
-        vob[i] = n0 + r < p.N ? (unsigned)((long)r * p.ldb * 2 + 16 * q) : kOutOfRange;
-      } else {
-        constexpr int GPR = RBB / 16;
-        const int k = c * (1024 / RBB) + lane / GPR, qp = lane % GPR;
-        const int q = 2 * ((qp >> 1) ^ hsw(k)) + (qp & 1);
-        klb[i] = k;
-        vob[i] = n0 + 8 * q < p.N ? (unsigned)((long)k * p.ldb * 2 + 16 * q) : kOutOfRange;
-      }
-    }
-  }
-  const long a_step = TA ? (long)BK * p.lda * 2 : (long)BK * 2;
-  const long b_step = TB ? (long)BK * 2 : (long)BK * p.ldb * 2;
-  const unsigned sbase = lds_offset(smem);
-  const int nk = kt1 - kt0;
-  const int nk2 = max(2, (nk + 1) & ~1);  // K-tiles the loop runs: tiles nk.. are all zeros
-  const long kend = min(p.K, (long)kt1 * BK) - (long)kt0 * BK;  // K extent of this range
-
-  // DMA of K-tile kt0 + t into LDS stage `stage` (the descriptors point at it). Lanes
-  // whose k lies at or past the range's end, which includes every lane of a tile
-  // t >= nk, load zeros.
-  auto issue = [&](int t, int stage) {
-    const unsigned st = sbase + (unsigned)(stage * STB);
-    const long krem_l = kend - (long)t * BK;
-    const int krem = (int)(krem_l < 0 ? 0 : (krem_l > BK ? BK : krem_l));
-#pragma unroll
-    for (int i = 0; i < IPA; ++i)
-      dma16(ra, kla[i] < krem ? voa[i] : kOutOfRange, __builtin_amdgcn_readfirstlane(st + (wave * IPA + i) * 1024));
-#pragma unroll
-    for (int i = 0; i < IPB; ++i)
-      dma16(rb, klb[i] < krem ? vob[i] : kOutOfRange,
-            __builtin_amdgcn_readfirstlane(st + OPA + (wave * IPB + i) * 1024));
-    rsrc_advance(ra, a_step);
-    rsrc_advance(rb, b_step);
-  };
-
-  auto frag_k = [&](const char *base, int row0) -> half8_t {
-    return *reinterpret_cast<const half8_t *>(base + (row0 >> 4) * 1024 + lane * 16);
-  };
-  auto frag_t = [&](const char *base, int col0, int rowb) -> half8_t {
-    const int s = lane & 15, g = lane >> 4;
-    const int k = 8 * g + (s >> 2);
-    const int col = col0 + 4 * (s & 3);
-    const char *p0 = base + k * rowb + (((col >> 4) ^ hsw(k)) << 5) + ((col & 15) << 1);
-    const trh4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((LDS_AS trh4_t *)(p0));
-    const trh4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((LDS_AS trh4_t *)(p0 + 4 * rowb));
-    const half4_t l4 = __builtin_bit_cast(half4_t, lo);
-    const half4_t h4 = __builtin_bit_cast(half4_t, hi);
-    return __builtin_shufflevector(l4, h4, 0, 1, 2, 3, 4, 5, 6, 7);
-  };
-
-  half8_t fa[2][FM], fb[2][FN];
-  auto read_frags = [&](int stage, int set) {
-    const char *st = smem + stage * STB;
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-      fa[set][i] = TA ? frag_t(st, wm * WTM + i * 16, RBA) : frag_k(st, wm * WTM + i * 16);
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-      fb[set][j] = TB ? frag_k(st + OPA, wn * WTN + j * 16) : frag_t(st + OPA, wn * WTN + j * 16, RBB);
-  };
-
-  auto mfma_set = [&](int set) {
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
-  };
-
-  // Prologue: tiles 0..S-2 in flight; wait for tile 0.
-#pragma unroll
-  for (int t = 0; t < S - 1; ++t) issue(t, t);
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 2) * LPW));
-  __syncthreads();
-
-  // One K-tile per step, the same instructions for every step: tile k+1 has landed
-  // (tiles k+2..k+S-2 may still be in flight); publish it, refill the stage tile k-1
-  // used with tile k+S-1 (zeros past the end of K), read tile k+1's fragments into the
-  // other register set, multiply tile k. The scheduling fences keep tile k's MFMAs
-  // ahead of the next barrier, and the group barriers interleave one LDS read per MFMA.
-  // The loop runs an even number of tiles; a padding tile multiplies zeros.
-  // Stages rotate: tile k+1 is read from stage sr and tile k+S-1 lands in stage si.
-  int sr = 1 % S, si = S - 1;
-  auto step = [&](int k, int set) {
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 3) * LPW));
-    __syncthreads();
-    __builtin_amdgcn_sched_barrier(0);
-    issue(k + S - 1, si);
-    read_frags(sr, set ^ 1);
-    mfma_set(set);
-#pragma unroll
-    for (int g = 0; g < FM + 2 * FN; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - (FM + 2 * FN), 0);
-    sr = sr + 1 == S ? 0 : sr + 1;
-    si = si + 1 == S ? 0 : si + 1;
-  };
-  read_frags(0, 0);
-  for (int k = 0; k < nk2; k += 2) {
-    step(k, 0);
-    step(k + 1, 1);
-  }
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-  __syncthreads();
-}
-
-// Writes one wave's accumulator tile to C through the LDS staging region (the ring).
-template <int BM, int BN, int WM, int WN, int S>
+// Writes one wave's accumulator tile to C through the LDS staging region (the ring,
+// RING bytes).
+template <int BM, int BN, int WM, int WN, int RING>
 __device__ __forceinline__ void ring_epilogue(const GemmParams &p, long m0, long n0, long z, char *smem,
                                               const float4_t (&acc)[BM / WM / 16][BN / WN / 16]) {
   constexpr int NW = WM * WN, WTM = BM / WM, WTN = BN / WN, FM = WTM / 16, FN = WTN / 16;
-  constexpr int RING = S * (BM + BN) * 32 * 2;
   constexpr int EP = (NW * 32 * (WTN + 4) * 4 <= RING) ? 32 : 16;  // rows per staging pass
   static_assert(NW * EP * (WTN + 4) * 4 <= RING, "epilogue staging exceeds the ring");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -732,36 +560,18 @@ __device__ __forceinline__ void ring_epilogue(const GemmParams &p, long m0, long
                                    std::make_integer_sequence<int, FM / (EP / 16)>{});
 }
 
-// One workgroup per output tile, the whole K range. WPE: waves per SIMD the register
-// allocation is sized for.
-template <int BM, int BN, int WM, int WN, int S, bool TA, bool TB, int WPE>
-__global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
-gemm_f16_ring_kernel(GemmParams p) {
-  using Cfg = RingCfg<BM, BN, WM, WN, S, TA, TB>;
-  __shared__ __attribute__((aligned(1024))) char smem[S * Cfg::STB];
-  int tm, tn;
-  tile_coords(p, tm, tn);
-  float4_t acc[Cfg::FM][Cfg::FN];
-#pragma unroll
-  for (int i = 0; i < Cfg::FM; ++i)
-#pragma unroll
-    for (int j = 0; j < Cfg::FN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-  const long m0 = (long)tm * BM, n0 = (long)tn * BN, z = blockIdx.z;
-  ring_mainloop<BM, BN, WM, WN, S, TA, TB>(p, m0, n0, z, 0, (int)((p.K + 31) / 32), smem, acc);
-  ring_epilogue<BM, BN, WM, WN, S>(p, m0, n0, z, smem, acc);
-}
-
-// Main loop for op(A) = A^T, op(B) = B (both operands MN-contiguous) with K-tile
-// pairs: the ring holds two slots of two consecutive K-tiles each (per operand, one
-// single-tile region per K-tile, laid out as in ring_mainloop), and one DMA burst fills
-// a whole slot. Only the odd step of a pair waits for data and passes a barrier (pair
-// pp+1 lands, then the slot pair pp used is refilled with pair pp+2); the even step
-// reads the second tile of a slot that is already visible. Half the barriers of
-// ring_mainloop, measured 3-4% faster for this layout. With a K-contiguous operand the
-// paired bursts were slower (NT -7%), so the other layouts keep ring_mainloop.
-template <int BM, int BN, int WM, int WN>
-__device__ __forceinline__ void ring2_tn_mainloop(const GemmParams &p, long m0, long n0, long z, int nk, char *smem,
-                                                  float4_t (&acc)[BM / WM / 16][BN / WN / 16]) {
+// Main loop of the ring kernel for one output tile (rows m0.., columns n0.., batch z),
+// nk K-tiles: adds the products into acc. K-tiles go in pairs: slot pp & 1 holds tiles
+// 2pp and 2pp+1 of A, then of B (one single-tile region each). Per pair, the even step
+// multiplies tile 2pp while reading tile 2pp+1's fragments from the same, already
+// visible slot; the odd step waits for pair pp+1, passes the pair's one barrier,
+// refills the slot just consumed with pair pp+2 and reads tile 2pp+2's fragments.
+// Measured against a 4-stage ring of single K-tiles with one barrier per tile: NN
+// 1139 -> 1170, TN 1139 -> 1179, TT 1145 -> 1156, NT equal (TFLOP/s, 8192^3). Leaves
+// every DMA complete and every wave past a barrier, so the caller may reuse smem.
+template <int BM, int BN, int WM, int WN, bool TA, bool TB>
+__device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long n0, long z, int nk, char *smem,
+                                              float4_t (&acc)[BM / WM / 16][BN / WN / 16]) {
   constexpr int BK = 32;
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -771,36 +581,49 @@ __device__ __forceinline__ void ring2_tn_mainloop(const GemmParams &p, long m0, 
   constexpr int CA = 2 * OPA / 1024, CB = 2 * OPB / 1024;
   constexpr int IPA = CA / NW, IPB = CB / NW;  // 1 KiB DMA chunks per wave per pair
   constexpr int LPW = IPA + IPB;
-  constexpr int RBA = BM * 2, RBB = BN * 2;  // LDS row bytes (one k row of a tile)
+  constexpr int RBA = BM * 2, RBB = BN * 2;  // LDS row bytes of MN-contiguous tiles (one k row)
   static_assert(CA % NW == 0 && CB % NW == 0 && IPA >= 1 && IPB >= 1, "DMA split");
   static_assert(LPW < 64, "vmcnt range");
-  static_assert(BM >= 128 && BN >= 128, "MN-contiguous rows need 8 XOR blocks of 32 B");
+  static_assert((!TA || BM >= 128) && (TB || BN >= 128), "MN-contiguous rows need 8 XOR blocks of 32 B");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int wm = wave / WN, wn = wave % WN;
 
-  // Per-lane DMA plan: chunk c of a pair is tile c / (nchunks / 2), k rows
-  // (c % (nchunks / 2)) * (1024 / row bytes).. of it, 32-byte blocks XOR-swizzled by
-  // hsw(k). Offset from the pair's start and the k (0..63) the lane covers; lanes
-  // whose columns lie past M (or N) get the out-of-range offset.
+  // Per-lane DMA plan: chunk c of a pair belongs to tile h = c / (nchunks / 2). For a
+  // K-contiguous operand it holds rows 16cl..16cl+15 (cl = c % (nchunks / 2)), lane
+  // quads per row as kq_slot lays out; for an MN-contiguous one, k rows
+  // cl * (1024 / row bytes).. with 32-byte blocks XOR-swizzled by hsw(k). Each lane
+  // keeps its offset from the pair's start and the k (0..63) it covers; lanes whose
+  // rows or columns lie past M (or N) get the out-of-range offset.
   BufRsrc ra, rb;
   unsigned voa[IPA], vob[IPB];
   int kla[IPA], klb[IPB];
-  auto plan = [&](int c, int nchunks, int rb_bytes, long ld, long lim, unsigned &vo, int &kl) {
+  auto plan = [&](bool kcontig, int c, int nchunks, int rb_bytes, long ld, long lim, unsigned &vo, int &kl) {
     const int h = c / (nchunks / 2), cl = c % (nchunks / 2);
+    if (kcontig) {
+      const int row = 16 * cl + (lane >> 2), q = kq_octet(lane);
+      kl = 32 * h + 8 * q;
+      vo = lim > row ? (unsigned)((long)row * ld * 2 + 64 * h + 16 * q) : kOutOfRange;
+      return;
+    }
     const int gpr = rb_bytes / 16;
     const int k = cl * (1024 / rb_bytes) + lane / gpr, qp = lane % gpr;
     const int q = 2 * ((qp >> 1) ^ hsw(k)) + (qp & 1);
     kl = 32 * h + k;
     vo = lim > 8 * q ? (unsigned)((long)(32 * h + k) * ld * 2 + 16 * q) : kOutOfRange;
   };
-  ra = make_rsrc(static_cast<const _Float16 *>(p.A) + z * p.strideA + m0);
-  rb = make_rsrc(static_cast<const _Float16 *>(p.B) + z * p.strideB + n0);
+  {
+    const _Float16 *A = static_cast<const _Float16 *>(p.A) + z * p.strideA;
+    const _Float16 *B = static_cast<const _Float16 *>(p.B) + z * p.strideB;
+    ra = make_rsrc(TA ? A + m0 : A + m0 * p.lda);
+    rb = make_rsrc(TB ? B + n0 * p.ldb : B + n0);
+  }
 #pragma unroll
-  for (int i = 0; i < IPA; ++i) plan(wave * IPA + i, CA, RBA, p.lda, p.M - m0, voa[i], kla[i]);
+  for (int i = 0; i < IPA; ++i) plan(!TA, wave * IPA + i, CA, RBA, p.lda, p.M - m0, voa[i], kla[i]);
 #pragma unroll
-  for (int i = 0; i < IPB; ++i) plan(wave * IPB + i, CB, RBB, p.ldb, p.N - n0, vob[i], klb[i]);
-  const long a_step = 2L * BK * p.lda * 2, b_step = 2L * BK * p.ldb * 2;
+  for (int i = 0; i < IPB; ++i) plan(TB, wave * IPB + i, CB, RBB, p.ldb, p.N - n0, vob[i], klb[i]);
+  const long a_step = TA ? 2L * BK * p.lda * 2 : 2L * BK * 2;
+  const long b_step = TB ? 2L * BK * 2 : 2L * BK * p.ldb * 2;
   const unsigned sbase = lds_offset(smem);
   const int np = max(1, (nk + 1) >> 1);  // pairs the loop runs; tiles past nk are zeros
 
@@ -832,15 +655,20 @@ __device__ __forceinline__ void ring2_tn_mainloop(const GemmParams &p, long m0, 
     return __builtin_shufflevector(l4, h4, 0, 1, 2, 3, 4, 5, 6, 7);
   };
 
+  auto frag_k = [&](const char *base, int row0) -> half8_t {
+    return *reinterpret_cast<const half8_t *>(base + (row0 >> 4) * 1024 + 16 * kq_slot(lane & 15, lane >> 4));
+  };
+
   half8_t fa[2][FM], fb[2][FN];
   auto read_frags = [&](int slot, int h, int set) {
-    const char *st = smem + slot * SLOT;
+    const char *sa = smem + slot * SLOT + h * OPA;
+    const char *sb = smem + slot * SLOT + 2 * OPA + h * OPB;
 #pragma unroll
-    for (int i = 0; i < FM; ++i) fa[set][i] = frag_t(st + h * OPA, wm * WTM + i * 16, RBA);
+    for (int i = 0; i < FM; ++i) fa[set][i] = TA ? frag_t(sa, wm * WTM + i * 16, RBA) : frag_k(sa, wm * WTM + i * 16);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) fb[set][j] = frag_t(st + 2 * OPA + h * OPB, wn * WTN + j * 16, RBB);
+    for (int j = 0; j < FN; ++j) fb[set][j] = TB ? frag_k(sb, wn * WTN + j * 16) : frag_t(sb, wn * WTN + j * 16, RBB);
   };
-  constexpr int NDS = 2 * (FM + FN);  // LDS read instructions per tile
+  constexpr int NDS = (TA ? 2 : 1) * FM + (TB ? 1 : 2) * FN;  // LDS read instructions per tile
   constexpr int NIL = NDS < FM * FN ? NDS : FM * FN;
   auto mfma_set = [&](int set) {
 #pragma unroll
@@ -884,21 +712,24 @@ __device__ __forceinline__ void ring2_tn_mainloop(const GemmParams &p, long m0, 
   __syncthreads();
 }
 
-template <int BM, int BN, int WM, int WN, int WPE>
+// One workgroup per output tile, the whole K range. WPE: waves per SIMD the register
+// allocation is sized for.
+template <int BM, int BN, int WM, int WN, bool TA, bool TB, int WPE>
 __global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
-gemm_f16_ring2_tn_kernel(GemmParams p) {
-  using Cfg = RingCfg<BM, BN, WM, WN, 4, true, false>;
-  __shared__ __attribute__((aligned(1024))) char smem[4 * Cfg::STB];  // two slots of two K-tiles
+gemm_f16_ring_kernel(GemmParams p) {
+  constexpr int FM = BM / WM / 16, FN = BN / WN / 16;
+  constexpr int RING = 4 * (BM + BN) * 32 * 2;  // two slots of two K-tiles of A and B
+  __shared__ __attribute__((aligned(1024))) char smem[RING];
   int tm, tn;
   tile_coords(p, tm, tn);
-  float4_t acc[Cfg::FM][Cfg::FN];
+  float4_t acc[FM][FN];
 #pragma unroll
-  for (int i = 0; i < Cfg::FM; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < Cfg::FN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < FN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
   const long m0 = (long)tm * BM, n0 = (long)tn * BN, z = blockIdx.z;
-  ring2_tn_mainloop<BM, BN, WM, WN>(p, m0, n0, z, (int)((p.K + 31) / 32), smem, acc);
-  ring_epilogue<BM, BN, WM, WN, 4>(p, m0, n0, z, smem, acc);
+  ring_mainloop<BM, BN, WM, WN, TA, TB>(p, m0, n0, z, (int)((p.K + 31) / 32), smem, acc);
+  ring_epilogue<BM, BN, WM, WN, RING>(p, m0, n0, z, smem, acc);
 }
 
 // ------------------------------------------------------------------ dispatch
@@ -920,15 +751,12 @@ hipError_t launch_f32(GemmParams p, long batch, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int BM, int BN, int WM, int WN, int S, bool TA, bool TB, int WPE = 2>
+template <int BM, int BN, int WM, int WN, bool TA, bool TB, int WPE = 2>
 hipError_t launch_f16_ring(GemmParams p, long batch, hipStream_t s) {
   p.tiles_m = (int)((p.M + BM - 1) / BM);
   p.tiles_n = (int)((p.N + BN - 1) / BN);
   dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
-  if constexpr (TA && !TB && S == 4)
-    hipLaunchKernelGGL((gemm_f16_ring2_tn_kernel<BM, BN, WM, WN, WPE>), grid, dim3(WM * WN * 64), 0, s, p);
-  else
-    hipLaunchKernelGGL((gemm_f16_ring_kernel<BM, BN, WM, WN, S, TA, TB, WPE>), grid, dim3(WM * WN * 64), 0, s, p);
+  hipLaunchKernelGGL((gemm_f16_ring_kernel<BM, BN, WM, WN, TA, TB, WPE>), grid, dim3(WM * WN * 64), 0, s, p);
   return hipGetLastError();
 }
 
@@ -943,7 +771,7 @@ hipError_t pick_f16(const GemmParams &p, long batch, hipStream_t s) {
     return launch_f16<64, 64, 64, 2, 2, TA, TB, VEC>(p, batch, s);
   } else {
     const long tiles256 = ((p.M + 255) / 256) * ((p.N + 255) / 256) * batch;
-    if (tiles256 >= 256 && ring_offsets_fit(p)) return launch_f16_ring<256, 256, 2, 4, 4, TA, TB>(p, batch, s);
+    if (tiles256 >= 256 && ring_offsets_fit(p)) return launch_f16_ring<256, 256, 2, 4, TA, TB>(p, batch, s);
     if (tiles256 >= 512) return launch_f16<256, 256, 64, 2, 4, TA, TB, VEC>(p, batch, s);
     const long tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
     if (tiles128 >= 128) {
