@@ -774,19 +774,23 @@ hipError_t pick_f16(const GemmParams &p, long batch, hipStream_t s) {
     if (tiles256 >= 256 && ring_offsets_fit(p)) return launch_f16_ring<256, 256, 2, 4, TA, TB>(p, batch, s);
     if (tiles256 >= 512) return launch_f16<256, 256, 64, 2, 4, TA, TB, VEC>(p, batch, s);
     const long tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
-    if (tiles128 >= 128) {
+    if (tiles128 >= 128 && ring_offsets_fit(p)) {
       if constexpr (TB) {
-        // Fewer tiles than two rounds of the 256 CUs: the busiest CU's work decides the
-        // time. 128x96 tiles (measured at ~0.89x the per-CU efficiency of 128x128)
-        // often balance better, e.g. the 512 x 11008 linear layer: 460 tiles, at most
-        // two per CU of 128*96, against 344 tiles, two per CU of 128*128 (79 vs 94 us).
+        // Two workgroups of these tiles share a CU, so the CU holding the most tiles
+        // needs ceil(ceil(tiles / 256) / 2) rounds. 128x96 tiles (a K-contiguous B
+        // allows N-tiles of 96) run at ~0.85x the per-CU rate of 128x128 and often
+        // need fewer rounds per unit of work: the 512 x 11008 linear layer takes
+        // 460 tiles of 128x96 in one round (55 us) against 344 of 128x128 (60 us);
+        // at 4096^3 (1376 against 1024 tiles) 128x128 wins.
+        auto rounds = [](long t) { return (double)(((t + 255) / 256 + 1) / 2); };
         const long tiles96 = ((p.M + 127) / 128) * ((p.N + 95) / 96) * batch;
-        const double c128 = (double)((tiles128 + 255) / 256) * (128.0 * 128.0);
-        const double c96 = (double)((tiles96 + 255) / 256) * (128.0 * 96.0) / 0.89;
-        if (c96 < c128) return launch_f16<128, 96, 64, 2, 2, TA, TB, VEC>(p, batch, s);
+        const double c128 = rounds(tiles128) * (128.0 * 128.0);
+        const double c96 = rounds(tiles96) * (128.0 * 96.0) / 0.85;
+        if (c96 < c128) return launch_f16_ring<128, 96, 2, 2, TA, TB>(p, batch, s);
       }
-      return launch_f16<128, 128, 64, 2, 2, TA, TB, VEC>(p, batch, s);
+      return launch_f16_ring<128, 128, 2, 2, TA, TB>(p, batch, s);
     }
+    if (tiles128 >= 128) return launch_f16<128, 128, 64, 2, 2, TA, TB, VEC>(p, batch, s);
     return launch_f16<64, 64, 64, 2, 2, TA, TB, VEC>(p, batch, s);
   }
 }

@@ -375,8 +375,8 @@ def test_f16_ring_batched_and_epilogue(dev):
 # ------------------------------------------------------------------ fp16, fewer 256x256 tiles than CUs
 @pytest.mark.parametrize("tA,tB", VARIANTS)
 def test_f16_few_tiles_ragged_all_transposes(dev, tA, tB):
-    """3 x 12 tiles of 256 (the register-staged kernels take it) with M, N ragged and an
-    8-deep K tail (K = 5000)."""
+    """3 x 12 tiles of 256: the 128-wide ring kernels take it (128x128 tiles for NN and
+    TN, 128x96 for NT and TT), with M, N ragged and an 8-deep K tail (K = 5000)."""
     rng = np.random.default_rng(43)
     M, N, K = 704, 3000, 5000
     A = rng.standard_normal((M, K)).astype(np.float32)
@@ -435,3 +435,29 @@ def test_f16_128x96_tiles_ragged(dev, tA):
     assert err <= 1e-5
     assert np.isfinite(C).all()
 
+
+
+def test_f16_register_staged_when_ring_offsets_overflow(dev):
+    """A leading dimension of 2^21 halves or more overflows the ring kernels' 32-bit DMA
+    offsets, so the register-staged kernel takes the 128x128 tiles. Its result equals the
+    ring kernel's on a compact copy of the operand, bit for bit (same summation order)."""
+    import torch
+
+    torch.manual_seed(61)
+    M, N, K = 128, 16384, 64
+    lda = (1 << 21) + 64
+    a_big = torch.zeros(M * lda, dtype=torch.float16, device=dev)  # 512 MiB
+    a = torch.randn(M, K, device=dev).half()
+    a_view = a_big.as_strided((M, K), (lda, 1))
+    a_view.copy_(a)
+    b = (0.05 * torch.randn(K, N, device=dev)).half()
+    c_wide = torch.empty(M, N, device=dev)
+    c_compact = torch.empty(M, N, device=dev)
+    G.gemm(a_view, b, c_wide)
+    G.gemm(a, b, c_compact)
+    torch.cuda.synchronize()
+    same = torch.equal(c_wide, c_compact)
+    _say("register-staged vs ring (lda 2^21+64)", same)
+    assert same
+    ref = a.float() @ b.float()
+    assert ((c_wide - ref).norm() / ref.norm()).item() <= 1e-5
