@@ -294,6 +294,56 @@ int perform_sparse_matvec(GPUPtr aValuesPtr, int *aRowPtr, long aRowPtrLen, int 
                   });
 }
 
+// ActivationForward entries (metal_bridge_activation.m forwards): a device kernel over
+// the buffers, then a synchronisation as every Part-1 call.
+static int activation_forward(GPUPtr inputPtr, GPUPtr outputPtr, long rows, long cols, int act, float alpha,
+                              const char *name, CError *err) {
+  gn::Context *ctx = gn::context(err);
+  if (!ctx) return -1;
+  Buffer *in = gn::as_buffer(inputPtr), *out = gn::as_buffer(outputPtr);
+  if (!in || !out) return set_error(err, -1, "Invalid buffer pointers for %s forward.", name);
+  if (rows < 0 || cols < 0) return set_error(err, -1, "Invalid size for %s forward.", name);
+  if (!fits(in, rows, cols, 4) || !fits(out, rows, cols, 4))
+    return set_error(err, -1, "Buffer smaller than the %ld values of %s forward.", rows * cols, name);
+  const float *x = static_cast<const float *>(in->dptr);
+  float *y = static_cast<float *>(out->dptr);
+  const int rc = act == 3 ? gn::launch_softmax_rows(x, y, rows, cols, ctx->stream, err)
+                          : gn::launch_act_forward(x, y, rows * cols, act, alpha, ctx->stream, err);
+  if (rc) return -1;
+  return sync(ctx->stream, err, -1);
+}
+
+int perform_activation_relu_forward(GPUPtr inputPtr, long size, GPUPtr outputPtr, DevicePtr, CError *err) {
+  return activation_forward(inputPtr, outputPtr, 1, size, 0, 0.0f, "ReLU", err);
+}
+int perform_activation_sigmoid_forward(GPUPtr inputPtr, long size, GPUPtr outputPtr, DevicePtr, CError *err) {
+  return activation_forward(inputPtr, outputPtr, 1, size, 1, 0.0f, "Sigmoid", err);
+}
+int perform_activation_tanh_forward(GPUPtr inputPtr, long size, GPUPtr outputPtr, DevicePtr, CError *err) {
+  return activation_forward(inputPtr, outputPtr, 1, size, 2, 0.0f, "Tanh", err);
+}
+int perform_activation_softmax_1d_forward(GPUPtr inputPtr, long size, GPUPtr outputPtr, DevicePtr, CError *err) {
+  return activation_forward(inputPtr, outputPtr, 1, size, 3, 0.0f, "Softmax 1D", err);
+}
+int perform_activation_softmax_2d_forward(GPUPtr inputPtr, long batchSize, long features, GPUPtr outputPtr,
+                                          DevicePtr, CError *err) {
+  return activation_forward(inputPtr, outputPtr, batchSize, features, 3, 0.0f, "Softmax 2D", err);
+}
+int perform_activation_leaky_relu_forward(GPUPtr inputPtr, long size, float alpha, GPUPtr outputPtr, DevicePtr,
+                                          CError *err) {
+  return activation_forward(inputPtr, outputPtr, 1, size, 4, alpha, "Leaky ReLU", err);
+}
+int perform_activation_elu_forward(GPUPtr inputPtr, long size, float alpha, GPUPtr outputPtr, DevicePtr,
+                                   CError *err) {
+  return activation_forward(inputPtr, outputPtr, 1, size, 5, alpha, "ELU", err);
+}
+int perform_activation_swish_forward(GPUPtr inputPtr, long size, GPUPtr outputPtr, DevicePtr, CError *err) {
+  return activation_forward(inputPtr, outputPtr, 1, size, 6, 0.0f, "Swish", err);
+}
+int perform_activation_gelu_forward(GPUPtr inputPtr, long size, GPUPtr outputPtr, DevicePtr, CError *err) {
+  return activation_forward(inputPtr, outputPtr, 1, size, 7, 0.0f, "GELU", err);
+}
+
 void free_c_error_message(char *message) { free(message); }
 
 // ---------------------------------------------------------------- remaining sparse entries
@@ -605,6 +655,16 @@ int gn_activation_backward(const float *grad_out, const float *pre, long rows, l
   if (!gn::context(err)) return -1;
   return gn::launch_act_backward(grad_out, pre, rows, cols, act, alpha, scale, grad_in, grad_bias,
                                  gn::resolve_stream(stream), err);
+}
+
+int gn_activation_forward(const float *in, float *out, long n, int act, float alpha, void *stream, CError *err) {
+  if (!gn::context(err)) return -1;
+  return gn::launch_act_forward(in, out, n, act, alpha, gn::resolve_stream(stream), err);
+}
+
+int gn_softmax_rows(const float *in, float *out, long rows, long cols, void *stream, CError *err) {
+  if (!gn::context(err)) return -1;
+  return gn::launch_softmax_rows(in, out, rows, cols, gn::resolve_stream(stream), err);
 }
 
 int gn_transpose_f32(const float *in, long rows, long cols, float *out, void *stream, CError *err) {

@@ -81,6 +81,11 @@ int launch_cast_f16_f32(const uint16_t *in, float *out, size_t n, hipStream_t s,
 int launch_transpose_f32(const float *in, long rows, long cols, float *out, hipStream_t s, CError *err);
 // grad_in = grad_out * act'(pre) * scale element-wise (derivative with respect to the
 // pre-activation), and optionally grad_bias[j] = sum over rows of grad_in[., j].
+// y = act(x) element-wise over n floats (act.h codes, GN_ACT_NONE copies).
+bool act_forward_supported(int act);
+int launch_act_forward(const float *in, float *out, long n, int act, float alpha, hipStream_t s, CError *err);
+// Row-wise softmax of a row-major [rows, cols] matrix.
+int launch_softmax_rows(const float *in, float *out, long rows, long cols, hipStream_t s, CError *err);
 int launch_act_backward(const float *grad_out, const float *pre, long rows, long cols, int act, float alpha,
                         float scale, float *grad_in, float *grad_bias, hipStream_t s, CError *err);
 bool act_grad_supported(int act);

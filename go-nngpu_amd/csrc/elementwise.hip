@@ -2,6 +2,7 @@
 // transpose, synthetic-data generators and a flag-clearing kernel.
 #include <algorithm>
 
+#include "act.h"
 #include "common.h"
 
 namespace gn {
@@ -9,6 +10,7 @@ namespace {
 
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
 
 unsigned grid_for(size_t work_items, unsigned block) {
   size_t g = (work_items + block - 1) / block;
@@ -127,7 +129,7 @@ uint64_t stream_base(uint64_t seed, uint64_t sid) {
 }
 
 // ------------------------------------------------------------------ activation backward
-// Derivative of the epilogue activations (apply_act in gemm.hip, Go ActivationType codes)
+// Derivative of the activations of act.h (apply_act, Go ActivationType codes)
 // with respect to their input x, evaluated at x.
 __device__ __forceinline__ float act_grad(int act, float x, float a) {
   switch (act) {
@@ -177,6 +179,63 @@ __global__ void __launch_bounds__(256) act_backward_kernel(const float *__restri
   if (partial) partial[(long)blockIdx.y * N + j] = sum;
 }
 
+// ------------------------------------------------------------------ activation forward
+// y = act(x) element-wise (act.h, precise math). VEC: in and out are 16-byte aligned and
+// n4 float4 groups are processed as vectors; the n % 4 tail is done by the first lanes.
+template <bool VEC>
+__global__ void __launch_bounds__(256) act_forward_kernel(const float *__restrict__ in, float *__restrict__ out,
+                                                          size_t n, int act, float alpha) {
+  const size_t tid = (size_t)blockIdx.x * 256 + threadIdx.x, stride = (size_t)gridDim.x * 256;
+  size_t done = 0;
+  if (VEC) {
+    const size_t n4 = n / 4;
+    for (size_t i = tid; i < n4; i += stride) {
+      float4_t v = reinterpret_cast<const float4_t *>(in)[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = apply_act<false>(act, v[e], alpha);
+      reinterpret_cast<float4_t *>(out)[i] = v;
+    }
+    done = n4 * 4;
+  }
+  for (size_t i = done + tid; i < n; i += stride) out[i] = apply_act<false>(act, in[i], alpha);
+}
+
+// Sum (MAX = false) or maximum (MAX = true) over the 256 threads of a block; every
+// thread gets the result. red holds 4 floats of LDS.
+template <bool MAX>
+__device__ __forceinline__ float block_reduce(float v, float *red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float w = __shfl_xor(v, o, 64);
+    v = MAX ? fmaxf(v, w) : v + w;
+  }
+  __syncthreads();  // red is reused by consecutive reductions
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return MAX ? fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])) : (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// Row-wise softmax of a [rows, cols] matrix, one 256-thread block per row (grid-stride
+// over rows): m = max of the row (fmaxf, so NaNs are skipped as in the reference),
+// s = sum of expf(x - m), y = expf(x - m) / s. The reference's loops
+// (metal_bridge_activation.m:206-242, :283-325) compute the same per element; only the
+// order of the sum differs.
+__global__ void __launch_bounds__(256) softmax_rows_kernel(const float *__restrict__ in, float *__restrict__ out,
+                                                           long rows, long cols) {
+  __shared__ float red[4];
+  for (long r = blockIdx.x; r < rows; r += gridDim.x) {
+    const float *x = in + r * cols;
+    float *y = out + r * cols;
+    float m = -INFINITY;
+    for (long i = threadIdx.x; i < cols; i += 256) m = fmaxf(m, x[i]);
+    m = block_reduce<true>(m, red);
+    float sum = 0.0f;
+    for (long i = threadIdx.x; i < cols; i += 256) sum += expf(x[i] - m);
+    sum = block_reduce<false>(sum, red);
+    for (long i = threadIdx.x; i < cols; i += 256) y[i] = expf(x[i] - m) / sum;
+  }
+}
+
 // out[j] = sum of partial[c, j] over c = 0, 1, ... (fixed order: deterministic).
 __global__ void __launch_bounds__(256) colsum_finish_kernel(const float *__restrict__ partial, long chunks, long N,
                                                             float *__restrict__ out) {
@@ -224,6 +283,32 @@ int launch_act_backward(const float *grad_out, const float *pre, long rows, long
                        grad_bias);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? 0 : hip_error(err, -6, "activation backward launch", e);
+}
+
+bool act_forward_supported(int act) { return act == -1 || act == 0 || act == 1 || act == 2 || (act >= 4 && act <= 7); }
+
+int launch_act_forward(const float *in, float *out, long n, int act, float alpha, hipStream_t s, CError *err) {
+  if (n < 0) return set_error(err, -1, "activation forward: negative size %ld", n);
+  if (!act_forward_supported(act)) return set_error(err, -1, "activation forward: unsupported activation %d", act);
+  if (n == 0) return 0;
+  const bool vec = (((uintptr_t)in | (uintptr_t)out) & 15) == 0;
+  const long per = vec ? 4 : 1;
+  const long blocks = std::max(1L, std::min(8192L, (n / per + 255) / 256));
+  if (vec)
+    hipLaunchKernelGGL(act_forward_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, in, out, (size_t)n, act, alpha);
+  else
+    hipLaunchKernelGGL(act_forward_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, in, out, (size_t)n, act, alpha);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : hip_error(err, -1, "activation forward launch", e);
+}
+
+int launch_softmax_rows(const float *in, float *out, long rows, long cols, hipStream_t s, CError *err) {
+  if (rows < 0 || cols < 0) return set_error(err, -1, "softmax: negative size");
+  if (rows == 0 || cols == 0) return 0;
+  const long blocks = std::min(rows, 65536L);
+  hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, s, in, out, rows, cols);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : hip_error(err, -1, "softmax launch", e);
 }
 
 int launch_cast_f32_f16(const float *in, uint16_t *out, size_t n, int mode, hipStream_t s, CError *err) {

@@ -25,6 +25,7 @@
 //    panels in that XCD's L2.
 #include <utility>
 
+#include "act.h"
 #include "common.h"
 
 namespace gn {
@@ -54,27 +55,6 @@ struct GemmParams {
 };
 
 // ------------------------------------------------------------------ epilogue
-__device__ __forceinline__ float apply_act(int act, float x, float a) {
-  switch (act) {
-    case 0: return fmaxf(0.0f, x);
-    case 1: { float c = fmaxf(-88.0f, fminf(88.0f, x)); return 1.0f / (1.0f + __expf(-c)); }
-    case 2: return tanhf(x);
-    case 4: return x > 0.0f ? x : a * x;
-    case 5: return x > 0.0f ? x : a * (__expf(fmaxf(-88.0f, x)) - 1.0f);
-    case 6: { float c = fmaxf(-88.0f, fminf(88.0f, x)); return c / (1.0f + __expf(-c)); }
-    case 7: {
-      // tanh(u) = 1 - 2 / (e^(2u) + 1): one exp and one divide instead of tanhf; the
-      // limits are exact (e -> 0 gives -1, e -> inf gives +1), and near u = 0 the
-      // absolute error stays at fp32 rounding level, far below the GEMM's own.
-      float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-      inner = fmaxf(-88.0f, fminf(88.0f, inner));
-      const float t = 1.0f - 2.0f / (__expf(2.0f * inner) + 1.0f);
-      return 0.5f * x * (1.0f + t);
-    }
-    default: return x;
-  }
-}
-
 // Writes one 16x16 MFMA accumulator block (lane l holds rows 4*(l/16)+r, column l%16).
 __device__ __forceinline__ void store_block(const GemmParams &p, float *C, long row0, long col0, float4_t acc) {
   const int lane = threadIdx.x & 63;

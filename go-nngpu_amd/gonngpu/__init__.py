@@ -81,6 +81,17 @@ SIGNATURES = {
     "gn_cast_f16_f32": (_I, [_VP, _VP, _SZ, _VP, _ERR]),
     "gn_activation_backward": (_I, [_VP, _VP, _L, _L, _I, _F, _F, _VP, _VP, _VP, _ERR]),
     "gn_transpose_f32": (_I, [_VP, _L, _L, _VP, _VP, _ERR]),
+    "gn_activation_forward": (_I, [_VP, _VP, _L, _I, _F, _VP, _ERR]),
+    "gn_softmax_rows": (_I, [_VP, _VP, _L, _L, _VP, _ERR]),
+    "perform_activation_relu_forward": (_I, [_VP, _L, _VP, _VP, _ERR]),
+    "perform_activation_sigmoid_forward": (_I, [_VP, _L, _VP, _VP, _ERR]),
+    "perform_activation_tanh_forward": (_I, [_VP, _L, _VP, _VP, _ERR]),
+    "perform_activation_softmax_1d_forward": (_I, [_VP, _L, _VP, _VP, _ERR]),
+    "perform_activation_softmax_2d_forward": (_I, [_VP, _L, _L, _VP, _VP, _ERR]),
+    "perform_activation_leaky_relu_forward": (_I, [_VP, _L, _F, _VP, _VP, _ERR]),
+    "perform_activation_elu_forward": (_I, [_VP, _L, _F, _VP, _VP, _ERR]),
+    "perform_activation_swish_forward": (_I, [_VP, _L, _VP, _VP, _ERR]),
+    "perform_activation_gelu_forward": (_I, [_VP, _L, _VP, _VP, _ERR]),
     "gn_spmm_csr": (_I, [_L, _L, _L, _L, _VP, _VP, _VP, _VP, _L, _VP, _L, _VP, _VP, _ERR]),
     "gn_spmv_csr": (_I, [_L, _L, _L, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _ERR]),
     "gn_fill_uniform_f32": (_I, [_VP, _SZ, _U64, _U64, _F, _F, _VP, _ERR]),
@@ -260,6 +271,17 @@ def activation_backward(grad_out, pre, act, grad_in, grad_bias=None, alpha=0.0, 
     rows, cols = pre.shape
     _dispatch(stream_ptr, "gn_activation_backward", _ptr(grad_out), _ptr(pre), rows, cols, act, alpha, scale,
               _ptr(grad_in), _ptr(grad_bias))
+
+
+def activation_forward(x, out, act, alpha=0.0, stream_ptr=None):
+    """out = act(x) element-wise (ActivationType code other than Softmax, or ACT_NONE)."""
+    _dispatch(stream_ptr, "gn_activation_forward", _ptr(x), _ptr(out), x.numel(), act, alpha)
+
+
+def softmax_rows(x, out, stream_ptr=None):
+    """Row-wise softmax of a 2-D tensor (a 1-D tensor is one row)."""
+    rows, cols = (1, x.shape[0]) if x.dim() == 1 else (x.shape[0], x.shape[1])
+    _dispatch(stream_ptr, "gn_softmax_rows", _ptr(x), _ptr(out), rows, cols)
 
 
 def transpose(x, out, stream_ptr=None):

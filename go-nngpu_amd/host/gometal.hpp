@@ -194,6 +194,13 @@ using tensor::SparseTensorPtr;
 
 // ActivationType (gpu/matrix/activation.go:18-29).
 enum ActivationType { ReLU = 0, Sigmoid = 1, Tanh = 2, Softmax = 3, LeakyReLU = 4, ELU = 5, Swish = 6, GELU = 7 };
+std::string String(ActivationType t);  // activation.go:32-53 ("Unknown" otherwise)
+
+// ActivationForward (activation.go:56-175): a new tensor of input's shape holding
+// act(input), computed on the device by the perform_activation_*_forward entries. Softmax
+// is row-wise over the last dimension of a 1-D or 2-D tensor; other ranks are an error,
+// as are an empty shape and an unknown type. alpha is used by LeakyReLU and ELU.
+Result<TensorPtr> ActivationForward(Tensor &input, ActivationType activationType, float alpha);
 
 // Dense ops (gpu/matrix/matrix.go:53-105, :357-404).
 Result<TensorPtr> MatMul(Tensor &A, Tensor &B);

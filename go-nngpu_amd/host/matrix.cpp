@@ -74,6 +74,56 @@ Result<TensorPtr> Transpose(Tensor &A) {
   return {result, {}};
 }
 
+std::string String(ActivationType t) {
+  switch (t) {
+    case ReLU: return "ReLU";
+    case Sigmoid: return "Sigmoid";
+    case Tanh: return "Tanh";
+    case Softmax: return "Softmax";
+    case LeakyReLU: return "LeakyReLU";
+    case ELU: return "ELU";
+    case Swish: return "Swish";
+    case GELU: return "GELU";
+  }
+  return "Unknown";
+}
+
+Result<TensorPtr> ActivationForward(Tensor &input, ActivationType activationType, float alpha) {
+  if (input.Shape.empty()) return {nullptr, Errorf("cannot apply activation to empty tensor")};
+  // The rank and type errors of the reference's switch (:146-160), checked before any
+  // device work rather than after the result allocation.
+  if (activationType == Softmax && input.Shape.size() > 2)
+    return {nullptr, Errorf("softmax currently supports only 1D and 2D tensors")};
+  if (String(activationType) == "Unknown")
+    return {nullptr, Errorf("unsupported activation type: %s", String(activationType).c_str())};
+  long size = 1;
+  for (int d : input.Shape) size *= d;
+  auto [result, rerr] = Tensor::NewDeviceResult(input.Shape);
+  if (rerr) return {nullptr, wrap("failed to create result tensor", rerr)};
+  if (Error e = input.EnsureGPU()) return {nullptr, wrap("failed to move input tensor to GPU", e)};
+  GPUPtr in = input.GPUPtr(), out = result->GPUPtr();
+  DevicePtr dev = input.DevicePtr();
+  CError ce{nullptr};
+  int rc = 0;
+  switch (activationType) {
+    case ReLU: rc = perform_activation_relu_forward(in, size, out, dev, &ce); break;
+    case Sigmoid: rc = perform_activation_sigmoid_forward(in, size, out, dev, &ce); break;
+    case Tanh: rc = perform_activation_tanh_forward(in, size, out, dev, &ce); break;
+    case LeakyReLU: rc = perform_activation_leaky_relu_forward(in, size, alpha, out, dev, &ce); break;
+    case ELU: rc = perform_activation_elu_forward(in, size, alpha, out, dev, &ce); break;
+    case Swish: rc = perform_activation_swish_forward(in, size, out, dev, &ce); break;
+    case GELU: rc = perform_activation_gelu_forward(in, size, out, dev, &ce); break;
+    case Softmax:
+      if (input.Shape.size() == 1)
+        rc = perform_activation_softmax_1d_forward(in, input.Shape[0], out, dev, &ce);
+      else
+        rc = perform_activation_softmax_2d_forward(in, input.Shape[0], input.Shape[1], out, dev, &ce);
+      break;
+  }
+  if (rc != 0) return {nullptr, op_error("GPU activation forward", rc, ce)};
+  return {result, {}};
+}
+
 Result<TensorPtr> OptimizedGEMM(Tensor &A, Tensor &B, float alpha, float beta) {
   if (A.Shape.size() != 2 || B.Shape.size() != 2) return {nullptr, Errorf("optimized GEMM requires 2D tensors")};
   const int M = A.Shape[0], K = A.Shape[1], K2 = B.Shape[0], N = B.Shape[1];

@@ -177,6 +177,35 @@ int perform_dense_to_sparse(GPUPtr denseMatrixPtr, long rows, long cols, float t
                             int *colIndices, float *values, long *actualNNZ, long maxNNZ, DevicePtr mtlDevicePtr,
                             CError *err);
 
+/* metal_bridge.h:257-396, the forward half (ActivationForward, gpu/matrix/activation.go:
+ * 56-175). output = act(input) element-wise over `size` floats, with the reference's
+ * formulas (metal_bridge_activation.m): ReLU max(0,x) (:26-51); Sigmoid and Tanh of x
+ * clamped to [-88, 88] (:84-110, :145-171); Leaky ReLU x > 0 ? x : alpha*x (:371-397);
+ * ELU x > 0 ? x : alpha*(exp(max(x,-88)) - 1) (:435-467); Swish c*sigmoid(c) with
+ * c = x clamped to [-88, 88] (:514-542); GELU tanh form, inner argument clamped to
+ * [-88, 88] (:606-639). Softmax 1-D over `size` values and 2-D row-wise over
+ * [batchSize, features] (:206-242, :283-325): max-subtracted exp, divided by the sum.
+ * Input and output may be the same buffer. Codes: -1 NULL or too small buffer,
+ * negative size, or execution error (the reference returns -1 for bad buffers). */
+int perform_activation_relu_forward(GPUPtr inputPtr, long size, GPUPtr outputPtr, DevicePtr mtlDevicePtr,
+                                    CError *err);
+int perform_activation_sigmoid_forward(GPUPtr inputPtr, long size, GPUPtr outputPtr, DevicePtr mtlDevicePtr,
+                                       CError *err);
+int perform_activation_tanh_forward(GPUPtr inputPtr, long size, GPUPtr outputPtr, DevicePtr mtlDevicePtr,
+                                    CError *err);
+int perform_activation_softmax_1d_forward(GPUPtr inputPtr, long size, GPUPtr outputPtr, DevicePtr mtlDevicePtr,
+                                          CError *err);
+int perform_activation_softmax_2d_forward(GPUPtr inputPtr, long batchSize, long features, GPUPtr outputPtr,
+                                          DevicePtr mtlDevicePtr, CError *err);
+int perform_activation_leaky_relu_forward(GPUPtr inputPtr, long size, float alpha, GPUPtr outputPtr,
+                                          DevicePtr mtlDevicePtr, CError *err);
+int perform_activation_elu_forward(GPUPtr inputPtr, long size, float alpha, GPUPtr outputPtr,
+                                   DevicePtr mtlDevicePtr, CError *err);
+int perform_activation_swish_forward(GPUPtr inputPtr, long size, GPUPtr outputPtr, DevicePtr mtlDevicePtr,
+                                     CError *err);
+int perform_activation_gelu_forward(GPUPtr inputPtr, long size, GPUPtr outputPtr, DevicePtr mtlDevicePtr,
+                                    CError *err);
+
 /* metal_bridge.h:250. */
 void free_c_error_message(char *message);
 
@@ -240,6 +269,11 @@ int gn_activation_backward(const float *grad_out, const float *pre, long rows, l
                            float scale, float *grad_in, float *grad_bias, void *stream, CError *err);
 
 /* out[cols,rows] = in[rows,cols]^T, fp32, LDS-tiled. */
+/* out = act(in) element-wise over n floats (the Part-1 activation forwards on device
+ * pointers; act is an ActivationType code other than 3, or GN_ACT_NONE to copy). */
+int gn_activation_forward(const float *in, float *out, long n, int act, float alpha, void *stream, CError *err);
+/* Row-wise softmax of a row-major [rows, cols] fp32 matrix (Softmax in ActivationForward). */
+int gn_softmax_rows(const float *in, float *out, long rows, long cols, void *stream, CError *err);
 int gn_transpose_f32(const float *in, long rows, long cols, float *out, void *stream, CError *err);
 
 /* CSR SpMM on device arrays: C[M,N] = S[M,K] * D[K,N] (ld = row pitch in elements).

@@ -501,6 +501,25 @@ void orc_linear_f64(long batch, long in, long out, const float *X, const float *
     }
 }
 
+/* Row-wise softmax in float64 of a [rows, cols] fp32 matrix (ActivationForward's
+ * Softmax: metal_bridge_activation.m:206-242 for 1-D, :283-325 for 2-D): m = the row's
+ * maximum by fmax from its first element (NaNs skipped), y = exp(x - m), then y /= sum. */
+void orc_softmax_rows_f64(long rows, long cols, const float *in, double *out) {
+  for (long r = 0; r < rows; ++r) {
+    const float *x = in + r * cols;
+    double *y = out + r * cols;
+    if (cols <= 0) continue;
+    double m = x[0];
+    for (long i = 1; i < cols; ++i) m = fmax(m, (double)x[i]);
+    double s = 0.0;
+    for (long i = 0; i < cols; ++i) {
+      y[i] = exp((double)x[i] - m);
+      s += y[i];
+    }
+    for (long i = 0; i < cols; ++i) y[i] /= s;
+  }
+}
+
 /* ------------------------------------------------------------------------- */
 void orc_transpose_f32(long rows, long cols, const float *in, float *out) {
   for (long i = 0; i < rows; ++i)

@@ -128,6 +128,10 @@ int orc_dense_to_coo(long M, long N, const float *D, float threshold, int32_t *r
  * closed forms (tanh(0)=0, sigmoid(0)=1/2, large-|x| limits). Returns NaN for code 3. */
 double orc_act_f64(int code, double alpha, double x);
 float orc_act_f32(int code, float alpha, float x);
+/* Row-wise softmax (ActivationForward Softmax, metal_bridge_activation.m:206-242,
+ * :283-325) in float64. Pinned by tests/test_oracle.py: rows sum to 1, invariance to a
+ * per-row shift, the two-element closed form 1/(1+exp(b-a)), scipy.special.softmax. */
+void orc_softmax_rows_f64(long rows, long cols, const float *in, double *out);
 /* Y[b,o] = act(sum_i X[b,i]*W(i,o) + bias[o]) in float64; W(i,o) = W[i*out+o] when
  * w_out_in=0 (reference layout, fused-operations.go:413-415 / default.metal:478) or
  * W[o*in+i] when w_out_in=1 (nn.Linear layout). bias may be NULL. */

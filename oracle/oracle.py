@@ -56,6 +56,7 @@ def lib():
         "orc_spmv_csr_f32": (None, [_L, _i32p, _i32p, _f32p, _f32p, _f32p, ctypes.c_int]),
         "orc_spmv_csr_f64": (None, [_L, _i32p, _i32p, _f32p, _f32p, _f64p]),
         "orc_act_f64": (ctypes.c_double, [ctypes.c_int, ctypes.c_double, ctypes.c_double]),
+        "orc_softmax_rows_f64": (None, [_L, _L, _f32p, _f64p]),
         "orc_act_f32": (ctypes.c_float, [ctypes.c_int, ctypes.c_float, ctypes.c_float]),
         "orc_spgemm_csr_csc_f32": (None, [_L, _L, _i32p, _i32p, _f32p, _i32p, _i32p, _f32p, _f32p, _L, ctypes.c_int]),
         "orc_dense_csc_f32": (None, [_L, _L, _L, _f32p, _L, _i32p, _i32p, _f32p, _f32p, _L, ctypes.c_int]),
@@ -330,6 +331,16 @@ def linear_backward_f64(X, W, pre, dY, act, alpha=0.0, scale=1.0, act_applied=Tr
     dX = G32 @ np.asarray(W, dtype=np.float64).T
     dW = np.asarray(X, dtype=np.float64).T @ G32
     return dX, dW, G32.sum(axis=0), G
+
+
+def softmax_rows_f64(x):
+    """Row-wise softmax of a 2-D fp32 array (a 1-D array is one row) in float64
+    (orc_softmax_rows_f64)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    x2 = x.reshape(1, -1) if x.ndim == 1 else x
+    out = np.empty(x2.shape, dtype=np.float64)
+    lib().orc_softmax_rows_f64(x2.shape[0], x2.shape[1], x2.reshape(-1), out.reshape(-1))
+    return out.reshape(x.shape)
 
 
 def act_f32(code, x, alpha=0.0):

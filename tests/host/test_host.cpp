@@ -231,6 +231,13 @@ void TestShapeErrorsBeforeDevice() {
   // the same tensor as both operands: A goes to CSR, then B (already CSR) cannot become
   // CSC, as in sparseSparseMatMul (sparse-matrix.go:71-76, sparse-tensor.go:189-191)
   CHECK_ERR_HAS(matrix::SparseMatMul(*sq, *sq).err, "can only convert from COO to CSC format");
+  // ActivationForward (activation.go:56-175): errors before any device call
+  tensor::Tensor empty;
+  CHECK_ERR_HAS(matrix::ActivationForward(empty, matrix::ReLU, 0).err, "cannot apply activation to empty tensor");
+  auto t3 = NewTensor({2, 1, 3}, std::vector<float>(6)).value;
+  CHECK_ERR_HAS(matrix::ActivationForward(*t3, matrix::Softmax, 0).err, "softmax currently supports only 1D and 2D");
+  CHECK(matrix::String(matrix::GELU) == "GELU" && matrix::String((matrix::ActivationType)42) == "Unknown");
+  CHECK_ERR_HAS(matrix::ActivationForward(*t3, (matrix::ActivationType)42, 0).err, "unsupported activation type: Unknown");
   matrix::FusedLinearActivation f;
   CHECK_ERR_HAS(f.Forward({a.get(), b.get()}, nullptr).err, "invalid config");
   matrix::FusedLinearConfig cfg;
@@ -238,6 +245,37 @@ void TestShapeErrorsBeforeDevice() {
 }
 
 // ============================================================== device tests
+void TestActivationForward() {
+  // activation_test.go:32-51: ReLU of [-2,-1,0,1,2,3]
+  auto x = NewTensor({2, 3}, {-2, -1, 0, 1, 2, 3}).value;
+  auto [r, err] = matrix::ActivationForward(*x, matrix::ReLU, 0);
+  CHECK_NOERR(err);
+  CHECK_NOERR(r->RetrieveCPU());
+  CHECK((r->Data == std::vector<float>{0, 0, 0, 1, 2, 3}));
+  auto in = NewTensor({64, 129}, uniform(64 * 129, 9, -6.0f, 6.0f)).value;
+  const matrix::ActivationType types[] = {matrix::ReLU, matrix::Sigmoid, matrix::Tanh, matrix::LeakyReLU,
+                                          matrix::ELU, matrix::Swish, matrix::GELU};
+  for (matrix::ActivationType t : types) {
+    const float alpha = t == matrix::LeakyReLU ? 0.1f : 1.0f;
+    auto y = matrix::ActivationForward(*in, t, alpha).value;
+    CHECK(y && y->Shape == in->Shape);
+    if (!y) continue;
+    CHECK_NOERR(y->RetrieveCPU());
+    std::vector<double> ref(in->Data.size());
+    for (size_t i = 0; i < ref.size(); ++i) ref[i] = orc_act_f64((int)t, alpha, in->Data[i]);
+    CHECK(rel(y->Data, ref) <= 1e-5);
+  }
+  std::vector<double> sm(in->Data.size());
+  orc_softmax_rows_f64(64, 129, in->Data.data(), sm.data());
+  auto s2 = matrix::ActivationForward(*in, matrix::Softmax, 0).value;
+  CHECK_NOERR(s2->RetrieveCPU());
+  CHECK(rel(s2->Data, sm) <= 1e-5);
+  auto v = NewTensor({129}, std::vector<float>(in->Data.begin(), in->Data.begin() + 129)).value;
+  auto s1 = matrix::ActivationForward(*v, matrix::Softmax, 0).value;
+  CHECK_NOERR(s1->RetrieveCPU());
+  CHECK(rel(s1->Data, std::vector<double>(sm.begin(), sm.begin() + 129)) <= 1e-5);
+}
+
 void TestMatMul() {
   const int M = 96, K = 130, N = 70;
   auto A = NewTensor({M, K}, uniform((size_t)M * K, 1)).value;
@@ -658,6 +696,7 @@ int main(int argc, char **argv) {
       {"TestGonumDense", TestGonumDense, false},
       {"TestGPUSparseAtAndErrors", TestGPUSparseAtAndErrors, false},
       {"TestShapeErrorsBeforeDevice", TestShapeErrorsBeforeDevice, false},
+      {"TestActivationForward", TestActivationForward, true},
       {"TestMatMul", TestMatMul, true},
       {"TestResidencyReuploadsHostWrites", TestResidencyReuploadsHostWrites, true},
       {"TestMemoryStatsTrackTensors", TestMemoryStatsTrackTensors, true},

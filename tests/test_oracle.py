@@ -295,6 +295,31 @@ def test_activation_closed_forms():
         np.testing.assert_allclose(O.act_f32(code, x, 0.1), O.act_f64(code, x.astype(np.float64), 0.1), rtol=2e-6, atol=2e-6)
 
 
+def test_softmax_rows_pins():
+    """orc_softmax_rows_f64 against what fixes softmax independently: scipy's routine, rows
+    summing to 1, invariance to a per-row shift, the two-element closed form
+    1 / (1 + exp(b - a)), a constant row giving 1/n, and NaN handling (fmax skips NaN in
+    the maximum, exp then spreads it over the row)."""
+    from scipy.special import softmax
+
+    rng = np.random.default_rng(17)
+    x = (3.0 * rng.standard_normal((37, 129))).astype(np.float32)
+    y = O.softmax_rows_f64(x)
+    np.testing.assert_allclose(y, softmax(x.astype(np.float64), axis=1), rtol=1e-12, atol=1e-15)
+    np.testing.assert_allclose(y.sum(axis=1), 1.0, rtol=1e-12)
+    np.testing.assert_allclose(O.softmax_rows_f64(x + np.float32(5.0)), y, rtol=1e-5)  # x+5 rounds in fp32
+    two = np.array([[1.5, -0.25], [-30.0, 30.0]], np.float32)
+    t = O.softmax_rows_f64(two)
+    for r in range(2):
+        a, b = float(two[r, 0]), float(two[r, 1])
+        assert t[r, 0] == pytest.approx(1.0 / (1.0 + math.exp(b - a)), rel=1e-12)
+    np.testing.assert_allclose(O.softmax_rows_f64(np.full((1, 8), 2.5, np.float32)), 1.0 / 8, rtol=1e-15)
+    one = O.softmax_rows_f64(np.array([3.0, 1.0, 0.5], np.float32))  # 1-D is one row
+    assert one.shape == (3,) and one.sum() == pytest.approx(1.0)
+    nan_row = O.softmax_rows_f64(np.array([[np.nan, 1.0, 2.0]], np.float32))
+    assert np.isnan(nan_row).all()
+
+
 @pytest.mark.parametrize("w_out_in", [0, 1])
 def test_linear_f64_matches_numpy(w_out_in):
     rng = np.random.default_rng(5)
