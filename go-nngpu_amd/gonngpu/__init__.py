@@ -82,6 +82,17 @@ SIGNATURES = {
     "gn_activation_backward": (_I, [_VP, _VP, _L, _L, _I, _F, _F, _VP, _VP, _VP, _ERR]),
     "gn_transpose_f32": (_I, [_VP, _L, _L, _VP, _VP, _ERR]),
     "gn_activation_forward": (_I, [_VP, _VP, _L, _I, _F, _VP, _ERR]),
+    "createMPSGraph": (_VP, []),
+    "createMatMulNode": (_VP, [_VP, _VP, _VP]),
+    "createReLUNode": (_VP, [_VP, _VP]),
+    "compileGraph": (_VP, [_VP, _VP]),
+    "executeCompiledGraph": (None, [_VP, _VP, ctypes.POINTER(_VP), _L, ctypes.POINTER(_VP), _L]),
+    "gn_graph_placeholder": (_VP, [_VP, _L, _L, _I]),
+    "gn_graph_matmul": (_VP, [_VP, _VP, _VP, _I, _I]),
+    "gn_graph_activation": (_VP, [_VP, _VP, _I, _F]),
+    "gn_graph_compile": (_I, [_VP, ctypes.POINTER(_VP), _L, ctypes.POINTER(_VP), _L, ctypes.POINTER(_VP), _ERR]),
+    "gn_graph_execute": (_I, [_VP, _VP, ctypes.POINTER(_VP), _L, ctypes.POINTER(_VP), _L, _ERR]),
+    "gn_graph_release": (None, [_VP]),
     "gn_softmax_rows": (_I, [_VP, _VP, _L, _L, _VP, _ERR]),
     "perform_activation_relu_forward": (_I, [_VP, _L, _VP, _VP, _ERR]),
     "perform_activation_sigmoid_forward": (_I, [_VP, _L, _VP, _VP, _ERR]),
@@ -105,7 +116,7 @@ def header_symbols(path=HEADER_PATH):
     """Function names declared in include/gonngpu.h."""
     text = open(path).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b([a-z_][a-z0-9_]*)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b([A-Za-z_][A-Za-z0-9_]*)\s*\(", text, flags=re.M)))
 
 
 def load(path=LIB_PATH):

@@ -26,8 +26,11 @@
 // allocation is released when it is replaced or when the tensor is destroyed.
 #pragma once
 
+#include <any>
 #include <cstdint>
+#include <map>
 #include <memory>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -202,6 +205,11 @@ std::string String(ActivationType t);  // activation.go:32-53 ("Unknown" otherwi
 // as are an empty shape and an unknown type. alpha is used by LeakyReLU and ELU.
 Result<TensorPtr> ActivationForward(Tensor &input, ActivationType activationType, float alpha);
 
+// SetGlobalMatrixDevice (matrix.go:22-24). The reference routes MatMul through a
+// unified-memory adapter once a device is set (:27-50), which loses the result (defect
+// D2). Here the device is implicit (one GPU per process), so the pointer is only kept.
+void SetGlobalMatrixDevice(void *device);
+
 // Dense ops (gpu/matrix/matrix.go:53-105, :357-404).
 Result<TensorPtr> MatMul(Tensor &A, Tensor &B);
 Result<TensorPtr> Transpose(Tensor &A);
@@ -242,9 +250,29 @@ struct FusedLinearConfig {
   std::shared_ptr<FusedActivationConfig> Activation;  // nil -> ReLU
   float Dropout = 0.0f;
 };
-class FusedLinearActivation {
+// FusedOperation (fused-operations.go:67-73). config stands for Go's interface{}: a
+// std::any holding a pointer to the operation's config type (FusedLinearConfig * or
+// const FusedLinearConfig * for linear_activation); anything else is "invalid config
+// type", as a failed Go type assertion.
+class FusedOperation {
  public:
-  std::string GetName() const { return "linear_activation"; }
+  virtual ~FusedOperation() = default;
+  virtual Result<TensorPtr> Forward(const std::vector<Tensor *> &inputs, const std::any &config) = 0;
+  virtual Result<std::vector<TensorPtr>> Backward(Tensor &gradOutput, const std::vector<Tensor *> &savedTensors,
+                                                  const std::any &config) = 0;
+  virtual std::string GetName() const = 0;
+  virtual int64_t GetMemorySavings() const = 0;
+  virtual float GetSpeedup() const = 0;
+};
+
+class FusedLinearActivation : public FusedOperation {
+ public:
+  std::string GetName() const override { return "linear_activation"; }
+  int64_t GetMemorySavings() const override { return 512 * 1024; }  // fused-operations.go:372-374
+  float GetSpeedup() const override { return 1.4f; }                 // :376-378
+  Result<TensorPtr> Forward(const std::vector<Tensor *> &inputs, const std::any &config) override;
+  Result<std::vector<TensorPtr>> Backward(Tensor &gradOutput, const std::vector<Tensor *> &savedTensors,
+                                          const std::any &config) override;
   // inputs = {input [batch,in], weight [in,out], optional bias [out]}.
   Result<TensorPtr> Forward(const std::vector<Tensor *> &inputs, const FusedLinearConfig *config);
   // FusedLinearActivation.Backward (fused-operations.go:467-578). savedTensors =
@@ -257,9 +285,62 @@ class FusedLinearActivation {
                                           const FusedLinearConfig *config);
 };
 
+// The fusion registry (fused-operations.go:75-121). It starts with linear_activation,
+// the one fused operation on this library's path; the reference's other entries
+// (conv_bn_relu, attention, gelu_dropout, layer_norm_linear, residual_block) are not
+// provided, so looking them up reports false. Safe for concurrent use.
+void RegisterFusedOperation(const std::string &name, std::shared_ptr<FusedOperation> operation);
+std::pair<std::shared_ptr<FusedOperation>, bool> GetFusedOperation(const std::string &name);
+
 // matmulBackward of gpu/matrix/gradient.go:601-637 for C = A * B:
 // {grad_A = grad_output * B^T, grad_B = A^T * grad_output} (device-resident).
 Result<std::vector<TensorPtr>> MatMulBackward(Tensor &gradOutput, Tensor &A, Tensor &B);
+
+// MPSGraphManager (gpu/matrix/mps-graph-integration.go:15-296): named graph tensors,
+// MatMul and activation nodes, compiled subgraphs and their execution, over the graph
+// calls of the C ABI (a compiled subgraph is a HIP graph; a MatMul read only by one
+// activation runs as one GEMM with the activation in its epilogue, the LinearActivation
+// fusion of :103-115). Names follow the Go code: MatMulOp returns "matmul_<a>_<b>",
+// ActivationOp "<type>_<input>". Unknown names, mismatched shapes and unknown activation
+// types panic, where the Go code would dereference a nil tensor or panic itself (:209).
+// CompileGraph and Execute report errors instead of returning nil / empty maps.
+struct CompiledOperation {
+  void *Executable = nullptr;  // the compiled HIP graph (owned by the manager)
+  std::vector<std::string> Inputs, Outputs;
+  std::vector<std::vector<int>> InputShapes, OutputShapes;
+  std::string CacheKey;
+};
+class MPSGraphManager {
+ public:
+  explicit MPSGraphManager(void *device = nullptr);
+  ~MPSGraphManager();
+  MPSGraphManager(const MPSGraphManager &) = delete;
+  MPSGraphManager &operator=(const MPSGraphManager &) = delete;
+  // A 2-D placeholder ("float16" / "half": fp16 on the device, cast from the fp32 input
+  // tensors at execution; anything else fp32). Cached by name, as :136-148.
+  void *CreateTensor(const std::string &name, const std::vector<int> &shape, const std::string &dataType);
+  std::string MatMulOp(const std::string &a, const std::string &b, bool transposeA, bool transposeB);
+  std::string ActivationOp(const std::string &input, const std::string &activationType);  // ReLU, Sigmoid, Tanh
+  // Cached by "inputs->outputs" (:227-268).
+  Result<std::shared_ptr<CompiledOperation>> CompileGraph(const std::vector<std::string> &inputs,
+                                                          const std::vector<std::string> &outputs);
+  // Runs a compiled subgraph: inputs by name (fp32 host tensors, uploaded as needed);
+  // the outputs come back as device-resident tensors by name.
+  Result<std::map<std::string, TensorPtr>> Execute(const CompiledOperation &compiled,
+                                                   const std::map<std::string, Tensor *> &inputs);
+
+ private:
+  struct Node {
+    void *handle;
+    std::vector<int> shape;
+    bool half;
+  };
+  void *graph_ = nullptr;
+  std::mutex mu_;
+  std::map<std::string, Node> tensors_;
+  std::map<std::string, std::shared_ptr<CompiledOperation>> compiled_;
+  const Node &node(const std::string &name) const;
+};
 
 // Mixed precision (gpu/matrix/mixed-precision.go).
 using FloatMP16 = uint16_t;

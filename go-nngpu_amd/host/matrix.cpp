@@ -5,6 +5,8 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
 
 #include "../../include/gonngpu.h"
 #include "gometal.hpp"
@@ -73,6 +75,11 @@ Result<TensorPtr> Transpose(Tensor &A) {
   if (rc != 0) return {nullptr, op_error("GPU matrix transpose", rc, ce)};
   return {result, {}};
 }
+
+namespace {
+void *g_matrix_device = nullptr;
+}
+void SetGlobalMatrixDevice(void *device) { g_matrix_device = device; }
 
 std::string String(ActivationType t) {
   switch (t) {
@@ -334,6 +341,56 @@ Result<SparseTensorPtr> SparseTranspose(const SparseTensor &A) {  // sparse-matr
 }
 
 // ------------------------------------------------------------------ fused linear
+namespace {
+const FusedLinearConfig *linear_config(const std::any &config, bool &ok) {
+  ok = true;
+  if (auto p = std::any_cast<FusedLinearConfig *>(&config)) return *p;
+  if (auto q = std::any_cast<const FusedLinearConfig *>(&config)) return *q;
+  ok = false;
+  return nullptr;
+}
+
+struct FusionRegistry {
+  std::mutex mu;
+  std::map<std::string, std::shared_ptr<FusedOperation>> ops;
+  FusionRegistry() { ops["linear_activation"] = std::make_shared<FusedLinearActivation>(); }
+};
+FusionRegistry &registry() {
+  static FusionRegistry r;
+  return r;
+}
+}  // namespace
+
+void RegisterFusedOperation(const std::string &name, std::shared_ptr<FusedOperation> operation) {
+  FusionRegistry &r = registry();
+  std::lock_guard<std::mutex> lk(r.mu);
+  r.ops[name] = std::move(operation);
+}
+
+std::pair<std::shared_ptr<FusedOperation>, bool> GetFusedOperation(const std::string &name) {
+  FusionRegistry &r = registry();
+  std::lock_guard<std::mutex> lk(r.mu);
+  auto it = r.ops.find(name);
+  if (it == r.ops.end()) return {nullptr, false};
+  return {it->second, true};
+}
+
+Result<TensorPtr> FusedLinearActivation::Forward(const std::vector<Tensor *> &inputs, const std::any &config) {
+  bool ok;
+  const FusedLinearConfig *c = linear_config(config, ok);
+  if (!ok) return {nullptr, Errorf("invalid config type for FusedLinearActivation")};
+  return Forward(inputs, c);
+}
+
+Result<std::vector<TensorPtr>> FusedLinearActivation::Backward(Tensor &gradOutput,
+                                                               const std::vector<Tensor *> &savedTensors,
+                                                               const std::any &config) {
+  bool ok;
+  const FusedLinearConfig *c = linear_config(config, ok);
+  if (!ok) return {{}, Errorf("invalid config type for FusedLinearActivation backward")};
+  return Backward(gradOutput, savedTensors, c);
+}
+
 Result<TensorPtr> FusedLinearActivation::Forward(const std::vector<Tensor *> &inputs,
                                                   const FusedLinearConfig *config) {
   if (!config) return {nullptr, Errorf("invalid config type for FusedLinearActivation")};

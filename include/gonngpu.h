@@ -206,6 +206,27 @@ int perform_activation_swish_forward(GPUPtr inputPtr, long size, GPUPtr outputPt
 int perform_activation_gelu_forward(GPUPtr inputPtr, long size, GPUPtr outputPtr, DevicePtr mtlDevicePtr,
                                     CError *err);
 
+/* MPSGraph calls, metal_bridge.h:1800-1826 (placeholders in the reference,
+ * metal_bridge_phase9b.m:82-97, :298-410; Go side gpu/matrix/mps-graph-integration.go).
+ * Here a graph of GEMM and activation nodes compiled into a HIP graph:
+ *  createMPSGraph      a new, empty graph (NULL on failure);
+ *  createMatMulNode    C = A*B of two tensors of the graph (placeholders come from
+ *                      gn_graph_placeholder, nodes from these calls); NULL when the inner
+ *                      dimensions differ or the data types of A and B differ;
+ *  createReLUNode      max(0, x) of an fp32 tensor;
+ *  compileGraph        the whole graph: every placeholder is an input (creation order),
+ *                      every tensor no node reads is an output (creation order); device is
+ *                      ignored (one GPU per process). NULL on failure;
+ *  executeCompiledGraph  inputs / outputs are GPUPtr buffers in those orders; runs on the
+ *                      stream commandBuffer (NULL: the library stream) and returns after it.
+ *                      It reports no error (void, as in the reference): gn_graph_execute does. */
+void *createMPSGraph(void);
+void *createMatMulNode(void *graph, void *inputA, void *inputB);
+void *createReLUNode(void *graph, void *input);
+void *compileGraph(void *graph, void *device);
+void executeCompiledGraph(void *compiledGraph, void *commandBuffer, void **inputs, long numInputs, void **outputs,
+                          long numOutputs);
+
 /* metal_bridge.h:250. */
 void free_c_error_message(char *message);
 
@@ -274,6 +295,26 @@ int gn_activation_backward(const float *grad_out, const float *pre, long rows, l
 int gn_activation_forward(const float *in, float *out, long n, int act, float alpha, void *stream, CError *err);
 /* Row-wise softmax of a row-major [rows, cols] fp32 matrix (Softmax in ActivationForward). */
 int gn_softmax_rows(const float *in, float *out, long rows, long cols, void *stream, CError *err);
+/* Graph extensions (the MPSGraph calls above). gn_graph_placeholder: a rows x cols
+ * input of dtype GN_F32 or GN_F16 (fp16 operands of a MatMul must both be fp16; results
+ * are fp32). gn_graph_matmul: op(A)*op(B) with transposes (mps-graph-integration.go:151-170
+ * passes them; its cgo stub drops them). gn_graph_activation: an element-wise activation
+ * (ActivationType code, not Softmax) of an fp32 tensor. gn_graph_compile: the subgraph
+ * that computes `outputs` from `inputs` (every placeholder it needs must be an input);
+ * a MatMul read only by one activation becomes one GEMM with that activation in its
+ * epilogue. gn_graph_execute: copies the inputs in, replays the HIP graph, copies the
+ * outputs out, synchronises; executions of one compiled graph are serialised.
+ * gn_graph_release: frees a graph or a compiled graph (compiled graphs outlive their
+ * graph). Node calls return NULL on invalid arguments. */
+void *gn_graph_placeholder(void *graph, long rows, long cols, int dtype);
+void *gn_graph_matmul(void *graph, void *inputA, void *inputB, int transA, int transB);
+void *gn_graph_activation(void *graph, void *input, int act, float alpha);
+int gn_graph_compile(void *graph, void *const *inputs, long numInputs, void *const *outputs, long numOutputs,
+                     void **compiled, CError *err);
+int gn_graph_execute(void *compiledGraph, void *stream, GPUPtr const *inputs, long numInputs, GPUPtr const *outputs,
+                     long numOutputs, CError *err);
+void gn_graph_release(void *graphOrCompiled);
+
 int gn_transpose_f32(const float *in, long rows, long cols, float *out, void *stream, CError *err);
 
 /* CSR SpMM on device arrays: C[M,N] = S[M,K] * D[K,N] (ld = row pitch in elements).

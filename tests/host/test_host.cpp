@@ -4,6 +4,8 @@
 //
 //   test_host --cpu   host-only behaviour (no device calls)
 //   test_host --gpu   everything, including the device paths through the C ABI
+#include <algorithm>
+#include <any>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -244,6 +246,19 @@ void TestShapeErrorsBeforeDevice() {
   CHECK_ERR_HAS(f.Forward({a.get()}, &cfg).err, "requires at least input and weight");
 }
 
+void TestFusionRegistry() {
+  auto [op, ok] = matrix::GetFusedOperation("linear_activation");
+  CHECK(ok && op && op->GetName() == "linear_activation");
+  CHECK(op->GetMemorySavings() == 512 * 1024 && op->GetSpeedup() == 1.4f);
+  CHECK(!matrix::GetFusedOperation("attention").second);  // not on this library's path
+  auto x = NewTensor({2, 3}, std::vector<float>(6)).value;
+  auto w = NewTensor({3, 4}, std::vector<float>(12)).value;
+  CHECK_ERR_HAS(op->Forward({x.get(), w.get()}, std::any(42)).err, "invalid config type for FusedLinearActivation");
+  CHECK_ERR_HAS(op->Backward(*x, {x.get(), w.get()}, std::any()).err, "invalid config type for FusedLinearActivation backward");
+  matrix::RegisterFusedOperation("my_linear", std::make_shared<matrix::FusedLinearActivation>());
+  CHECK(matrix::GetFusedOperation("my_linear").second);
+}
+
 // ============================================================== device tests
 void TestActivationForward() {
   // activation_test.go:32-51: ReLU of [-2,-1,0,1,2,3]
@@ -274,6 +289,70 @@ void TestActivationForward() {
   auto s1 = matrix::ActivationForward(*v, matrix::Softmax, 0).value;
   CHECK_NOERR(s1->RetrieveCPU());
   CHECK(rel(s1->Data, std::vector<double>(sm.begin(), sm.begin() + 129)) <= 1e-5);
+}
+
+void TestMPSGraphManager() {
+  const int B = 64, IN = 96, HID = 80, OUT = 48;
+  auto x = NewTensor({B, IN}, uniform((size_t)B * IN, 31)).value;
+  auto w1 = NewTensor({IN, HID}, uniform((size_t)IN * HID, 32)).value;
+  auto w2 = NewTensor({OUT, HID}, uniform((size_t)OUT * HID, 33)).value;  // used transposed
+  matrix::MPSGraphManager g;
+  g.CreateTensor("x", {B, IN}, "float32");
+  g.CreateTensor("w1", {IN, HID}, "float32");
+  g.CreateTensor("w2", {OUT, HID}, "float32");
+  const std::string h = g.MatMulOp("x", "w1", false, false);
+  CHECK(h == "matmul_x_w1");
+  const std::string r = g.ActivationOp(h, "ReLU");  // fused into the first GEMM
+  CHECK(r == "ReLU_matmul_x_w1");
+  const std::string y = g.MatMulOp(r, "w2", false, true);
+  auto [c, err] = g.CompileGraph({"x", "w1", "w2"}, {y});
+  CHECK_NOERR(err);
+  if (!c) return;
+  CHECK(g.CompileGraph({"x", "w1", "w2"}, {y}).value == c);  // cached by key
+  // float64 reference: relu(x w1) w2^T
+  std::vector<double> H = gemm64(x->Data, w1->Data, B, HID, IN);
+  std::vector<float> Hf(H.size());
+  for (size_t i = 0; i < H.size(); ++i) Hf[i] = (float)std::max(0.0, H[i]);
+  std::vector<float> w2t((size_t)HID * OUT);
+  for (int o = 0; o < OUT; ++o)
+    for (int k = 0; k < HID; ++k) w2t[(size_t)k * OUT + o] = w2->Data[(size_t)o * HID + k];
+  for (int rep = 0; rep < 2; ++rep) {  // the second run replays the same HIP graph
+    auto [out, e2] = g.Execute(*c, {{"x", x.get()}, {"w1", w1.get()}, {"w2", w2.get()}});
+    CHECK_NOERR(e2);
+    if (e2) return;
+    tensor::TensorPtr Y = out[y];
+    CHECK(Y && Y->IsOnGPU() && Y->Shape == (std::vector<int>{B, OUT}));
+    CHECK_NOERR(Y->RetrieveCPU());
+    CHECK(rel(Y->Data, gemm64(Hf, w2t, B, OUT, HID)) <= 1e-5);
+  }
+  // fp16 placeholders: sigmoid(f16(a) f16(b)), fp32 accumulation
+  matrix::MPSGraphManager g16;
+  g16.CreateTensor("a", {B, IN}, "float16");
+  g16.CreateTensor("b", {IN, HID}, "float16");
+  const std::string s16 = g16.ActivationOp(g16.MatMulOp("a", "b", false, false), "Sigmoid");
+  auto c16 = g16.CompileGraph({"a", "b"}, {s16}).value;
+  CHECK(c16);
+  if (c16) {
+    auto o16 = g16.Execute(*c16, {{"a", x.get()}, {"b", w1.get()}}).value;
+    tensor::TensorPtr S = o16[s16];
+    CHECK(S);
+    if (S) {
+      CHECK_NOERR(S->RetrieveCPU());
+      auto r16 = [](const std::vector<float> &v) {
+        std::vector<float> o(v.size());
+        for (size_t i = 0; i < v.size(); ++i) o[i] = orc_f16_to_f32(orc_f32_to_f16_rne(v[i]));
+        return o;
+      };
+      std::vector<double> P = gemm64(r16(x->Data), r16(w1->Data), B, HID, IN);
+      for (double &v : P) v = orc_act_f64(matrix::Sigmoid, 0.0, v);
+      CHECK(rel(S->Data, P) <= 1e-5);
+    }
+  }
+  CHECK_PANICS(g.ActivationOp(h, "Softplus"));
+  CHECK_PANICS(g.MatMulOp("x", "x", false, false));
+  CHECK_PANICS(g.MatMulOp("x", "nope", false, false));
+  CHECK_ERR_HAS(g.CompileGraph({"x"}, {y}).err, "is needed but not an input");
+  CHECK_ERR_HAS(g.Execute(*c, {{"x", x.get()}}).err, "missing input w1");
 }
 
 void TestMatMul() {
@@ -428,6 +507,26 @@ void TestFusedLinearActivation() {
 // FusedLinearActivation.Backward (fused-operations.go:467-578) against the float64
 // restatement: G = dY * act'(pre) * scale, grad_input = G W^T, grad_weight = X^T G,
 // grad_bias = column sums of G (shape [1, out]).
+void TestFusedOperationInterface() {
+  const int B = 33, IN = 70, OUT = 50;
+  auto x = NewTensor({B, IN}, uniform((size_t)B * IN, 21)).value;
+  auto w = NewTensor({IN, OUT}, uniform((size_t)IN * OUT, 22)).value;
+  auto b = NewTensor({OUT}, uniform(OUT, 23)).value;
+  matrix::FusedLinearConfig cfg;
+  cfg.Bias = true;
+  cfg.Activation = std::make_shared<matrix::FusedActivationConfig>();
+  cfg.Activation->ActivationType = matrix::GELU;
+  auto op = matrix::GetFusedOperation("linear_activation").first;
+  auto y1 = op->Forward({x.get(), w.get(), b.get()}, std::any(&cfg)).value;
+  matrix::FusedLinearActivation direct;
+  auto y2 = direct.Forward({x.get(), w.get(), b.get()}, &cfg).value;
+  CHECK(y1 && y2);
+  if (!y1 || !y2) return;
+  CHECK_NOERR(y1->RetrieveCPU());
+  CHECK_NOERR(y2->RetrieveCPU());
+  CHECK(y1->Data == y2->Data);
+}
+
 void TestFusedLinearBackward() {
   const int batch = 33, in = 50, out = 70;
   auto X = NewTensor({batch, in}, uniform((size_t)batch * in, 21)).value;
@@ -696,7 +795,9 @@ int main(int argc, char **argv) {
       {"TestGonumDense", TestGonumDense, false},
       {"TestGPUSparseAtAndErrors", TestGPUSparseAtAndErrors, false},
       {"TestShapeErrorsBeforeDevice", TestShapeErrorsBeforeDevice, false},
+      {"TestFusionRegistry", TestFusionRegistry, false},
       {"TestActivationForward", TestActivationForward, true},
+      {"TestMPSGraphManager", TestMPSGraphManager, true},
       {"TestMatMul", TestMatMul, true},
       {"TestResidencyReuploadsHostWrites", TestResidencyReuploadsHostWrites, true},
       {"TestMemoryStatsTrackTensors", TestMemoryStatsTrackTensors, true},
@@ -704,6 +805,7 @@ int main(int argc, char **argv) {
       {"TestOptimizedGEMMAndBatch", TestOptimizedGEMMAndBatch, true},
       {"TestSparseMatMulAndMatVec", TestSparseMatMulAndMatVec, true},
       {"TestFusedLinearActivation", TestFusedLinearActivation, true},
+      {"TestFusedOperationInterface", TestFusedOperationInterface, true},
       {"TestFusedLinearBackward", TestFusedLinearBackward, true},
       {"TestMatMulBackward", TestMatMulBackward, true},
       {"TestForwardFloat16", TestForwardFloat16, true},

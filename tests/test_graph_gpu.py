@@ -73,3 +73,79 @@ def test_graph_replays_match_eager(dev):
             same = torch.equal(gt, ref)
             _say("replay", rep, name, "bit-identical" if same else "DIFFERS")
             assert same, (rep, name)
+
+
+def _ptrs(*bufs):
+    import ctypes
+
+    return (ctypes.c_void_p * len(bufs))(*[b.handle.value for b in bufs])
+
+
+def test_mpsgraph_abi_matmul_relu_chain(dev):
+    """createMPSGraph / createMatMulNode / createReLUNode / compileGraph /
+    executeCompiledGraph (metal_bridge.h:1800-1826): Y = relu(X W1) W2 (the MatMul + ReLU
+    pair runs as one GEMM with a ReLU epilogue) against float64, executed twice with new
+    inputs through the same compiled HIP graph."""
+    L = G.load()
+    g = L.createMPSGraph()
+    assert g
+    X = L.gn_graph_placeholder(g, 70, 96, G.GN_F32)
+    W1 = L.gn_graph_placeholder(g, 96, 130, G.GN_F32)
+    W2 = L.gn_graph_placeholder(g, 130, 40, G.GN_F32)
+    y = L.createMatMulNode(g, L.createReLUNode(g, L.createMatMulNode(g, X, W1)), W2)
+    assert y
+    assert not L.createMatMulNode(g, X, W2)  # inner dimensions 96 and 130
+    c = L.compileGraph(g, None)
+    assert c
+    rng = np.random.default_rng(71)
+    for rep in range(2):
+        x = rng.standard_normal((70, 96)).astype(np.float32)
+        w1 = rng.standard_normal((96, 130)).astype(np.float32)
+        w2 = rng.standard_normal((130, 40)).astype(np.float32)
+        bx, b1, b2, by = G.Buffer.from_array(x), G.Buffer.from_array(w1), G.Buffer.from_array(w2), G.Buffer(70 * 40 * 4)
+        L.executeCompiledGraph(c, None, _ptrs(bx, b1, b2), 3, _ptrs(by), 1)
+        h = np.maximum(x.astype(np.float64) @ w1, 0.0).astype(np.float32)
+        err = O.rel_frob(by.to_array((70, 40)), h.astype(np.float64) @ w2)
+        _say("mpsgraph chain", rep, err)
+        assert err <= 1e-5
+    rc, msg = G.call_rc("gn_graph_execute", c, None, _ptrs(bx), 1, _ptrs(by), 1)
+    assert rc == -1 and "expected 3 inputs" in msg
+    L.gn_graph_release(c)
+    L.gn_graph_release(g)
+
+
+def test_graph_subgraph_fp16_transposed_gelu(dev):
+    """gn_graph_compile of a subgraph: GELU(A16 * B16^T) with fp16 placeholders and a
+    transposed B, plus a second output (the unfused MatMul result read twice)."""
+    import ctypes
+
+    L = G.load()
+    g = L.createMPSGraph()
+    A = L.gn_graph_placeholder(g, 300, 256, G.GN_F16)
+    B = L.gn_graph_placeholder(g, 520, 256, G.GN_F16)
+    unused = L.gn_graph_placeholder(g, 8, 8, G.GN_F32)
+    m = L.gn_graph_matmul(g, A, B, 0, 1)
+    act = L.gn_graph_activation(g, m, G.ACT_GELU, 0.0)
+    tanh = L.gn_graph_activation(g, m, G.ACT_TANH, 0.0)
+    assert m and act and tanh
+    assert not L.gn_graph_activation(g, A, G.ACT_RELU, 0.0)  # fp16 tensors only feed MatMuls
+    comp = ctypes.c_void_p()
+    ins = (ctypes.c_void_p * 3)(A, B, unused)
+    outs = (ctypes.c_void_p * 2)(act, tanh)
+    G.call("gn_graph_compile", g, ins, 3, outs, 2, ctypes.byref(comp))
+    rng = np.random.default_rng(73)
+    a = rng.standard_normal((300, 256)).astype(np.float32)
+    b = (0.1 * rng.standard_normal((520, 256))).astype(np.float32)
+    a16, b16 = a.astype(np.float16), b.astype(np.float16)
+    ba, bb = G.Buffer(data=a16.view(np.uint16)), G.Buffer(data=b16.view(np.uint16))
+    bu, bo1, bo2 = G.Buffer(8 * 8 * 4), G.Buffer(300 * 520 * 4), G.Buffer(300 * 520 * 4)
+    G.call("gn_graph_execute", comp.value, None, _ptrs(ba, bb, bu), 3, _ptrs(bo1, bo2), 2)
+    pre = a16.astype(np.float64) @ b16.astype(np.float64).T
+    e1 = O.rel_frob(bo1.to_array((300, 520)), O.act_f64(G.ACT_GELU, pre))
+    e2 = O.rel_frob(bo2.to_array((300, 520)), np.tanh(pre))
+    _say("graph fp16 gelu / tanh", e1, e2)
+    assert e1 <= 1e-5 and e2 <= 1e-5
+    rc, msg = G.call_rc("gn_graph_compile", g, ins, 1, outs, 1, ctypes.byref(comp))
+    assert rc == -1 and "needed but not an input" in msg
+    L.gn_graph_release(comp.value)
+    L.gn_graph_release(g)
