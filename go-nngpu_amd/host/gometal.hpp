@@ -61,6 +61,8 @@ class Tensor;
 class SparseTensor;
 using TensorPtr = std::shared_ptr<Tensor>;
 using SparseTensorPtr = std::shared_ptr<SparseTensor>;
+class Float16Tensor;
+using Float16TensorPtr = std::shared_ptr<Float16Tensor>;
 
 // GetGlobalMemoryStats (tensor/tensor.go:74-77): bytes held by tensors' device
 // copies, the peak of that, and the number of live allocations.
@@ -101,6 +103,30 @@ class Tensor {
   long gpuBytes_ = 0;
   void dropDeviceCopy();
 };
+
+// A device-resident fp16 matrix with no host copy: the fp16 data type of the chaining
+// path. Operands converted once (weights, typically) are reused by every fp16 GEMM
+// (MixedPrecisionTrainer::ForwardFloat16, matrix::MatMulFloat16) without another upload
+// or cast. FromTensor converts an fp32 tensor on the device, with the reference's
+// truncation (Float32ToFloatMP16, gpu/matrix/mixed-precision.go:106-151) by default or
+// with IEEE round-to-nearest-even.
+class Float16Tensor {
+ public:
+  std::vector<int> Shape;
+
+  Float16Tensor(const Float16Tensor &) = delete;
+  Float16Tensor &operator=(const Float16Tensor &) = delete;
+  ~Float16Tensor();
+  static Result<Float16TensorPtr> FromTensor(Tensor &t, bool truncate = true);
+  const void *DeviceData() const { return data_; }
+  long Size() const;
+  Result<TensorPtr> ToFloat32() const;  // exact fp16 -> fp32 widening, device-resident
+
+ private:
+  Float16Tensor() = default;
+  void *data_ = nullptr;
+};
+
 
 // NewTensor (tensor.go:90-109): len(data) must equal the product of shape.
 Result<TensorPtr> NewTensor(std::vector<int> shape, std::vector<float> data);
@@ -213,6 +239,10 @@ void SetGlobalMatrixDevice(void *device);
 // Dense ops (gpu/matrix/matrix.go:53-105, :357-404).
 Result<TensorPtr> MatMul(Tensor &A, Tensor &B);
 Result<TensorPtr> Transpose(Tensor &A);
+
+// C = A * B of two device fp16 matrices (fp16 MFMA, fp32 accumulation), device-resident
+// fp32 result: chained fp16 GEMMs without host round trips or casts of their operands.
+Result<TensorPtr> MatMulFloat16(const tensor::Float16Tensor &A, const tensor::Float16Tensor &B);
 
 // Custom-kernel GEMMs (gpu/matrix/optimized-kernels.go:21-75, :78-135).
 Result<TensorPtr> OptimizedGEMM(Tensor &A, Tensor &B, float alpha, float beta);
@@ -366,6 +396,9 @@ class MixedPrecisionTrainer {
   // broadcast over rows (bias length must equal the output width). Runs the cast and
   // an fp16 MFMA GEMM (exact fp16 products, fp32 accumulation) on the device.
   Result<TensorPtr> ForwardFloat16(Tensor &input, Tensor &weights, Tensor *bias);
+  // The same product with weights already converted (Float16Tensor::FromTensor with the
+  // default truncation): bit-identical to the call above, without the weights' cast.
+  Result<TensorPtr> ForwardFloat16(Tensor &input, const tensor::Float16Tensor &weights, Tensor *bias);
   float GetCurrentLossScale() const { return currentLossScale_; }
 
  private:

@@ -584,41 +584,84 @@ Result<TensorPtr> MixedPrecisionTrainer::ConvertTensorToFloat16(const Tensor &in
   return {t, {}};
 }
 
-Result<TensorPtr> MixedPrecisionTrainer::ForwardFloat16(Tensor &input, Tensor &weights, Tensor *bias) {
-  if (!config_->Enabled) return MatMul(input, weights);
-  if (input.Shape.size() != 2 || weights.Shape.size() != 2) return {nullptr, Errorf("MatMul requires 2D tensors (matrices)")};
-  const long M = input.Shape[0], K = input.Shape[1], N = weights.Shape[1];
-  if (weights.Shape[0] != K)
-    return {nullptr, Errorf("incompatible matrix dimensions for multiplication: A columns (%ld) != B rows (%d)", K,
-                            weights.Shape[0])};
+namespace {
+// input (rounded to fp16 by truncation on the device) x w16 [K, N] (device fp16), plus
+// the fp16-rounded bias in the GEMM epilogue; device-resident fp32 result.
+Result<TensorPtr> forward_f16(Tensor &input, const void *w16, long K, long N, Tensor *bias) {
+  const long M = input.Shape[0];
   if (bias && bias->Size() != N)
     return {nullptr, Errorf("bias length (%ld) must equal the output width (%ld)", bias->Size(), N)};
   if (Error e = input.EnsureGPU()) return {nullptr, wrap("failed to convert input to float16", e)};
-  if (Error e = weights.EnsureGPU()) return {nullptr, wrap("failed to convert weights to float16", e)};
   if (bias)
     if (Error e = bias->EnsureGPU()) return {nullptr, wrap("failed to convert bias to float16", e)};
   auto [result, rerr] = Tensor::NewDeviceResult({(int)M, (int)N});
   if (rerr) return {nullptr, wrap("failed to perform float16 matrix multiplication", rerr)};
-  DeviceScratch a16, w16, b16, bf;
+  DeviceScratch a16, b16, bf;
   if (Error e = a16.alloc((size_t)(M * K) * 2)) return {nullptr, e};
-  if (Error e = w16.alloc((size_t)(K * N) * 2)) return {nullptr, e};
   if (bias) {
     if (Error e = b16.alloc((size_t)N * 2)) return {nullptr, e};
     if (Error e = bf.alloc((size_t)N * 4)) return {nullptr, e};
   }
   CError ce{nullptr};
   int rc = gn_cast_f32_f16(dptr(input), (uint16_t *)a16.p, (size_t)(M * K), GN_ROUND_TOWARD_ZERO, nullptr, &ce);
-  if (rc == 0) rc = gn_cast_f32_f16(dptr(weights), (uint16_t *)w16.p, (size_t)(K * N), GN_ROUND_TOWARD_ZERO, nullptr, &ce);
   if (rc == 0 && bias) {
     rc = gn_cast_f32_f16(dptr(*bias), (uint16_t *)b16.p, (size_t)N, GN_ROUND_TOWARD_ZERO, nullptr, &ce);
     if (rc == 0) rc = gn_cast_f16_f32((const uint16_t *)b16.p, (float *)bf.p, (size_t)N, nullptr, &ce);
   }
   if (rc == 0)
-    rc = gn_gemm(GN_F16, 0, 0, M, N, K, 1.0f, a16.p, K, 0, w16.p, N, 0, 0.0f, dptr(*result), N, 0, 1,
+    rc = gn_gemm(GN_F16, 0, 0, M, N, K, 1.0f, a16.p, K, 0, w16, N, 0, 0.0f, dptr(*result), N, 0, 1,
                  bias ? (const float *)bf.p : nullptr, GN_ACT_NONE, 0.0f, nullptr, &ce);
   if (rc == 0) rc = gn_synchronize(nullptr, &ce);
   if (rc != 0) return {nullptr, op_error("float16 matrix multiplication", rc, ce)};
   return {result, {}};
+}
+}  // namespace
+
+Result<TensorPtr> MixedPrecisionTrainer::ForwardFloat16(Tensor &input, Tensor &weights, Tensor *bias) {
+  if (!config_->Enabled) return MatMul(input, weights);
+  if (input.Shape.size() != 2 || weights.Shape.size() != 2) return {nullptr, Errorf("MatMul requires 2D tensors (matrices)")};
+  const long K = input.Shape[1], N = weights.Shape[1];
+  if (weights.Shape[0] != K)
+    return {nullptr, Errorf("incompatible matrix dimensions for multiplication: A columns (%ld) != B rows (%d)", K,
+                            weights.Shape[0])};
+  if (Error e = weights.EnsureGPU()) return {nullptr, wrap("failed to convert weights to float16", e)};
+  DeviceScratch w16;
+  if (Error e = w16.alloc((size_t)(K * N) * 2)) return {nullptr, e};
+  CError ce{nullptr};
+  if (int rc = gn_cast_f32_f16(dptr(weights), (uint16_t *)w16.p, (size_t)(K * N), GN_ROUND_TOWARD_ZERO, nullptr, &ce))
+    return {nullptr, op_error("float16 matrix multiplication", rc, ce)};
+  return forward_f16(input, w16.p, K, N, bias);
+}
+
+Result<TensorPtr> MixedPrecisionTrainer::ForwardFloat16(Tensor &input, const tensor::Float16Tensor &weights,
+                                                        Tensor *bias) {
+  if (input.Shape.size() != 2 || weights.Shape.size() != 2) return {nullptr, Errorf("MatMul requires 2D tensors (matrices)")};
+  const long K = input.Shape[1], N = weights.Shape[1];
+  if (weights.Shape[0] != K)
+    return {nullptr, Errorf("incompatible matrix dimensions for multiplication: A columns (%ld) != B rows (%d)", K,
+                            weights.Shape[0])};
+  if (!config_->Enabled) {  // fp32 MatMul of the (already rounded) weights, as the reference's disabled path
+    auto [w32, err] = weights.ToFloat32();
+    if (err) return {nullptr, err};
+    return MatMul(input, *w32);
+  }
+  return forward_f16(input, weights.DeviceData(), K, N, bias);
+}
+
+Result<TensorPtr> MatMulFloat16(const tensor::Float16Tensor &A, const tensor::Float16Tensor &B) {
+  if (A.Shape.size() != 2 || B.Shape.size() != 2) return {nullptr, Errorf("MatMul requires 2D tensors (matrices)")};
+  const long M = A.Shape[0], K = A.Shape[1], N = B.Shape[1];
+  if (B.Shape[0] != K)
+    return {nullptr, Errorf("incompatible matrix dimensions for multiplication: A columns (%ld) != B rows (%d)", K,
+                            B.Shape[0])};
+  auto [C, err] = Tensor::NewDeviceResult({(int)M, (int)N});
+  if (err) return {nullptr, wrap("failed to create result tensor", err)};
+  CError ce{nullptr};
+  int rc = gn_gemm(GN_F16, 0, 0, M, N, K, 1.0f, A.DeviceData(), K, 0, B.DeviceData(), N, 0, 0.0f, dptr(*C), N, 0, 1,
+                   nullptr, GN_ACT_NONE, 0.0f, nullptr, &ce);
+  if (rc == 0) rc = gn_synchronize(nullptr, &ce);
+  if (rc != 0) return {nullptr, op_error("float16 matrix multiplication", rc, ce)};
+  return {C, {}};
 }
 
 // ------------------------------------------------------------------ LinearLayer

@@ -158,6 +158,46 @@ void Tensor::ReleaseGPU() {
   if (isOnGPU_ && gpuPtr_ && isOwner_) dropDeviceCopy();
 }
 
+// ------------------------------------------------------------------ Float16Tensor
+Float16Tensor::~Float16Tensor() {
+  if (data_) gn_free(data_);
+}
+
+long Float16Tensor::Size() const {
+  long n = 1;
+  for (int d : Shape) n *= d;
+  return n;
+}
+
+Result<Float16TensorPtr> Float16Tensor::FromTensor(Tensor &t, bool truncate) {
+  Float16TensorPtr h(new Float16Tensor());
+  h->Shape = t.Shape;
+  const long n = t.Size();
+  if (Error e = t.EnsureGPU()) return {nullptr, e};
+  CError ce{nullptr};
+  int rc = n > 0 ? gn_malloc(&h->data_, (size_t)n * 2, &ce) : 0;
+  if (rc == 0 && n > 0)
+    rc = gn_cast_f32_f16(static_cast<const float *>(gn_buffer_device_ptr(t.GPUPtr())),
+                         static_cast<uint16_t *>(h->data_), (size_t)n,
+                         truncate ? GN_ROUND_TOWARD_ZERO : GN_ROUND_NEAREST_EVEN, nullptr, &ce);
+  if (rc == 0) rc = gn_synchronize(nullptr, &ce);
+  if (rc != 0) return {nullptr, abi_error("float16 conversion", rc, ce)};
+  return {h, {}};
+}
+
+Result<TensorPtr> Float16Tensor::ToFloat32() const {
+  auto [t, err] = Tensor::NewDeviceResult(Shape);
+  if (err) return {nullptr, err};
+  CError ce{nullptr};
+  int rc = Size() > 0 ? gn_cast_f16_f32(static_cast<const uint16_t *>(data_),
+                                        static_cast<float *>(gn_buffer_device_ptr(t->GPUPtr())), (size_t)Size(),
+                                        nullptr, &ce)
+                      : 0;
+  if (rc == 0) rc = gn_synchronize(nullptr, &ce);
+  if (rc != 0) return {nullptr, abi_error("float16 widening", rc, ce)};
+  return {t, {}};
+}
+
 // ------------------------------------------------------------------ SparseTensor
 std::string String(SparseFormat f) {
   switch (f) {

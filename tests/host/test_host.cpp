@@ -625,6 +625,46 @@ void TestForwardFloat16() {
   CHECK_ERR_HAS(mp->ForwardFloat16(*X, *W, wrong.get()).err, "bias length");
 }
 
+void TestFloat16Chaining() {
+  const int M = 70, K = 136, N = 90;
+  auto X = NewTensor({M, K}, uniform((size_t)M * K, 41)).value;
+  auto W = NewTensor({K, N}, uniform((size_t)K * N, 42, -0.05f, 0.05f)).value;
+  auto b = NewTensor({N}, uniform(N, 43, -0.01f, 0.01f)).value;
+  auto mp = matrix::NewMixedPrecisionTrainer(nullptr).value;
+  auto [W16, werr] = tensor::Float16Tensor::FromTensor(*W);  // the reference's truncation
+  CHECK_NOERR(werr);
+  if (!W16) return;
+  // reusing the converted weights gives the same bits as converting them per call
+  auto Y1 = mp->ForwardFloat16(*X, *W, b.get()).value;
+  auto Y2 = mp->ForwardFloat16(*X, *W16, b.get()).value;
+  CHECK(Y1 && Y2);
+  if (!Y1 || !Y2) return;
+  CHECK_NOERR(Y1->RetrieveCPU());
+  CHECK_NOERR(Y2->RetrieveCPU());
+  CHECK(Y1->Data == Y2->Data);
+  // widening is exact: the truncated values of Float32ToFloatMP16
+  auto W32 = W16->ToFloat32().value;
+  CHECK_NOERR(W32->RetrieveCPU());
+  bool same = true;
+  for (size_t i = 0; i < W->Data.size(); ++i)
+    same &= W32->Data[i] == matrix::FloatMP16ToFloat32(matrix::Float32ToFloatMP16(W->Data[i]));
+  CHECK(same);
+  // a chained fp16 product from round-to-nearest conversions
+  auto X16 = tensor::Float16Tensor::FromTensor(*X, false).value;
+  auto Wn16 = tensor::Float16Tensor::FromTensor(*W, false).value;
+  auto C = matrix::MatMulFloat16(*X16, *Wn16).value;
+  CHECK(C && C->IsOnGPU());
+  if (!C) return;
+  CHECK_NOERR(C->RetrieveCPU());
+  auto rne = [](const std::vector<float> &v) {
+    std::vector<float> o(v.size());
+    for (size_t i = 0; i < v.size(); ++i) o[i] = orc_f16_to_f32(orc_f32_to_f16_rne(v[i]));
+    return o;
+  };
+  CHECK(rel(C->Data, gemm64(rne(X->Data), rne(W->Data), M, N, K)) <= 1e-5);
+  CHECK_ERR_HAS(matrix::MatMulFloat16(*W16, *W16).err, "incompatible matrix dimensions");
+}
+
 void TestLinearLayer() {
   auto layer = matrix::NewLinearLayer(50, 30, true, 5);
   for (int j = 0; j < 30; ++j) layer->Bias->Data[j] = 0.01f * (float)j;
@@ -809,6 +849,7 @@ int main(int argc, char **argv) {
       {"TestFusedLinearBackward", TestFusedLinearBackward, true},
       {"TestMatMulBackward", TestMatMulBackward, true},
       {"TestForwardFloat16", TestForwardFloat16, true},
+      {"TestFloat16Chaining", TestFloat16Chaining, true},
       {"TestLinearLayer", TestLinearLayer, true},
       {"TestGPUDenseAndGPUMatMul", TestGPUDenseAndGPUMatMul, true},
       {"TestGPUSparseMatMulAndMatVec", TestGPUSparseMatMulAndMatVec, true},
