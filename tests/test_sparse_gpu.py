@@ -205,3 +205,39 @@ def test_spmv_wave_kernel_empty_rows_and_bad_columns(dev):
     rc, msg = G.call_rc("perform_sparse_matvec", bv.handle, rp.ctypes.data, rp.size, bad.ctypes.data, bad.size, M, K,
                         val.size, bx.handle, K, by.handle, M, None)
     assert rc == -3 and "column" in msg
+
+
+@pytest.mark.parametrize("K,mean", [(20000, 100.0), (70001, 280.0)])
+def test_spmv_long_rows_skew_unsorted_and_errors(dev, K, mean):
+    """Wide x (K = 20000 and 70001) with unsorted columns and duplicates, one row of
+    200000 entries among rows of ~100-280 and 100 empty rows. The device-pointer entry with
+    x 4 bytes past 16-byte alignment gives the same bits; an out-of-range column is
+    reported."""
+    import torch
+
+    rng = np.random.default_rng(K)
+    M = 4096
+    lens = rng.poisson(mean, M).astype(np.int64)
+    lens[100] = 200000
+    lens[500:600] = 0
+    rp = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    col = rng.integers(0, K, int(rp[-1])).astype(np.int32)
+    val = rng.uniform(-1, 1, col.size).astype(np.float32)
+    x = rng.standard_normal(K).astype(np.float32)
+    y = _spmv_abi(rp, col, val, x, M, K)
+    assert np.all(y[500:600] == 0)
+    err = O.rel_frob(y, O.spmv_f64(rp, col, val, x))
+    _say("spmv wide/skewed", K, col.size, err)
+    assert err <= 1e-5
+    d = [torch.from_numpy(a).to(dev) for a in (rp, col, val)]
+    xt = torch.empty(K + 1, dtype=torch.float32, device=dev)
+    xt[1:].copy_(torch.from_numpy(x))
+    yd = torch.empty(M, dtype=torch.float32, device=dev)
+    G.spmv_csr(M, K, val.size, d[0], d[1], d[2], xt[1:], yd)
+    np.testing.assert_array_equal(yd.cpu().numpy(), y)
+    bad = col.copy()
+    bad[rp[7] + 2] = K + 5
+    bv, bx, by = G.Buffer.from_array(val), G.Buffer.from_array(x), G.Buffer(M * 4)
+    rc, msg = G.call_rc("perform_sparse_matvec", bv.handle, rp.ctypes.data, rp.size, bad.ctypes.data, bad.size, M, K,
+                        val.size, bx.handle, K, by.handle, M, None)
+    assert rc == -3 and "column" in msg
