@@ -461,3 +461,36 @@ def test_f16_register_staged_when_ring_offsets_overflow(dev):
     assert same
     ref = a.float() @ b.float()
     assert ((c_wide - ref).norm() / ref.norm()).item() <= 1e-5
+
+
+@pytest.mark.parametrize("tA,tB", VARIANTS)
+def test_f16_ring128_batched_alpha_beta_bias_act(dev, tA, tB):
+    """The 128-wide ring tiles (128x128, or 128x96 when B is K-contiguous) with a batch of
+    2, alpha, beta*C, bias and Leaky ReLU, ragged M and N: every batch against float64 of
+    the fp16-rounded inputs."""
+    import torch
+
+    rng = np.random.default_rng(79)
+    bs, M, N, K = 2, 520, 2000, 264
+    A = rng.standard_normal((bs, M, K)).astype(np.float32)
+    B = (0.05 * rng.standard_normal((bs, K, N))).astype(np.float32)
+    C0 = rng.standard_normal((bs, M, N)).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    As = np.ascontiguousarray(A.transpose(0, 2, 1)) if tA else A
+    Bs = np.ascontiguousarray(B.transpose(0, 2, 1)) if tB else B
+    a16 = torch.from_numpy(As).to(dev).half()
+    b16 = torch.from_numpy(Bs).to(dev).half()
+    C = torch.from_numpy(C0).to(dev)
+    G.gemm(a16, b16, C, transA=tA, transB=tB, M=M, N=N, K=K, batch=bs, strideA=M * K, strideB=K * N,
+           strideC=M * N, alpha=0.75, beta=-0.5, bias=torch.from_numpy(bias).to(dev), act=G.ACT_LEAKY_RELU,
+           act_alpha=0.1)
+    Cn = C.cpu().numpy()
+    Ar = a16.float().cpu().numpy()
+    Br = b16.float().cpu().numpy()
+    for z in range(bs):
+        Az = Ar[z].T if tA else Ar[z]
+        Bz = Br[z].T if tB else Br[z]
+        pre = 0.75 * (Az.astype(np.float64) @ Bz.astype(np.float64)) - 0.5 * C0[z] + bias
+        err = O.rel_frob(Cn[z], O.act_f64(G.ACT_LEAKY_RELU, pre, 0.1))
+        _say("ring128 epilogue", tA, tB, z, err)
+        assert err <= 1e-5, (z, err)
