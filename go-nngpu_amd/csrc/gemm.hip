@@ -791,21 +791,21 @@ hipError_t pick_f32(const GemmParams &p, long batch, hipStream_t s) {
 }
 
 template <bool VEC>
-hipError_t dispatch(const GemmDesc &d, const GemmParams &p, hipStream_t s) {
+hipError_t dispatch(const GemmDesc &d, const GemmParams &p, long batch, hipStream_t s) {
   const int v = (d.ta ? 2 : 0) | (d.tb ? 1 : 0);
   if (d.dtype == GN_F16) {
     switch (v) {
-      case 0: return pick_f16<false, false, VEC>(p, d.batch, s);
-      case 1: return pick_f16<false, true, VEC>(p, d.batch, s);
-      case 2: return pick_f16<true, false, VEC>(p, d.batch, s);
-      default: return pick_f16<true, true, VEC>(p, d.batch, s);
+      case 0: return pick_f16<false, false, VEC>(p, batch, s);
+      case 1: return pick_f16<false, true, VEC>(p, batch, s);
+      case 2: return pick_f16<true, false, VEC>(p, batch, s);
+      default: return pick_f16<true, true, VEC>(p, batch, s);
     }
   }
   switch (v) {
-    case 0: return pick_f32<false, false, VEC>(p, d.batch, s);
-    case 1: return pick_f32<false, true, VEC>(p, d.batch, s);
-    case 2: return pick_f32<true, false, VEC>(p, d.batch, s);
-    default: return pick_f32<true, true, VEC>(p, d.batch, s);
+    case 0: return pick_f32<false, false, VEC>(p, batch, s);
+    case 1: return pick_f32<false, true, VEC>(p, batch, s);
+    case 2: return pick_f32<true, false, VEC>(p, batch, s);
+    default: return pick_f32<true, true, VEC>(p, batch, s);
   }
 }
 
@@ -838,7 +838,6 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
   const long b_rows = d.tb ? d.N : d.K, b_cols = d.tb ? d.K : d.N;
   if ((d.K > 0 && (d.lda < a_cols || d.ldb < b_cols)) || d.ldc < d.N)
     return set_error(err, -1, "gemm: leading dimension smaller than row length");
-  if (d.batch > 65535) return set_error(err, -1, "gemm: batch %ld exceeds 65535", d.batch);
   (void)a_rows; (void)b_rows;
   const long tiles = ((d.M + 63) / 64) * ((d.N + 63) / 64);
   if (tiles > (1L << 30)) return set_error(err, -1, "gemm: problem too large for the grid");
@@ -865,7 +864,18 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
     const long a_contig = d.ta ? d.M : d.K, b_contig = d.tb ? d.K : d.N;
     const bool vec = aligned(d.A, d.lda, d.strideA) && aligned(d.B, d.ldb, d.strideB) && a_contig % epv == 0 &&
                      b_contig % epv == 0;
-    e = vec ? dispatch<true>(d, p, s) : dispatch<false>(d, p, s);
+    // The batch index is blockIdx.z (at most 65535 per launch): larger batches run as
+    // consecutive launches over chunks of the batch, each with offset operands.
+    constexpr long kMaxZ = 65535;
+    e = hipSuccess;
+    for (long z0 = 0; z0 < d.batch && e == hipSuccess; z0 += kMaxZ) {
+      GemmParams q = p;
+      q.A = static_cast<const char *>(d.A) + z0 * d.strideA * (long)esz;
+      q.B = static_cast<const char *>(d.B) + z0 * d.strideB * (long)esz;
+      q.C = d.C + z0 * d.strideC;
+      const long nb = std::min(kMaxZ, d.batch - z0);
+      e = vec ? dispatch<true>(d, q, nb, s) : dispatch<false>(d, q, nb, s);
+    }
   }
   if (e != hipSuccess) return hip_error(err, -6, "gemm launch", e);
   return 0;

@@ -494,3 +494,25 @@ def test_f16_ring128_batched_alpha_beta_bias_act(dev, tA, tB):
         err = O.rel_frob(Cn[z], O.act_f64(G.ACT_LEAKY_RELU, pre, 0.1))
         _say("ring128 epilogue", tA, tB, z, err)
         assert err <= 1e-5, (z, err)
+
+
+def test_batch_beyond_one_launch(dev):
+    """70000 small problems (more than the 65535 batches of one launch's grid.z): the
+    launcher runs chunks with offset operands; every problem matches float64 and the
+    chunk boundary (problems 65534..65536) is exact for small integers."""
+    import torch
+
+    rng = np.random.default_rng(83)
+    bs, M, N, K = 70000, 5, 3, 4
+    A = rng.integers(-4, 5, size=(bs, M, K)).astype(np.float32)
+    B = rng.integers(-4, 5, size=(bs, K, N)).astype(np.float32)
+    ad, bd = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
+    C = torch.full((bs, M, N), float("nan"), device=dev)
+    G.gemm(ad, bd, C, batch=bs, strideA=M * K, strideB=K * N, strideC=M * N)
+    got = C.cpu().numpy()
+    ref = np.einsum("bmk,bkn->bmn", A.astype(np.float64), B.astype(np.float64))
+    np.testing.assert_array_equal(got, ref)  # small integers: exact in fp32
+    a16, b16 = ad.half(), bd.half()
+    C16 = torch.full((bs, M, N), float("nan"), device=dev)
+    G.gemm(a16, b16, C16, batch=bs, strideA=M * K, strideB=K * N, strideC=M * N)
+    np.testing.assert_array_equal(C16.cpu().numpy(), ref)
