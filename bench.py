@@ -21,7 +21,11 @@ profiles/traffic.json when that file holds an entry for the kernel, else null.
 cpu_baseline: the oracle's float64 GEMM (a restatement of gonum Dense.Mul
 semantics) on a bounded row sample of the headline problem, on the host cores.
 
-`--only a,b,...` runs a subset of {c3, c2, c4, spmm, spmv, copy} (used by the
+`e2e` (in `secondary`, never `value`): the headline GEMM from host memory through the
+C ABI, PCIe included: upload fp32 A and B (create_gpu_buffer), cast both to fp16 on
+the device, GEMM, download C (retrieve_gpu_buffer_data), wall-clock per step.
+
+`--only a,b,...` runs a subset of {c3, c2, c4, spmm, spmv, e2e, copy} (used by the
 rocprofv3 passes that produce profiles/); `copy` is a 1 GiB device copy used to
 calibrate the HBM byte counters.
 """
@@ -40,7 +44,7 @@ METRIC = "GEMM TFLOP/s + % MFMA peak (fp32, fp16→fp32); CSR SpMM HBM GB/s, 1 M
 PEAK_F16_TFLOPS = 2516.6  # dense MFMA fp16, 256 CU x 4096 flop/clk x 2.4 GHz
 PEAK_F32_TFLOPS = 157.3   # fp32 MFMA
 PEAK_HBM_GBS = 8000.0
-ALL = ("c3", "c2", "c4", "spmm", "spmv", "copy")
+ALL = ("c3", "c2", "c4", "spmm", "spmv", "e2e", "copy")
 
 
 def log(*a):
@@ -205,6 +209,42 @@ def run_spmv(c, steps, warmup, csr):
             "bytes_streamed": b_s}
 
 
+def run_e2e(c, steps, warmup):
+    """C3 from host fp32 arrays: upload, device fp16 cast, GEMM, download (wall clock)."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    G = c.G
+    n = 8192
+    A = O.normal((n, n), 42, 201)
+    B = O.normal((n, n), 42, 202, 0.0, 0.02)
+    Cout = np.empty((n, n), dtype=np.float32)
+
+    def step():
+        ba, bb = G.Buffer.from_array(A), G.Buffer.from_array(B)
+        a16, b16, bc = G.Buffer(n * n * 2), G.Buffer(n * n * 2), G.Buffer(n * n * 4)
+        G.call("gn_cast_f32_f16", ba.device_ptr, a16.device_ptr, n * n, G.ROUND_NEAREST_EVEN, None)
+        G.call("gn_cast_f32_f16", bb.device_ptr, b16.device_ptr, n * n, G.ROUND_NEAREST_EVEN, None)
+        G.call("gn_gemm", G.GN_F16, 0, 0, n, n, n, 1.0, a16.device_ptr, n, 0, b16.device_ptr, n, 0, 0.0,
+               bc.device_ptr, n, 0, 1, None, G.ACT_NONE, 0.0, None)
+        G.call("retrieve_gpu_buffer_data", bc.handle, Cout.ctypes.data, Cout.nbytes)
+        for b in (ba, bb, a16, b16, bc):
+            b.release()
+
+    for _ in range(warmup):
+        step()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    tf = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+    assert np.isfinite(Cout[:4]).all()
+    log(f"e2e: {ms:.2f} ms per host-to-host 8192^3 fp16 GEMM (PCIe included), {tf:.1f} TFLOP/s")
+    return {"ms": round(ms, 3), "TFLOP/s": round(tf, 1),
+            "steps": f"upload A, B fp32 (256 MiB each), device fp16 cast, GEMM, download C fp32 (256 MiB)"}
+
+
 def run_copy(c, steps, warmup):
     """1 GiB device-to-device copy (torch's copy kernel): calibration for the PMC byte counters."""
     n = 1 << 28
@@ -254,6 +294,9 @@ def main():
         if "spmv" in only:
             secondary["c5_spmv"] = run_spmv(c, steps2 * 4, 5, csr)
         del csr
+        c.torch.cuda.empty_cache()
+    if "e2e" in only:
+        secondary["c3_from_host_buffers"] = run_e2e(c, 3, 1)
         c.torch.cuda.empty_cache()
     if "copy" in only:
         secondary["copy_calibration"] = run_copy(c, steps2, 3)

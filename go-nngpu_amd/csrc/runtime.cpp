@@ -3,7 +3,10 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
+#include <condition_variable>
 #include <mutex>
+#include <thread>
 #include <unordered_map>
 #include <unordered_set>
 #include <vector>
@@ -173,7 +176,79 @@ void memory_stats(long *cur, long *peak, long *n) {
 
 // ------------------------------------------------------------------ staging
 namespace {
-constexpr size_t kStageBytes = 8u << 20;  // two 8 MiB pinned buffers
+constexpr size_t kStageBytes = 32u << 20;  // two 32 MiB pinned buffers
+
+// Host copies between pageable memory and the pinned staging buffers, split over the
+// caller and kCopyWorkers persistent threads: one thread's memcpy runs at ~10-15 GB/s,
+// below what a PCIe Gen5 link carries. Started on first use and never stopped (the
+// threads wait on a condition variable between copies). Used under Staging::mu, so one
+// copy runs at a time.
+constexpr int kCopyWorkers = 4;
+class CopyPool {
+ public:
+  void copy(void *dst, const void *src, size_t n) {
+    if (n < (2u << 20)) {
+      memcpy(dst, src, n);
+      return;
+    }
+    start();
+    constexpr size_t parts = kCopyWorkers + 1;
+    const size_t slice = ((n + parts - 1) / parts + 63) & ~size_t(63);
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      dst_ = static_cast<char *>(dst);
+      src_ = static_cast<const char *>(src);
+      n_ = n;
+      slice_ = slice;
+      pending_ = kCopyWorkers;
+      ++gen_;
+    }
+    cv_.notify_all();
+    memcpy(dst, src, std::min(slice, n));  // slice 0 on the calling thread
+    std::unique_lock<std::mutex> lk(mu_);
+    done_.wait(lk, [&] { return pending_ == 0; });
+  }
+
+ private:
+  void start() {
+    if (started_) return;
+    started_ = true;
+    for (int w = 0; w < kCopyWorkers; ++w) std::thread([this, w] { worker(w + 1); }).detach();
+  }
+  void worker(int part) {
+    uint64_t seen = 0;
+    for (;;) {
+      char *dst;
+      const char *src;
+      size_t n, slice;
+      {
+        std::unique_lock<std::mutex> lk(mu_);
+        cv_.wait(lk, [&] { return gen_ != seen; });
+        seen = gen_;
+        dst = dst_;
+        src = src_;
+        n = n_;
+        slice = slice_;
+      }
+      const size_t off = (size_t)part * slice;
+      if (off < n) memcpy(dst + off, src + off, std::min(slice, n - off));
+      std::lock_guard<std::mutex> lk(mu_);
+      if (--pending_ == 0) done_.notify_one();
+    }
+  }
+  std::mutex mu_;
+  std::condition_variable cv_, done_;
+  char *dst_ = nullptr;
+  const char *src_ = nullptr;
+  size_t n_ = 0, slice_ = 0;
+  int pending_ = 0;
+  uint64_t gen_ = 0;
+  bool started_ = false;
+};
+CopyPool &copy_pool() {
+  static CopyPool *p = new CopyPool();
+  return *p;
+}
 struct Staging {
   std::mutex mu;
   void *buf[2] = {nullptr, nullptr};
@@ -211,7 +286,7 @@ int upload(void *dst_dev, const void *src_host, size_t bytes, hipStream_t s, CEr
       hipError_t e = hipEventSynchronize(st.ev[b]);
       if (e != hipSuccess) return hip_error(err, -4, "upload wait", e);
     }
-    memcpy(st.buf[b], static_cast<const char *>(src_host) + off, n);
+    copy_pool().copy(st.buf[b], static_cast<const char *>(src_host) + off, n);
     hipError_t e = hipMemcpyAsync(static_cast<char *>(dst_dev) + off, st.buf[b], n, hipMemcpyHostToDevice, s);
     if (e != hipSuccess) return hip_error(err, -4, "upload hipMemcpyAsync", e);
     e = hipEventRecord(st.ev[b], s);
@@ -249,7 +324,7 @@ int download(void *dst_host, const void *src_dev, size_t bytes, hipStream_t s, C
       int b = (int)(j & 1);
       hipError_t e = hipEventSynchronize(st.ev[b]);
       if (e != hipSuccess) return hip_error(err, -4, "download wait", e);
-      memcpy(static_cast<char *>(dst_host) + off, st.buf[b], n);
+      copy_pool().copy(static_cast<char *>(dst_host) + off, st.buf[b], n);
     }
   }
   return 0;

@@ -29,9 +29,13 @@ def test_buffer_roundtrip_and_partial_retrieve(dev):
 
 
 def test_large_buffer_crosses_staging_chunks(dev):
-    x = np.random.default_rng(0).standard_normal(5_000_003).astype(np.float32)  # > 2 staging chunks, odd size
-    b = G.Buffer.from_array(x)
-    np.testing.assert_array_equal(b.to_array(x.shape), x)
+    # 80 MB: three 32 MiB staging chunks, each host copy split over the copy threads, odd
+    # size; then 3 MiB + 3 floats (one chunk, split copy with a ragged last slice)
+    for n in (20_000_003, 786_435):
+        x = np.random.default_rng(n).standard_normal(n).astype(np.float32)
+        b = G.Buffer.from_array(x)
+        np.testing.assert_array_equal(b.to_array(x.shape), x)
+        b.release()
 
 
 def test_zero_filled_buffer_and_stats(dev):
