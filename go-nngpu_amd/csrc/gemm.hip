@@ -23,8 +23,6 @@
 //  * a grouped, XCD-aware tile order: hardware dispatches workgroup w to XCD w % 8,
 //    so w is remapped to give each XCD a contiguous band of tiles that share A/B
 //    panels in that XCD's L2.
-#include <utility>
-
 #include "act.h"
 #include "common.h"
 
@@ -55,21 +53,59 @@ struct GemmParams {
 };
 
 // ------------------------------------------------------------------ epilogue
-// Writes one 16x16 MFMA accumulator block (lane l holds rows 4*(l/16)+r, column l%16).
-__device__ __forceinline__ void store_block(const GemmParams &p, float *C, long row0, long col0, float4_t acc) {
-  const int lane = threadIdx.x & 63;
-  const long col = col0 + (lane & 15);
-  if (col >= p.N) return;
-  const float b = p.bias ? p.bias[col] : 0.0f;
+// Writes a workgroup's BM x BN accumulator tile to C in row order. Pass f stages MFMA
+// block-row f of every wave (WM x 16 tile rows, all BN columns) in LDS at `stg` (pitch
+// BN + 4 floats: the 4 row groups of one ds_write_b32 fall on distinct banks), then the
+// workgroup stores those rows as 16-byte vectors with consecutive lanes along a row, so
+// each store instruction writes long contiguous row segments (one whole 1 KiB row at
+// BN = 256). All CUs write their tiles at about the same time; when each wave stored
+// only its own 256-byte row pieces (rows 32 KiB apart), the writes drained so slowly
+// that the 8192^3 GEMM took 11% longer (4096^3: 17%). alpha, beta*C, bias and the
+// activation are applied on the way; scalar stores at ragged edges or when ldc / C do
+// not allow aligned 16-byte stores. The pass loop is unrolled so every accumulator index
+// is static (a runtime index would move the accumulators to scratch memory).
+template <int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void store_tile_rows(const GemmParams &p, long m0, long n0, long z, float *stg,
+                                                const float4_t (&acc)[BM / WM / 16][BN / WN / 16]) {
+  constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 16, FN = WTN / 16;
+  constexpr int LP = BN + 4, CPR = BN / 4, NTH = WM * WN * 64;
+  static_assert(BN % 4 == 0, "row vectors");
+  const int wave = threadIdx.x >> 6, wm = wave / WN, wn = wave % WN, lane = threadIdx.x & 63;
+  const int c = lane & 15, g = lane >> 4;
+  float *C = p.C + z * p.strideC;
+  const bool vec_ok = (p.ldc % 4 == 0) && (((uintptr_t)C & 15) == 0);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const long row = row0 + 4 * (lane >> 4) + r;
-    if (row < p.M) {
+  for (int f = 0; f < FM; ++f) {
+    __syncthreads();  // the previous pass (or the main loop) is done with stg
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) stg[(wm * 16 + 4 * g + r) * LP + wn * WTN + 16 * j + c] = acc[f][j][r];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < WM * 16 * CPR; idx += NTH) {
+      const int t = idx / CPR, c4 = idx % CPR;
+      const long row = m0 + (t / 16) * WTM + f * 16 + (t % 16), col = n0 + 4 * c4;
+      if (row >= p.M) continue;
+      const float4_t v = *reinterpret_cast<const float4_t *>(stg + t * LP + 4 * c4);
       float *dst = C + row * p.ldc + col;
-      float v = p.alpha * acc[r];
-      if (p.beta != 0.0f) v += p.beta * *dst;
-      v += b;
-      *dst = apply_act(p.act, v, p.act_alpha);
+      if (vec_ok && col + 3 < p.N) {
+        float4_t o;
+        const float4_t old = p.beta != 0.0f ? *reinterpret_cast<const float4_t *>(dst) : float4_t{0.f, 0.f, 0.f, 0.f};
+        const float4_t b = p.bias ? *reinterpret_cast<const float4_t *>(p.bias + col) : float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = apply_act(p.act, p.alpha * v[e] + p.beta * old[e] + b[e], p.act_alpha);
+        __builtin_nontemporal_store(o, reinterpret_cast<float4_t *>(dst));  // C is not re-read: keep L2 for A/B
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (col + e < p.N) {
+            float x = p.alpha * v[e];
+            if (p.beta != 0.0f) x += p.beta * dst[e];
+            if (p.bias) x += p.bias[col + e];
+            dst[e] = apply_act(p.act, x, p.act_alpha);
+          }
+        }
+      }
     }
   }
 }
@@ -204,7 +240,6 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f16_kernel(GemmParams p) {
   const long z = blockIdx.z;
   const _Float16 *A = static_cast<const _Float16 *>(p.A) + z * p.strideA;
   const _Float16 *B = static_cast<const _Float16 *>(p.B) + z * p.strideB;
-  float *C = p.C + z * p.strideC;
 
   const int wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -262,11 +297,8 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f16_kernel(GemmParams p) {
     __syncthreads();
   }
 
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-      store_block(p, C, m0 + wm * WTM + i * 16, n0 + wn * WTN + j * 16, acc[i][j]);
+  static_assert(WM * 16 * (BN + 4) * 4 <= 2 * (A_ELEMS + B_ELEMS) * 2, "epilogue staging exceeds LDS");
+  store_tile_rows<BM, BN, WM, WN>(p, m0, n0, z, reinterpret_cast<float *>(smem), acc);
 }
 
 // ------------------------------------------------------------------ fp32 kernel
@@ -296,7 +328,6 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32_kernel(GemmParams p) {
   const long z = blockIdx.z;
   const float *A = static_cast<const float *>(p.A) + z * p.strideA;
   const float *B = static_cast<const float *>(p.B) + z * p.strideB;
-  float *C = p.C + z * p.strideC;
 
   const int wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -372,11 +403,8 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32_kernel(GemmParams p) {
     __syncthreads();
   }
 
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-      store_block(p, C, m0 + wm * WTM + i * 16, n0 + wn * WTN + j * 16, acc[i][j]);
+  static_assert(WM * 16 * (BN + 4) <= 2 * (A_ELEMS + B_ELEMS), "epilogue staging exceeds LDS");
+  store_tile_rows<BM, BN, WM, WN>(p, m0, n0, z, smem, acc);
 }
 
 // ------------------------------------------------------------------ fp16 DMA-ring kernel
@@ -452,66 +480,6 @@ __device__ __forceinline__ unsigned lds_offset(const void *p) {
 // 32-byte block XOR of row k of an MN-contiguous tile.
 __device__ __forceinline__ int hsw(int k) { return (k & 3) | ((k >> 1) & 4); }
 
-// Epilogue for one wave's WTM x WTN accumulator tile, staged through a wave-private
-// LDS region so that C is written in row-major 16-byte vectors (a 16x16 MFMA block
-// alone only gives each store instruction 64-byte row pieces). EP rows at a time go
-// to LDS with a pitch of WTN + 4 floats (the 4 row groups of one ds_write_b32 then
-// fall on distinct banks), then each lane reads 4 consecutive columns back and
-// applies alpha, beta*C, bias and the activation before one 16-byte store. vec_ok:
-// ldc, N and C allow aligned 16-byte stores; otherwise elements are stored singly.
-// The pass index is a template parameter so every accumulator index is static (a
-// runtime index would move the whole accumulator array to scratch memory).
-template <int FM, int FN, int EP, int PASS>
-__device__ __forceinline__ void store_pass(const GemmParams &p, float *C, long row0, long col0,
-                                           const float4_t (&acc)[FM][FN], float *region, bool vec_ok) {
-  constexpr int WTN = FN * 16, LDSP = WTN + 4, CPR = WTN / 4;  // float4 per row
-  constexpr int FB = EP / 16;                                   // MFMA block rows per pass
-  const int lane = threadIdx.x & 63;
-  const int c = lane & 15, g = lane >> 4;
-#pragma unroll
-  for (int ii = 0; ii < FB; ++ii)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) region[(16 * ii + 4 * g + r) * LDSP + 16 * j + c] = acc[PASS * FB + ii][j][r];
-#pragma unroll
-  for (int t = 0; t < EP * CPR / 64; ++t) {
-    const int idx = t * 64 + lane, rr = idx / CPR, c4 = idx % CPR;
-    const float4_t v = *reinterpret_cast<const float4_t *>(region + rr * LDSP + 4 * c4);
-    const long row = row0 + PASS * EP + rr, col = col0 + 4 * c4;
-    if (row < p.M) {
-      float *dst = C + row * p.ldc + col;
-      if (vec_ok && col + 3 < p.N) {
-        float4_t o;
-        const float4_t old =
-            p.beta != 0.0f ? *reinterpret_cast<const float4_t *>(dst) : float4_t{0.f, 0.f, 0.f, 0.f};
-        const float4_t b = p.bias ? *reinterpret_cast<const float4_t *>(p.bias + col) : float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = apply_act(p.act, p.alpha * v[e] + p.beta * old[e] + b[e], p.act_alpha);
-        __builtin_nontemporal_store(o, reinterpret_cast<float4_t *>(dst));  // C is not re-read: keep L2 for A/B
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (col + e < p.N) {
-            float x = p.alpha * v[e];
-            if (p.beta != 0.0f) x += p.beta * dst[e];
-            if (p.bias) x += p.bias[col + e];
-            dst[e] = apply_act(p.act, x, p.act_alpha);
-          }
-        }
-      }
-    }
-  }
-}
-
-template <int FM, int FN, int EP, int... PASS>
-__device__ __forceinline__ void store_tile_coalesced(const GemmParams &p, float *C, long row0, long col0,
-                                                     const float4_t (&acc)[FM][FN], float *region, bool vec_ok,
-                                                     std::integer_sequence<int, PASS...>) {
-  static_assert(FM % (EP / 16) == 0 && (EP * FN * 4) % 64 == 0, "epilogue pass shape");
-  (store_pass<FM, FN, EP, PASS>(p, C, row0, col0, acc, region, vec_ok), ...);
-}
-
 // K-contiguous tiles: a 1 KiB DMA chunk holds rows 16c..16c+15 (32 k each). Lane L
 // copies 16 bytes of row 16c + (L >> 2), so each lane quad reads one row's 64
 // contiguous bytes (a quad spread over four rows stalled the address unit on the L1
@@ -522,23 +490,6 @@ __device__ __forceinline__ void store_tile_coalesced(const GemmParams &p, float 
 __device__ __forceinline__ int kq_swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 __device__ __forceinline__ int kq_slot(int r, int q) { return 4 * r + (q ^ kq_swz(r)); }
 __device__ __forceinline__ int kq_octet(int lane) { return (lane & 3) ^ kq_swz(lane >> 2); }
-
-// Writes one wave's accumulator tile to C through the LDS staging region (the ring,
-// RING bytes).
-template <int BM, int BN, int WM, int WN, int RING>
-__device__ __forceinline__ void ring_epilogue(const GemmParams &p, long m0, long n0, long z, char *smem,
-                                              const float4_t (&acc)[BM / WM / 16][BN / WN / 16]) {
-  constexpr int NW = WM * WN, WTM = BM / WM, WTN = BN / WN, FM = WTM / 16, FN = WTN / 16;
-  constexpr int EP = (NW * 32 * (WTN + 4) * 4 <= RING) ? 32 : 16;  // rows per staging pass
-  static_assert(NW * EP * (WTN + 4) * 4 <= RING, "epilogue staging exceeds the ring");
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave / WN, wn = wave % WN;
-  float *C = p.C + z * p.strideC;
-  const bool vec_ok = (p.ldc % 4 == 0) && (((uintptr_t)C & 15) == 0);
-  float *region = reinterpret_cast<float *>(smem) + wave * EP * (WTN + 4);
-  store_tile_coalesced<FM, FN, EP>(p, C, m0 + wm * WTM, n0 + wn * WTN, acc, region, vec_ok,
-                                   std::make_integer_sequence<int, FM / (EP / 16)>{});
-}
 
 // Main loop of the ring kernel for one output tile (rows m0.., columns n0.., batch z),
 // nk K-tiles: adds the products into acc. K-tiles go in pairs: slot pp & 1 holds tiles
@@ -709,7 +660,8 @@ gemm_f16_ring_kernel(GemmParams p) {
     for (int j = 0; j < FN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
   const long m0 = (long)tm * BM, n0 = (long)tn * BN, z = blockIdx.z;
   ring_mainloop<BM, BN, WM, WN, TA, TB>(p, m0, n0, z, (int)((p.K + 31) / 32), smem, acc);
-  ring_epilogue<BM, BN, WM, WN, RING>(p, m0, n0, z, smem, acc);
+  static_assert(WM * 16 * (BN + 4) * 4 <= RING, "epilogue staging exceeds the ring");
+  store_tile_rows<BM, BN, WM, WN>(p, m0, n0, z, reinterpret_cast<float *>(smem), acc);
 }
 
 // ------------------------------------------------------------------ dispatch
