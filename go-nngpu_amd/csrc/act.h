@@ -11,27 +11,29 @@
 
 namespace gn {
 
-// FAST (the GEMM epilogue) uses __expf and GELU's one-exp tanh; the stand-alone
-// activation kernels are memory-bound and use expf and tanhf instead.
+// FAST (the GEMM epilogue, which runs while the matrix cores idle) uses __expf and the
+// hardware reciprocal (v_rcp_f32, 1 ulp) in place of expf and the IEEE divide sequence,
+// and GELU's sigmoid form; the stand-alone activation kernels are memory-bound and use
+// expf, tanhf and exact division instead.
 template <bool FAST = true>
 __device__ __forceinline__ float apply_act(int act, float x, float a) {
   auto ex = [](float v) { return FAST ? __expf(v) : expf(v); };
+  auto inv = [](float v) { return FAST ? __builtin_amdgcn_rcpf(v) : 1.0f / v; };
   switch (act) {
     case 0: return fmaxf(0.0f, x);
-    case 1: { float c = fmaxf(-88.0f, fminf(88.0f, x)); return 1.0f / (1.0f + ex(-c)); }
+    case 1: { float c = fmaxf(-88.0f, fminf(88.0f, x)); return inv(1.0f + ex(-c)); }
     case 2: return tanhf(fmaxf(-88.0f, fminf(88.0f, x)));
     case 4: return x > 0.0f ? x : a * x;
     case 5: return x > 0.0f ? x : a * (ex(fmaxf(-88.0f, x)) - 1.0f);
-    case 6: { float c = fmaxf(-88.0f, fminf(88.0f, x)); return c / (1.0f + ex(-c)); }
+    case 6: { float c = fmaxf(-88.0f, fminf(88.0f, x)); return c * inv(1.0f + ex(-c)); }
     case 7: {
       float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
       inner = fmaxf(-88.0f, fminf(88.0f, inner));
       if (!FAST) return 0.5f * x * (1.0f + tanhf(inner));
-      // tanh(u) = 1 - 2 / (e^(2u) + 1): one exp and one divide instead of tanhf; the
-      // limits are exact (e -> 0 gives -1, e -> inf gives +1), and near u = 0 the
-      // absolute error stays at fp32 rounding level, far below the GEMM's own.
-      const float t = 1.0f - 2.0f / (__expf(2.0f * inner) + 1.0f);
-      return 0.5f * x * (1.0f + t);
+      // 0.5 (1 + tanh(u)) = 1 / (1 + e^(-2u)): one exp and one reciprocal, no
+      // cancellation near u = 0, and the clamped limits are exact (e^(-2u) underflows
+      // to 0 at u = 88, giving x; it overflows to inf at u = -88, giving x * 0).
+      return x * inv(1.0f + __expf(-2.0f * inner));
     }
     default: return x;
   }
