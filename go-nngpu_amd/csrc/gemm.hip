@@ -53,6 +53,22 @@ struct GemmParams {
 };
 
 // ------------------------------------------------------------------ epilogue
+// Workgroup barrier that orders LDS accesses only (s_waitcnt lgkmcnt(0); s_barrier).
+// __syncthreads() also waits for vmcnt(0), i.e. for every global store the wave has
+// issued to complete, which between the epilogue's passes serialised each pass behind
+// the previous pass's C writes.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int V>
+struct ActCode {
+  static constexpr int value = V;
+};
+constexpr int kActRuntime = -1000;  // ActCode value: apply p.act, decided per element
+
 // Writes a workgroup's BM x BN accumulator tile to C in row order. Pass f stages MFMA
 // block-row f of every wave (WM x 16 tile rows, all BN columns) in LDS at `stg` (pitch
 // BN + 4 floats: the 4 row groups of one ds_write_b32 fall on distinct banks), then the
@@ -60,52 +76,80 @@ struct GemmParams {
 // each store instruction writes long contiguous row segments (one whole 1 KiB row at
 // BN = 256). All CUs write their tiles at about the same time; when each wave stored
 // only its own 256-byte row pieces (rows 32 KiB apart), the writes drained so slowly
-// that the 8192^3 GEMM took 11% longer (4096^3: 17%). alpha, beta*C, bias and the
-// activation are applied on the way; scalar stores at ragged edges or when ldc / C do
-// not allow aligned 16-byte stores. The pass loop is unrolled so every accumulator index
-// is static (a runtime index would move the accumulators to scratch memory).
+// that the 8192^3 GEMM took 11% longer (4096^3: 17%). Each thread owns one column quad
+// for the whole epilogue, so its bias values are loaded once, before the first pass: a
+// load inside the passes would wait for all earlier stores (vmcnt counts stores too).
+// The passes are separated by LDS-only barriers, so the stores of one pass drain while
+// the next is staged. alpha, beta*C, bias and the activation are applied on the way;
+// scalar stores at ragged edges or when ldc / C do not allow aligned 16-byte stores.
+// The pass loop is unrolled so every accumulator index is static (a runtime index would
+// move the accumulators to scratch memory).
 template <int BM, int BN, int WM, int WN>
 __device__ __forceinline__ void store_tile_rows(const GemmParams &p, long m0, long n0, long z, float *stg,
                                                 const float4_t (&acc)[BM / WM / 16][BN / WN / 16]) {
   constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 16, FN = WTN / 16;
   constexpr int LP = BN + 4, CPR = BN / 4, NTH = WM * WN * 64;
-  static_assert(BN % 4 == 0, "row vectors");
+  constexpr int ROWS = WM * 16;       // tile rows staged per pass
+  constexpr int RPS = NTH / CPR;      // rows one sweep of the workgroup's threads covers
+  constexpr int SWEEPS = (ROWS + RPS - 1) / RPS;
+  static_assert(BN % 4 == 0 && CPR <= NTH, "row vectors");
   const int wave = threadIdx.x >> 6, wm = wave / WN, wn = wave % WN, lane = threadIdx.x & 63;
   const int c = lane & 15, g = lane >> 4;
+  const int c4 = threadIdx.x % CPR, r0 = threadIdx.x / CPR;  // threads with r0 >= RPS only stage
+  const long col = n0 + 4 * c4;
   float *C = p.C + z * p.strideC;
-  const bool vec_ok = (p.ldc % 4 == 0) && (((uintptr_t)C & 15) == 0);
+  const bool vec = (p.ldc % 4 == 0) && (((uintptr_t)C & 15) == 0) && col + 3 < p.N;
+  float bv[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) bv[e] = (p.bias && col + e < p.N) ? p.bias[col + e] : 0.0f;
 #pragma unroll
   for (int f = 0; f < FM; ++f) {
-    __syncthreads();  // the previous pass (or the main loop) is done with stg
+    lds_barrier();  // the previous pass (or the main loop) is done with stg
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) stg[(wm * 16 + 4 * g + r) * LP + wn * WTN + 16 * j + c] = acc[f][j][r];
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < WM * 16 * CPR; idx += NTH) {
-      const int t = idx / CPR, c4 = idx % CPR;
-      const long row = m0 + (t / 16) * WTM + f * 16 + (t % 16), col = n0 + 4 * c4;
-      if (row >= p.M) continue;
-      const float4_t v = *reinterpret_cast<const float4_t *>(stg + t * LP + 4 * c4);
-      float *dst = C + row * p.ldc + col;
-      if (vec_ok && col + 3 < p.N) {
-        float4_t o;
-        const float4_t old = p.beta != 0.0f ? *reinterpret_cast<const float4_t *>(dst) : float4_t{0.f, 0.f, 0.f, 0.f};
-        const float4_t b = p.bias ? *reinterpret_cast<const float4_t *>(p.bias + col) : float4_t{0.f, 0.f, 0.f, 0.f};
+    lds_barrier();
+    // The common activations get their own copy of the row sweep with the code fixed at
+    // compile time: the generic one inlines every case of apply_act for every element,
+    // and that long branchy code cost 3.5 us per launch at 512 x 11008 x 512 (ReLU).
+    auto sweep = [&](auto act_c) {
+      constexpr int ACT = decltype(act_c)::value;
+      const int act = ACT == kActRuntime ? p.act : ACT;
+      // a runtime loop: unrolling it as well made the pass loop too large to unroll
+      // fully (the 256 x 256 kernels then kept the accumulators in scratch memory)
+#pragma unroll 1
+      for (int s = 0; s < SWEEPS; ++s) {
+        const int t = r0 + s * RPS;
+        if (r0 >= RPS || t >= ROWS) continue;
+        const long row = m0 + (t / 16) * WTM + f * 16 + (t % 16);
+        if (row >= p.M) continue;
+        const float4_t v = *reinterpret_cast<const float4_t *>(stg + t * LP + 4 * c4);
+        float *dst = C + row * p.ldc + col;
+        if (vec) {
+          float4_t o;
+          const float4_t old =
+              p.beta != 0.0f ? *reinterpret_cast<const float4_t *>(dst) : float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = apply_act(p.act, p.alpha * v[e] + p.beta * old[e] + b[e], p.act_alpha);
-        __builtin_nontemporal_store(o, reinterpret_cast<float4_t *>(dst));  // C is not re-read: keep L2 for A/B
-      } else {
+          for (int e = 0; e < 4; ++e) o[e] = apply_act(act, p.alpha * v[e] + p.beta * old[e] + bv[e], p.act_alpha);
+          __builtin_nontemporal_store(o, reinterpret_cast<float4_t *>(dst));  // C is not re-read: keep L2 for A/B
+        } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (col + e < p.N) {
-            float x = p.alpha * v[e];
-            if (p.beta != 0.0f) x += p.beta * dst[e];
-            if (p.bias) x += p.bias[col + e];
-            dst[e] = apply_act(p.act, x, p.act_alpha);
+          for (int e = 0; e < 4; ++e) {
+            if (col + e < p.N) {
+              float x = p.alpha * v[e];
+              if (p.beta != 0.0f) x += p.beta * dst[e];
+              dst[e] = apply_act(act, x + bv[e], p.act_alpha);
+            }
           }
         }
       }
+    };
+    switch (p.act) {
+      case -1: sweep(ActCode<-1>{}); break;
+      case 0: sweep(ActCode<0>{}); break;
+      case 7: sweep(ActCode<7>{}); break;
+      default: sweep(ActCode<kActRuntime>{}); break;
     }
   }
 }
