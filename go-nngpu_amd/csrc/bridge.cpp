@@ -24,8 +24,8 @@ int sync(hipStream_t s, CError *err, int code) {
 }
 
 bool fits(const Buffer *b, long rows, long cols, size_t esz) {
-  if (rows < 0 || cols < 0) return false;
-  return (size_t)rows * (size_t)cols * esz <= b->bytes;
+  size_t n;
+  return gn::matrix_bytes(rows, cols, esz, &n) && n <= b->bytes;
 }
 
 // Uploads host CSR index arrays into device scratch, runs fn, and converts the
@@ -199,7 +199,10 @@ static int batched_gemm(GPUPtr aPtr, GPUPtr bPtr, GPUPtr cPtr, long batch, long 
   if (!a || !b || !c) return set_error(err, -2, "Invalid buffer pointers");
   if (batch < 0 || M < 0 || N < 0 || K < 0) return set_error(err, -3, "Invalid GEMM sizes");
   if (batch == 0) return 0;
-  if (!fits(a, batch * M, K, 4) || !fits(b, batch * K, N, 4) || !fits(c, batch * M, N, 4))
+  long bM, bK;
+  if (__builtin_mul_overflow(batch, M, &bM) || __builtin_mul_overflow(batch, K, &bK))
+    return set_error(err, -3, "Invalid GEMM sizes");
+  if (!fits(a, bM, K, 4) || !fits(b, bK, N, 4) || !fits(c, bM, N, 4))
     return set_error(err, -3, "Buffer smaller than the matrices it describes.");
   gn::GemmDesc d{GN_F32, false, false, M, N, K, alpha, beta, a->dptr, K, M * K, b->dptr, N, K * N,
                  static_cast<float *>(c->dptr), N, M * N, batch, nullptr, GN_ACT_NONE, 0.0f};

@@ -19,6 +19,15 @@ int set_error(CError *err, int code, const char *fmt, ...) __attribute__((format
 // Maps a failed HIP call to code with "<what>: <hip error string>".
 int hip_error(CError *err, int code, const char *what, hipError_t e);
 
+// Bytes of a rows x cols matrix of esz-byte elements in *out; false when a size is
+// negative or the product overflows (caller-supplied sizes must not wrap into a small
+// allocation or a passing bounds check).
+inline bool matrix_bytes(long rows, long cols, size_t esz, size_t *out) {
+  if (rows < 0 || cols < 0) return false;
+  size_t n;
+  return !__builtin_mul_overflow((size_t)rows, (size_t)cols, &n) && !__builtin_mul_overflow(n, esz, out);
+}
+
 // ---------------------------------------------------------------- context
 struct Context {
   int device = 0;

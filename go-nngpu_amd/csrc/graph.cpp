@@ -114,7 +114,8 @@ void *createMPSGraph(void) {
 
 void *gn_graph_placeholder(void *graph, long rows, long cols, int dtype) {
   Graph *g = gn::as_graph(graph);
-  if (!g || rows < 0 || cols < 0 || (dtype != GN_F32 && dtype != GN_F16)) return nullptr;
+  size_t bytes;
+  if (!g || !gn::matrix_bytes(rows, cols, 4, &bytes) || (dtype != GN_F32 && dtype != GN_F16)) return nullptr;
   std::lock_guard<std::mutex> lk(g->mu);
   return gn::add_tensor(g, rows, cols, dtype, -1);
 }
@@ -127,7 +128,8 @@ void *gn_graph_matmul(void *graph, void *inputA, void *inputB, int transA, int t
   if (!a || !b || a->dtype != b->dtype) return nullptr;
   const long M = transA ? a->cols : a->rows, K = transA ? a->rows : a->cols;
   const long K2 = transB ? b->cols : b->rows, N = transB ? b->rows : b->cols;
-  if (K != K2) return nullptr;
+  size_t out_bytes;
+  if (K != K2 || !gn::matrix_bytes(M, N, 4, &out_bytes)) return nullptr;
   GraphOp op;
   op.matmul = true;
   op.a = a->id;

@@ -56,6 +56,15 @@ def test_matmul_dimension_errors(dev):
     assert rc == -2
     rc, _ = G.call_rc("perform_mps_matrix_multiplication", a.handle, 20, 30, b.handle, 30, 20, c.handle, 20, 20, None)
     assert rc == -3  # buffers too small for the claimed shapes
+    # sizes whose byte counts wrap around 2^64 (2^40 * 2^40 * 4 = 2^82) are rejected before any launch
+    big = 1 << 40
+    rc, _ = G.call_rc("perform_mps_matrix_multiplication", a.handle, big, big, b.handle, big, 1 << 24, c.handle, big,
+                      1 << 24, None)
+    assert rc == -3
+    rc, _ = G.call_rc("perform_batch_matmul_optimized", a.handle, b.handle, c.handle, 1 << 62, 4, 4, 4, None)
+    assert rc == -3  # batch * M overflows
+    rc, _ = G.call_rc("perform_mps_matrix_transpose", a.handle, big, big, b.handle, big, big, None)
+    assert rc == -3
 
 
 def test_optimized_gemm_alpha_beta(dev):

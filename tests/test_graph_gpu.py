@@ -95,6 +95,11 @@ def test_mpsgraph_abi_matmul_relu_chain(dev):
     y = L.createMatMulNode(g, L.createReLUNode(g, L.createMatMulNode(g, X, W1)), W2)
     assert y
     assert not L.createMatMulNode(g, X, W2)  # inner dimensions 96 and 130
+    g2 = L.createMPSGraph()  # shapes whose byte counts wrap around 2^64 are refused
+    assert not L.gn_graph_placeholder(g2, 1 << 40, 1 << 40, G.GN_F32)
+    tall, wide = L.gn_graph_placeholder(g2, 1 << 31, 1, G.GN_F32), L.gn_graph_placeholder(g2, 1, 1 << 40, G.GN_F32)
+    assert tall and wide and not L.createMatMulNode(g2, tall, wide)  # a 2^71-value product
+    L.gn_graph_release(g2)
     c = L.compileGraph(g, None)
     assert c
     rng = np.random.default_rng(71)
