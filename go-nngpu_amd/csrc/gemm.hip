@@ -830,11 +830,9 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
   if (d.M == 0 || d.N == 0) return 0;
   if (!d.C) return set_error(err, -1, "gemm: NULL C");
   if (d.K > 0 && (!d.A || !d.B)) return set_error(err, -1, "gemm: NULL operand");
-  const long a_rows = d.ta ? d.K : d.M, a_cols = d.ta ? d.M : d.K;
-  const long b_rows = d.tb ? d.N : d.K, b_cols = d.tb ? d.K : d.N;
+  const long a_cols = d.ta ? d.M : d.K, b_cols = d.tb ? d.K : d.N;  // stored row lengths
   if ((d.K > 0 && (d.lda < a_cols || d.ldb < b_cols)) || d.ldc < d.N)
     return set_error(err, -1, "gemm: leading dimension smaller than row length");
-  (void)a_rows; (void)b_rows;
   const long tiles = ((d.M + 63) / 64) * ((d.N + 63) / 64);
   if (tiles > (1L << 30)) return set_error(err, -1, "gemm: problem too large for the grid");
 
