@@ -43,6 +43,7 @@ for _p in (ROOT, os.path.join(ROOT, "go-nngpu_amd")):
 METRIC = "GEMM TFLOP/s + % MFMA peak (fp32, fp16→fp32); CSR SpMM HBM GB/s, 1 MI355X"
 PEAK_F16_TFLOPS = 2516.6  # dense MFMA fp16, 256 CU x 4096 flop/clk x 2.4 GHz
 PEAK_F32_TFLOPS = 157.3   # fp32 MFMA
+MIN_WARM_MS = 50.0        # least untimed GPU time per secondary leg (see timed())
 PEAK_HBM_GBS = 8000.0
 ALL = ("c3", "c2", "c4", "spmm", "spmv", "e2e", "copy")
 
@@ -51,13 +52,29 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def timed(fn, steps, warmup, stream):
-    """Mean ms per call of fn() over `steps` calls, events recorded on `stream`."""
+def timed(fn, steps, warmup, stream, min_warm_ms=0.0):
+    """Mean ms per call of fn() over `steps` calls, events recorded on `stream`.
+
+    `warmup` untimed calls come first; with min_warm_ms > 0 more untimed calls follow
+    until at least that much GPU time has gone into warming up. The secondary legs use
+    this: 50 launches of a 50 us kernel are 2.5 ms, and short kernels measured 10-25%
+    slow that early after a leg change (clock ramp), settling within ~30 ms."""
     import torch
 
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    if min_warm_ms > 0:
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        done = 0.0
+        while done < min_warm_ms:
+            for _ in range(10):
+                fn()
+            t1.record(stream)
+            t1.synchronize()
+            done = t0.elapsed_time(t1)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record(stream)
@@ -144,7 +161,7 @@ def run_c2(c, steps, warmup):
     res = {}
     for ta, tb, name in [(0, 0, "NN"), (0, 1, "NT"), (1, 0, "TN"), (1, 1, "TT")]:
         ms = timed(lambda: c.G.gemm(A, B, C, transA=bool(ta), transB=bool(tb), stream_ptr=c.sp), steps, warmup,
-                   c.stream)
+                   c.stream, MIN_WARM_MS)
         tf = 2.0 * m ** 3 / (ms * 1e-3) / 1e12
         res[f"c2_f32_4096_{name}"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 2),
                                       "frac_fp32_peak": round(tf / PEAK_F32_TFLOPS, 4)}
@@ -162,7 +179,7 @@ def run_c4(c, steps, warmup):
     res = {}
     for act, name in [(c.G.ACT_RELU, "relu"), (c.G.ACT_GELU, "gelu")]:
         ms = timed(lambda: c.G.gemm(X16, W16, Y, transB=True, bias=bias, act=act, stream_ptr=c.sp), steps, warmup,
-                   c.stream)
+                   c.stream, MIN_WARM_MS)
         tf = flop / (ms * 1e-3) / 1e12
         res[f"c4_linear_{name}"] = {"ms": round(ms, 5), "TFLOP/s": round(tf, 2),
                                     "frac_fp16_peak": round(tf / PEAK_F16_TFLOPS, 4)}
@@ -186,7 +203,7 @@ def run_spmm(c, steps, warmup, csr):
     c.G.fill_normal(D, 42, 8, stream_ptr=c.sp)
     Cs = c.empty((M, N))
     ms = timed(lambda: c.G.spmm_csr(M, N, K, nnz, d_rp, d_col, d_val, D, Cs, stream_ptr=c.sp), steps, warmup,
-               c.stream)
+               c.stream, MIN_WARM_MS)
     b_s = 4 * (M + 1) + 8 * nnz + 4 * nnz * N + 4 * M * N
     b_c = 4 * (M + 1) + 8 * nnz + 4 * K * N + 4 * M * N
     gbs = b_s / (ms * 1e-3) / 1e9
@@ -201,7 +218,8 @@ def run_spmv(c, steps, warmup, csr):
     M, K, nnz, d_rp, d_col, d_val = csr
     x, y = c.empty((K,)), c.empty((M,))
     c.G.fill_normal(x, 42, 9, stream_ptr=c.sp)
-    ms = timed(lambda: c.G.spmv_csr(M, K, nnz, d_rp, d_col, d_val, x, y, stream_ptr=c.sp), steps, warmup, c.stream)
+    ms = timed(lambda: c.G.spmv_csr(M, K, nnz, d_rp, d_col, d_val, x, y, stream_ptr=c.sp), steps, warmup, c.stream,
+               MIN_WARM_MS)
     b_s = 4 * (M + 1) + 12 * nnz + 4 * M
     gbs = b_s / (ms * 1e-3) / 1e9
     log(f"spmv: {ms * 1e3:.1f} us, {gbs:.0f} GB/s (streamed-bytes model)")

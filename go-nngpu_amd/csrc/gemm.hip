@@ -460,9 +460,9 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32_kernel(GemmParams p) {
 //    only one barrier per pair of K-tiles is needed;
 //  * out-of-range lanes (rows past M/N, the K tail) get a buffer offset beyond the
 //    descriptor's range, which the hardware turns into zeros;
-//  * K-contiguous operands are stored in 1 KiB chunks of 16 rows x 32 k, each MFMA
-//    fragment one ds_read_b128 within a chunk (lane quads copy whole 64-byte row
-//    pieces; see kq_slot);
+//  * K-contiguous operands are stored in 1 KiB chunks of 8 rows x 64 k (both K-tiles
+//    of a pair), each MFMA fragment one ds_read_b128 (lane octets copy whole 128-byte
+//    lines; see kc8_slot);
 //  * MN-contiguous operands keep their memory layout, rows of 2*BM (or 2*BN) bytes,
 //    with the 32-byte block index XORed by hsw(k) so the 8 rows one 32-lane phase of
 //    ds_read_b64_tr_b16 reads (k0+8g+r, g < 2, r < 4) fall on distinct banks;
@@ -524,16 +524,16 @@ __device__ __forceinline__ unsigned lds_offset(const void *p) {
 // 32-byte block XOR of row k of an MN-contiguous tile.
 __device__ __forceinline__ int hsw(int k) { return (k & 3) | ((k >> 1) & 4); }
 
-// K-contiguous tiles: a 1 KiB DMA chunk holds rows 16c..16c+15 (32 k each). Lane L
-// copies 16 bytes of row 16c + (L >> 2), so each lane quad reads one row's 64
-// contiguous bytes (a quad spread over four rows stalled the address unit on the L1
-// cache, measured 14% slower for NT). The hardware writes lane L's bytes to slot L of
-// the chunk, so the k octet it loads is permuted, q = (L & 3) ^ g(row), such that an
-// MFMA fragment read (lane l: row l & 15, octet l >> 4, slot kq_slot) hits 16 distinct
-// 16-byte bank groups in every 16 lanes and 8 distinct ones in every 8.
-__device__ __forceinline__ int kq_swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
-__device__ __forceinline__ int kq_slot(int r, int q) { return 4 * r + (q ^ kq_swz(r)); }
-__device__ __forceinline__ int kq_octet(int lane) { return (lane & 3) ^ kq_swz(lane >> 2); }
+// K-contiguous tiles: a 1 KiB DMA chunk holds rows 8c..8c+7 with the 64 k of a K-tile
+// pair (128 bytes) each. Lane L copies 16 bytes of row 8c + (L >> 3), so each lane
+// octet reads one whole 128-byte line: half the L1 requests of 16 rows x 64 bytes per
+// chunk (NT 882 -> 836 us at 8192^3), and lane quads stay on one row (quads spread over
+// four rows stalled the address unit on the L1 cache). The hardware writes lane L's
+// bytes to slot L of the chunk, so the octet it loads is permuted: octet o of row r sits
+// in slot 8 (r & 7) + (o ^ ((r >> 1) & 7)), and the 16 rows an MFMA fragment read
+// touches (two chunks, fixed o) land on 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int kc8_slot(int r, int o) { return 8 * (r & 7) + (o ^ ((r >> 1) & 7)); }
+__device__ __forceinline__ int kc8_octet(int r, int j) { return j ^ ((r >> 1) & 7); }
 
 // Main loop of the ring kernel for one output tile (rows m0.., columns n0.., batch z),
 // nk K-tiles: adds the products into acc. K-tiles go in pairs: slot pp & 1 holds tiles
@@ -564,10 +564,10 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
   const int lane = threadIdx.x & 63;
   const int wm = wave / WN, wn = wave % WN;
 
-  // Per-lane DMA plan: chunk c of a pair belongs to tile h = c / (nchunks / 2). For a
-  // K-contiguous operand it holds rows 16cl..16cl+15 (cl = c % (nchunks / 2)), lane
-  // quads per row as kq_slot lays out; for an MN-contiguous one, k rows
-  // cl * (1024 / row bytes).. with 32-byte blocks XOR-swizzled by hsw(k). Each lane
+  // Per-lane DMA plan. For a K-contiguous operand chunk c of a pair holds rows
+  // 8c..8c+7 of both K-tiles, octets as kc8_slot lays out. For an MN-contiguous one it
+  // belongs to tile h = c / (nchunks / 2) and holds k rows cl * (1024 / row bytes)..
+  // (cl = c % (nchunks / 2)) with 32-byte blocks XOR-swizzled by hsw(k). Each lane
   // keeps its offset from the pair's start and the k (0..63) it covers; lanes whose
   // rows or columns lie past M (or N) get the out-of-range offset.
   BufRsrc ra, rb;
@@ -575,10 +575,10 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
   int kla[IPA], klb[IPB];
   auto plan = [&](bool kcontig, int c, int nchunks, int rb_bytes, long ld, long lim, unsigned &vo, int &kl) {
     const int h = c / (nchunks / 2), cl = c % (nchunks / 2);
-    if (kcontig) {
-      const int row = 16 * cl + (lane >> 2), q = kq_octet(lane);
-      kl = 32 * h + 8 * q;
-      vo = lim > row ? (unsigned)((long)row * ld * 2 + 64 * h + 16 * q) : kOutOfRange;
+    if (kcontig) {  // chunk c: rows 8c..8c+7, the pair's 64 k (128 bytes) each
+      const int row = 8 * c + (lane >> 3), q = kc8_octet(row, lane & 7);
+      kl = 8 * q;
+      vo = lim > row ? (unsigned)((long)row * ld * 2 + 16 * q) : kOutOfRange;
       return;
     }
     const int gpr = rb_bytes / 16;
@@ -630,18 +630,22 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
     return __builtin_shufflevector(l4, h4, 0, 1, 2, 3, 4, 5, 6, 7);
   };
 
-  auto frag_k = [&](const char *base, int row0) -> half8_t {
-    return *reinterpret_cast<const half8_t *>(base + (row0 >> 4) * 1024 + 16 * kq_slot(lane & 15, lane >> 4));
+  auto frag_k = [&](const char *base, int row0, int h) -> half8_t {
+    const int row = row0 + (lane & 15);
+    return *reinterpret_cast<const half8_t *>(base + (row >> 3) * 1024 + 16 * kc8_slot(row, 4 * h + (lane >> 4)));
   };
 
   half8_t fa[2][FM], fb[2][FN];
   auto read_frags = [&](int slot, int h, int set) {
-    const char *sa = smem + slot * SLOT + h * OPA;
-    const char *sb = smem + slot * SLOT + 2 * OPA + h * OPB;
+    // K-contiguous operands hold both K-tiles of the pair in each chunk (no h offset)
+    const char *sa = smem + slot * SLOT + (TA ? h * OPA : 0);
+    const char *sb = smem + slot * SLOT + 2 * OPA + (TB ? 0 : h * OPB);
 #pragma unroll
-    for (int i = 0; i < FM; ++i) fa[set][i] = TA ? frag_t(sa, wm * WTM + i * 16, RBA) : frag_k(sa, wm * WTM + i * 16);
+    for (int i = 0; i < FM; ++i)
+      fa[set][i] = TA ? frag_t(sa, wm * WTM + i * 16, RBA) : frag_k(sa, wm * WTM + i * 16, h);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) fb[set][j] = TB ? frag_k(sb, wn * WTN + j * 16) : frag_t(sb, wn * WTN + j * 16, RBB);
+    for (int j = 0; j < FN; ++j)
+      fb[set][j] = TB ? frag_k(sb, wn * WTN + j * 16, h) : frag_t(sb, wn * WTN + j * 16, RBB);
   };
   constexpr int NDS = (TA ? 2 : 1) * FM + (TB ? 1 : 2) * FN;  // LDS read instructions per tile
   constexpr int NIL = NDS < FM * FN ? NDS : FM * FN;
