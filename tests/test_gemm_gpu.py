@@ -332,11 +332,11 @@ def test_f16_ring_transpose_variants_bit_identical(dev):
 
 
 @pytest.mark.parametrize("K", [8, 40, 968])
-def test_f16_ring_tn_pairs_odd_k_tiles(dev, K):
-    """op(A) = A^T, op(B) = B takes K-tiles two at a time on the ring. One 32-deep K-tile
-    (K = 8), two with a tail (K = 40) and 31 with a tail (K = 968) leave the last pair
-    half or wholly zero; the result equals the NN ring kernel's bit for bit (same
-    summation order per element) and the oracle within the fp16-input bar."""
+def test_f16_ring_odd_k_tiles_all_layouts(dev, K):
+    """The ring takes K-tiles two at a time. One 32-deep K-tile (K = 8), two with a tail
+    (K = 40) and 31 with a tail (K = 968) leave the last pair half or wholly zero; TN, NT
+    and TT equal the NN result bit for bit (same summation order per element), and TN
+    meets the oracle within the fp16-input bar."""
     rng = np.random.default_rng(K)
     M, N = 4096, 4104
     A = rng.standard_normal((M, K)).astype(np.float32)
@@ -344,10 +344,13 @@ def test_f16_ring_tn_pairs_odd_k_tiles(dev, K):
     c_tn = _gemm_dev(dev, A, B, True, False, G.GN_F16)
     c_nn = _gemm_dev(dev, A, B, False, False, G.GN_F16)
     np.testing.assert_array_equal(c_tn, c_nn)
+    # K-contiguous B (NT, TT) takes the 8-row x 128-byte chunk layout with its K tail
+    np.testing.assert_array_equal(_gemm_dev(dev, A, B, False, True, G.GN_F16), c_nn)
+    np.testing.assert_array_equal(_gemm_dev(dev, A, B, True, True, G.GN_F16), c_nn)
     rows = np.concatenate([np.arange(0, 8), rng.choice(M, 16, replace=False), np.arange(M - 8, M)])
     ref_r = O.gemm_f64_rows(O.round_f16(A[rows], False), O.round_f16(B, False), np.arange(rows.size))
     err = O.rel_frob(c_tn[rows], ref_r)
-    _say("ring tn pairs K", K, err)
+    _say("ring odd K tiles", K, err)
     assert err <= 1e-5
 
 
