@@ -535,6 +535,19 @@ __device__ __forceinline__ int hsw(int k) { return (k & 3) | ((k >> 1) & 4); }
 __device__ __forceinline__ int kc8_slot(int r, int o) { return 8 * (r & 7) + (o ^ ((r >> 1) & 7)); }
 __device__ __forceinline__ int kc8_octet(int r, int j) { return j ^ ((r >> 1) & 7); }
 
+// A scheduling region of NM MFMAs and NR LDS reads, interleaved 1:1 (then the rest).
+template <int NM, int NR>
+__device__ __forceinline__ void sched_interleave() {
+  constexpr int NP = NR < NM ? NR : NM;
+#pragma unroll
+  for (int g = 0; g < NP; ++g) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+  if constexpr (NM > NP) __builtin_amdgcn_sched_group_barrier(0x008, NM - NP, 0);
+  if constexpr (NR > NP) __builtin_amdgcn_sched_group_barrier(0x100, NR - NP, 0);
+}
+
 // Main loop of the ring kernel for one output tile (rows m0.., columns n0.., batch z),
 // nk K-tiles: adds the products into acc. K-tiles go in pairs: slot pp & 1 holds tiles
 // 2pp and 2pp+1 of A, then of B (one single-tile region each). Per pair, the even step
@@ -561,9 +574,10 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
   static_assert(LPW < 64, "vmcnt range");
   // Splitting each pair's DMA into two bursts (A at the barrier, B halfway through the
   // MFMAs) measured 2-4% faster at 256 x 256 with 8 waves (8192^3: NN 884 -> 851 us, NT
-  // 872 -> 851 us) and 10% slower for the 4-wave 128 x 96 tiles of the C4 shape.
-  constexpr bool kSplitDma = NW >= 8;
-  static_assert(!kSplitDma || FM % 2 == 0, "the odd step splits the MFMA rows in halves");
+  // 872 -> 851 us) and 10% slower for the 4-wave 128 x 96 tiles of the C4 shape; four
+  // bursts measured within 1% of two.
+  constexpr int kDmaParts = NW >= 8 ? 2 : 1;
+  static_assert(FM % kDmaParts == 0 && (kDmaParts == 1 || (FM % 2 == 0 && FN % 2 == 0)), "DMA bursts / read parts");
   static_assert((!TA || BM >= 128) && (TB || BN >= 128), "MN-contiguous rows need 8 XOR blocks of 32 B");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -607,24 +621,30 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
   const unsigned sbase = lds_offset(smem);
   const int np = max(1, (nk + 1) >> 1);  // pairs the loop runs; tiles past nk are zeros
 
-  // DMA of pair pp (K-tiles 2pp, 2pp+1) into slot `slot`: part 0 copies A, part 1
-  // copies B and then advances both descriptors to the next pair.
-  auto issue = [&](int pp, int slot, int part) {
+  // DMA of pair pp (K-tiles 2pp, 2pp+1) into slot `slot`, in parts: part q of NP copies
+  // the q-th share of the wave's A chunks (q < NP / 2) or of its B chunks; the last part
+  // also advances both descriptors to the next pair.
+  auto issue = [&](int pp, int slot, int q, int NPRT) {
     const unsigned st = sbase + (unsigned)(slot * SLOT);
     const long krem_l = p.K - (long)pp * 2 * BK;
     const int krem = (int)(krem_l < 0 ? 0 : (krem_l > 2 * BK ? 2 * BK : krem_l));
-    if (part == 0) {
+    const int half = NPRT / 2;
+    if (q < half) {
 #pragma unroll
       for (int i = 0; i < IPA; ++i)
-        dma16(ra, kla[i] < krem ? voa[i] : kOutOfRange, __builtin_amdgcn_readfirstlane(st + (wave * IPA + i) * 1024));
+        if (i * half / IPA == q)
+          dma16(ra, kla[i] < krem ? voa[i] : kOutOfRange, __builtin_amdgcn_readfirstlane(st + (wave * IPA + i) * 1024));
       return;
     }
 #pragma unroll
     for (int i = 0; i < IPB; ++i)
-      dma16(rb, klb[i] < krem ? vob[i] : kOutOfRange,
-            __builtin_amdgcn_readfirstlane(st + 2 * OPA + (wave * IPB + i) * 1024));
-    rsrc_advance(ra, a_step);
-    rsrc_advance(rb, b_step);
+      if (i * half / IPB == q - half)
+        dma16(rb, klb[i] < krem ? vob[i] : kOutOfRange,
+              __builtin_amdgcn_readfirstlane(st + 2 * OPA + (wave * IPB + i) * 1024));
+    if (q == NPRT - 1) {
+      rsrc_advance(ra, a_step);
+      rsrc_advance(rb, b_step);
+    }
   };
 
   auto frag_t = [&](const char *base, int col0, int rowb) -> half8_t {
@@ -645,17 +665,22 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
   };
 
   half8_t fa[2][FM], fb[2][FN];
-  auto read_frags = [&](int slot, int h, int set) {
+  // Fragments of tile h of slot `slot` into register set `set`; part q of NPRT reads
+  // the q-th share of the A and of the B fragments.
+  auto read_part = [&](int slot, int h, int set, int q, int NPRT) {
     // K-contiguous operands hold both K-tiles of the pair in each chunk (no h offset)
     const char *sa = smem + slot * SLOT + (TA ? h * OPA : 0);
     const char *sb = smem + slot * SLOT + 2 * OPA + (TB ? 0 : h * OPB);
 #pragma unroll
     for (int i = 0; i < FM; ++i)
-      fa[set][i] = TA ? frag_t(sa, wm * WTM + i * 16, RBA) : frag_k(sa, wm * WTM + i * 16, h);
+      if (i * NPRT / FM == q)
+        fa[set][i] = TA ? frag_t(sa, wm * WTM + i * 16, RBA) : frag_k(sa, wm * WTM + i * 16, h);
 #pragma unroll
     for (int j = 0; j < FN; ++j)
-      fb[set][j] = TB ? frag_k(sb, wn * WTN + j * 16, h) : frag_t(sb, wn * WTN + j * 16, RBB);
+      if (j * NPRT / FN == q)
+        fb[set][j] = TB ? frag_k(sb, wn * WTN + j * 16, h) : frag_t(sb, wn * WTN + j * 16, RBB);
   };
+  auto read_frags = [&](int slot, int h, int set) { read_part(slot, h, set, 0, 1); };
   constexpr int NDS = (TA ? 2 : 1) * FM + (TB ? 1 : 2) * FN;  // LDS read instructions per tile
   constexpr int NIL = NDS < FM * FN ? NDS : FM * FN;
   auto mfma_rows = [&](int set, int i0, int i1) {
@@ -664,17 +689,6 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
 #pragma unroll
       for (int j = 0; j < FN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
-  };
-  // First half of a tile's MFMAs with the next tile's NDS fragment reads, 1:1.
-  auto interleave_half = [&]() {
-    constexpr int NM = (FM / 2) * FN, NP = NDS < NM ? NDS : NM;
-#pragma unroll
-    for (int g = 0; g < NP; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-    if (NM > NP) __builtin_amdgcn_sched_group_barrier(0x008, NM - NP, 0);
-    if (NDS > NP) __builtin_amdgcn_sched_group_barrier(0x100, NDS - NP, 0);
   };
   auto mfma_set = [&](int set) {
 #pragma unroll
@@ -692,10 +706,10 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
     __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - NIL, 0);
   };
 
-  issue(0, 0, 0);
-  issue(0, 0, 1);
-  issue(1, 1, 0);
-  issue(1, 1, 1);
+  issue(0, 0, 0, 2);
+  issue(0, 0, 1, 2);
+  issue(1, 1, 0, 2);
+  issue(1, 1, 1, 2);
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPW));
   __syncthreads();
   read_frags(0, 0, 0);
@@ -711,19 +725,23 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (kSplitDma) {
-      // A's copies now, B's halfway through the tile's MFMAs: the address unit gets the
-      // pair's DMA in two bursts instead of one
-      issue(pp + 2, cur, 0);
-      read_frags(cur ^ 1, 0, 0);
-      mfma_rows(1, 0, FM / 2);
-      interleave_half();
-      __builtin_amdgcn_sched_barrier(0);
-      issue(pp + 2, cur, 1);
-      mfma_rows(1, FM / 2, FM);
+    if constexpr (kDmaParts > 1) {
+      // The pair's DMA in kDmaParts bursts spread over the tile's MFMAs (A's shares first);
+      // the next tile's fragment reads go with the MFMAs of the first two regions.
+      constexpr int QM = FM / kDmaParts;  // MFMA rows per region
+#pragma unroll
+      for (int q = 0; q < kDmaParts; ++q) {
+        if (q) __builtin_amdgcn_sched_barrier(0);
+        issue(pp + 2, cur, q, kDmaParts);
+        constexpr int NRH = (TA ? 2 : 1) * (FM / 2) + (TB ? 1 : 2) * (FN / 2);  // reads per half
+        if (q < 2) read_part(cur ^ 1, 0, 0, q, 2);
+        mfma_rows(1, q * QM, (q + 1) * QM);
+        if (q < 2) sched_interleave<QM * FN, NRH>();
+        else sched_interleave<QM * FN, 0>();
+      }
     } else {
-      issue(pp + 2, cur, 0);
-      issue(pp + 2, cur, 1);
+      issue(pp + 2, cur, 0, 2);
+      issue(pp + 2, cur, 1, 2);
       read_frags(cur ^ 1, 0, 0);
       mfma_set(1);
       interleave();
