@@ -193,7 +193,38 @@ def csr_workload(c):
     M = K = 65536
     rp, col, val = synth.csr_uniform(M, K, 65.536, seed=42)
     t = c.torch
+    c.csr_host = (rp, col, val)  # for the CPU baselines
     return M, K, int(val.size), t.from_numpy(rp).to(c.dev), t.from_numpy(col).to(c.dev), t.from_numpy(val).to(c.dev)
+
+
+def cpu_baseline_sparse(c, kind, rows):
+    """The reference's own CPU loop for SpMM (metal_bridge_sparse.m:117-133) or SpMV
+    (:325-339), restated in the oracle and run on one thread as the reference runs it, on
+    the first `rows` rows of the C5 matrix; reported in the GPU leg's streamed-bytes units."""
+    from oracle import oracle as O
+
+    rp, col, val = c.csr_host
+    M = rp.size - 1
+    rows = min(rows, M)
+    end = int(rp[rows])
+    srp, scol, sval = rp[:rows + 1], col[:end], val[:end]
+    if kind == "spmm":
+        N = 256
+        D = O.normal((M, N), 42, 108)
+        t0 = time.perf_counter()
+        O.spmm_f32(srp, scol, sval, D)
+        dt = time.perf_counter() - t0
+        b_s = 4 * (rows + 1) + 8 * end + 4 * end * N + 4 * rows * N
+    else:
+        x = O.normal((M,), 42, 109)
+        t0 = time.perf_counter()
+        O.spmv_f32(srp, scol, sval, x)
+        dt = time.perf_counter() - t0
+        b_s = 4 * (rows + 1) + 12 * end + 4 * rows
+    return {"value": round(b_s / dt / 1e9, 2), "unit": "GB/s (streamed-bytes model)", "cores": 1, "kind": "port",
+            "ms_full_matrix": round(dt * 1e3 * M / rows, 2),
+            "sample": f"oracle restatement of the reference's single-threaded CSR {kind} loop on rows 0..{rows - 1} "
+                      f"of the {M}-row C5 matrix ({end} stored entries), {dt:.2f} s"}
 
 
 def run_spmm(c, steps, warmup, csr):
@@ -309,8 +340,14 @@ def main():
         csr = csr_workload(c)
         if "spmm" in only:
             secondary["c5_spmm"] = run_spmm(c, steps2 * 2, 3, csr)
+            if not args.no_cpu:
+                secondary["c5_spmm"]["cpu_baseline"] = cpu_baseline_sparse(c, "spmm", 16384)
+                log(f"cpu_baseline spmm: {secondary['c5_spmm']['cpu_baseline']['value']} GB/s on 1 thread")
         if "spmv" in only:
             secondary["c5_spmv"] = run_spmv(c, steps2 * 4, 5, csr)
+            if not args.no_cpu:
+                secondary["c5_spmv"]["cpu_baseline"] = cpu_baseline_sparse(c, "spmv", 65536)
+                log(f"cpu_baseline spmv: {secondary['c5_spmv']['cpu_baseline']['value']} GB/s on 1 thread")
         del csr
         c.torch.cuda.empty_cache()
     if "e2e" in only:
