@@ -110,6 +110,22 @@ def cpu_baseline_gemm(n, rows):
                       f"headline problem, {dt:.1f} s on {threads} threads"}
 
 
+def cpu_numpy_gemm(n, rows):
+    """numpy float64 matmul (OpenBLAS, its own threads) on the same sample: an optimised
+    CPU line beside the oracle's plain restatement of gonum's Dense.Mul semantics."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    A = O.normal((rows, n), 42, 101).astype(np.float64)
+    B = O.normal((n, n), 42, 102, 0.0, 0.02).astype(np.float64)
+    t0 = time.perf_counter()
+    np.matmul(A, B)
+    dt = time.perf_counter() - t0
+    return {"value": round(2.0 * rows * n * n / dt / 1e12, 4), "unit": "TFLOP/s",
+            "sample": f"numpy float64 matmul ({rows}x{n}) . ({n}x{n}), {dt:.2f} s"}
+
+
 class Ctx:
     def __init__(self, args):
         import torch
@@ -361,6 +377,8 @@ def main():
         log(f"cpu_baseline: oracle float64 GEMM on {args.cpu_rows} rows of the 8192^3 problem")
         cpu = cpu_baseline_gemm(8192, args.cpu_rows)
         log(f"cpu_baseline: {cpu['value'] * 1e3:.2f} GFLOP/s")
+        secondary["cpu_numpy_gemm"] = cpu_numpy_gemm(8192, args.cpu_rows)
+        log(f"numpy float64 matmul: {secondary['cpu_numpy_gemm']['value'] * 1e3:.1f} GFLOP/s")
 
     roofline = None
     if head is not None:
