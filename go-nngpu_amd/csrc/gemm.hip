@@ -456,8 +456,9 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32_kernel(GemmParams p) {
 //  * global -> LDS copies are buffer loads with the LDS-direct bit (16 bytes per lane
 //    written to M0 + 16*lane): no staging VGPRs and no ds_write instructions;
 //  * the LDS ring holds two slots of two consecutive K-tiles each (BK = 32, 64 KiB per
-//    slot at 256 x 256): one DMA burst fills a slot while the other is multiplied, and
-//    only one barrier per pair of K-tiles is needed;
+//    slot at 256 x 256): the DMA fills one slot while the other is multiplied (at
+//    256 x 256 in two bursts, A then B, spread over the MFMAs), and only one barrier per
+//    pair of K-tiles is needed;
 //  * out-of-range lanes (rows past M/N, the K tail) get a buffer offset beyond the
 //    descriptor's range, which the hardware turns into zeros;
 //  * K-contiguous operands are stored in 1 KiB chunks of 8 rows x 64 k (both K-tiles
@@ -550,7 +551,8 @@ __device__ __forceinline__ void sched_interleave() {
 
 // Main loop of the ring kernel for one output tile (rows m0.., columns n0.., batch z),
 // nk K-tiles: adds the products into acc. K-tiles go in pairs: slot pp & 1 holds tiles
-// 2pp and 2pp+1 of A, then of B (one single-tile region each). Per pair, the even step
+// 2pp and 2pp+1 of A, then of B (a K-contiguous operand holds both tiles in each of its
+// chunks; an MN-contiguous one has a region per tile). Per pair, the even step
 // multiplies tile 2pp while reading tile 2pp+1's fragments from the same, already
 // visible slot; the odd step waits for pair pp+1, passes the pair's one barrier,
 // refills the slot just consumed with pair pp+2 and reads tile 2pp+2's fragments.
