@@ -579,7 +579,7 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
   // 872 -> 851 us) and 10% slower for the 4-wave 128 x 96 tiles of the C4 shape; four
   // bursts measured within 1% of two.
   constexpr int kDmaParts = NW >= 8 ? 2 : 1;
-  static_assert(FM % kDmaParts == 0 && (kDmaParts == 1 || (FM % 2 == 0 && FN % 2 == 0)), "DMA bursts / read parts");
+  static_assert(FM % kDmaParts == 0 && FM % 2 == 0, "DMA bursts / read parts");
   static_assert((!TA || BM >= 128) && (TB || BN >= 128), "MN-contiguous rows need 8 XOR blocks of 32 B");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
