@@ -166,7 +166,18 @@ def run_c3(c, steps, warmup):
     tf = flop / (ms * 1e-3) / 1e12
     assert c.torch.isfinite(out[:64]).all().item()
     log(f"c3: {ms:.4f} ms/launch, {tf:.1f} TFLOP/s ({100 * tf / PEAK_F16_TFLOPS:.1f}% of fp16 dense peak)")
+    c.vendor_c3 = vendor_reference(c, lambda: c.torch.matmul(a16, b16), flop, steps, "c3")
     return {"ms": ms, "tflops": tf, "flop": flop}
+
+
+def vendor_reference(c, fn, flop, steps, name):
+    """The same product through torch.matmul (hipBLASLt) on the same box, for scale only:
+    its output is fp16 (half the C bytes of ours) and it is never `value`."""
+    ms = timed(fn, steps, 10, c.stream, MIN_WARM_MS)
+    tf = flop / (ms * 1e-3) / 1e12
+    log(f"{name} torch.matmul (hipBLASLt, fp16 out): {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s")
+    return {"ms": round(ms, 5), "TFLOP/s": round(tf, 2),
+            "what": "torch.matmul on the same fp16 operands (hipBLASLt), fp16 output, no epilogue"}
 
 
 def run_c2(c, steps, warmup):
@@ -200,6 +211,7 @@ def run_c4(c, steps, warmup):
         res[f"c4_linear_{name}"] = {"ms": round(ms, 5), "TFLOP/s": round(tf, 2),
                                     "frac_fp16_peak": round(tf / PEAK_F16_TFLOPS, 4)}
         log(f"c4 {name}: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s")
+    res["c4_torch_matmul_reference"] = vendor_reference(c, lambda: c.torch.matmul(X16, W16.t()), flop, steps, "c4")
     return res
 
 
@@ -345,6 +357,7 @@ def main():
     head, secondary = None, {}
     if "c3" in only:
         head = run_c3(c, steps, warmup)
+        secondary["c3_torch_matmul_reference"] = c.vendor_c3
         c.torch.cuda.empty_cache()
     if "c2" in only:
         secondary.update(run_c2(c, steps2, 3))
