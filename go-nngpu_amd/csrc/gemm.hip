@@ -631,19 +631,20 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
     const long krem_l = p.K - (long)pp * 2 * BK;
     const int krem = (int)(krem_l < 0 ? 0 : (krem_l > 2 * BK ? 2 * BK : krem_l));
     const int half = NPRT / 2;
+    const bool last_call = q == NPRT - 1;
     if (q < half) {
 #pragma unroll
       for (int i = 0; i < IPA; ++i)
         if (i * half / IPA == q)
           dma16(ra, kla[i] < krem ? voa[i] : kOutOfRange, __builtin_amdgcn_readfirstlane(st + (wave * IPA + i) * 1024));
-      return;
-    }
+    } else {
 #pragma unroll
-    for (int i = 0; i < IPB; ++i)
-      if (i * half / IPB == q - half)
-        dma16(rb, klb[i] < krem ? vob[i] : kOutOfRange,
-              __builtin_amdgcn_readfirstlane(st + 2 * OPA + (wave * IPB + i) * 1024));
-    if (q == NPRT - 1) {
+      for (int i = 0; i < IPB; ++i)
+        if (i * half / IPB == q - half)
+          dma16(rb, klb[i] < krem ? vob[i] : kOutOfRange,
+                __builtin_amdgcn_readfirstlane(st + 2 * OPA + (wave * IPB + i) * 1024));
+    }
+    if (last_call) {
       rsrc_advance(ra, a_step);
       rsrc_advance(rb, b_step);
     }
