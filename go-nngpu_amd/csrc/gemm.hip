@@ -577,9 +577,9 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
   // Splitting each pair's DMA into two bursts (A at the barrier, B halfway through the
   // MFMAs) measured 2-4% faster at 256 x 256 with 8 waves (8192^3: NN 884 -> 851 us, NT
   // 872 -> 851 us) and 10% slower for the 4-wave 128 x 96 tiles of the C4 shape; four
-  // bursts measured within 1% of two.
+  // bursts (A and B halves at quarter points) measured within 1% of two.
   constexpr int kDmaParts = NW >= 8 ? 2 : 1;
-  static_assert(FM % kDmaParts == 0 && FM % 2 == 0, "DMA bursts / read parts");
+  static_assert(kDmaParts == 1 || FM % 4 == 0, "DMA burst split rows");
   static_assert((!TA || BM >= 128) && (TB || BN >= 128), "MN-contiguous rows need 8 XOR blocks of 32 B");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -743,19 +743,21 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (kDmaParts > 1) {
-      // The pair's DMA in kDmaParts bursts spread over the tile's MFMAs (A's shares first);
-      // the next tile's fragment reads go with the MFMAs of the first two regions.
-      constexpr int QM = FM / kDmaParts;  // MFMA rows per region
-#pragma unroll
-      for (int q = 0; q < kDmaParts; ++q) {
-        if (q) __builtin_amdgcn_sched_barrier(0);
-        issue(pp + 2, cur, q, kDmaParts);
-        constexpr int NRH = (TA ? 2 : 1) * (FM / 2) + (TB ? 1 : 2) * (FN / 2);  // reads per half
-        if (q < 2) read_part(cur ^ 1, 0, 0, q, 2);
-        mfma_rows(1, q * QM, (q + 1) * QM);
-        if (q < 2) sched_interleave<QM * FN, NRH>();
-        else sched_interleave<QM * FN, 0>();
-      }
+      // Two bursts: A's copies with the first R0 MFMA rows, B's with the rest; the next
+      // tile's fragment reads are split between the two regions. B's burst after 3/4 of
+      // the rows measured best for NN (8192^3: 808 -> 803 us against 1/2; 1/4: 824 us),
+      // after 1/2 for NT / TN / TT (3/4 cost them 1-1.5%).
+      constexpr int R0 = (!TA && !TB) ? 3 * FM / 4 : FM / 2;
+      constexpr int NRH = (TA ? 2 : 1) * (FM / 2) + (TB ? 1 : 2) * (FN / 2);  // reads per part
+      issue(pp + 2, cur, 0, 2);
+      read_part(cur ^ 1, 0, 0, 0, 2);
+      mfma_rows(1, 0, R0);
+      sched_interleave<R0 * FN, NRH>();
+      __builtin_amdgcn_sched_barrier(0);
+      issue(pp + 2, cur, 1, 2);
+      read_part(cur ^ 1, 0, 0, 1, 2);
+      mfma_rows(1, R0, FM);
+      sched_interleave<(FM - R0) * FN, NRH>();
     } else {
       issue(pp + 2, cur, 0, 2);
       issue(pp + 2, cur, 1, 2);
