@@ -43,7 +43,7 @@ for _p in (ROOT, os.path.join(ROOT, "go-nngpu_amd")):
 METRIC = "GEMM TFLOP/s + % MFMA peak (fp32, fp16→fp32); CSR SpMM HBM GB/s, 1 MI355X"
 PEAK_F16_TFLOPS = 2516.6  # dense MFMA fp16, 256 CU x 4096 flop/clk x 2.4 GHz
 PEAK_F32_TFLOPS = 157.3   # fp32 MFMA
-MIN_WARM_MS = 50.0        # least untimed GPU time per secondary leg (see timed())
+MIN_WARM_MS = 50.0        # least untimed GPU time before each timed leg (see timed())
 PEAK_HBM_GBS = 8000.0
 ALL = ("c3", "c2", "c4", "spmm", "spmv", "e2e", "copy")
 
@@ -56,9 +56,10 @@ def timed(fn, steps, warmup, stream, min_warm_ms=0.0):
     """Mean ms per call of fn() over `steps` calls, events recorded on `stream`.
 
     `warmup` untimed calls come first; with min_warm_ms > 0 more untimed calls follow
-    until at least that much GPU time has gone into warming up. The secondary legs use
-    this: 50 launches of a 50 us kernel are 2.5 ms, and short kernels measured 10-25%
-    slow that early after a leg change (clock ramp), settling within ~30 ms."""
+    until at least that much GPU time has gone into warming up. Every leg uses this, the
+    headline and its hipBLASLt line included, so all are timed at the same clock state:
+    50 launches of a 50 us kernel are 2.5 ms, and kernels measured 10-25% slow that
+    early after a leg change (clock ramp), settling within ~30 ms."""
     import torch
 
     for _ in range(warmup):
@@ -107,7 +108,41 @@ def cpu_baseline_gemm(n, rows):
     dt = time.perf_counter() - t0
     return {"value": 2.0 * rows * n * n / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"oracle float64 GEMM ({rows}x{n}) . ({n}x{n}): {rows} of the {n} output rows of the "
-                      f"headline problem, {dt:.1f} s on {threads} threads"}
+                      f"headline problem, {dt:.1f} s on {threads} threads (the GPU box's CPU share is 16)",
+            "host": host_info()}
+
+
+def host_info():
+    """The CPU the baselines ran on: logical CPUs of the host, CPUs this process may use,
+    the OpenMP thread setting and the model name."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    return {"nproc": os.cpu_count(), "affinity": affinity, "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+            "cpu_model": model}
+
+
+def cpu_gemm_1thread(n, rows):
+    """The same oracle float64 GEMM restatement on one thread (a smaller row sample)."""
+    from oracle import oracle as O
+
+    A = O.normal((rows, n), 42, 101)
+    B = O.normal((n, n), 42, 102, 0.0, 0.02)
+    t0 = time.perf_counter()
+    O.gemm_f64(A, B, nthreads=1)
+    dt = time.perf_counter() - t0
+    return {"value": round(2.0 * rows * n * n / dt / 1e12, 5), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"oracle float64 GEMM ({rows}x{n}) . ({n}x{n}) on one thread, {dt:.1f} s"}
 
 
 def cpu_numpy_gemm(n, rows):
@@ -160,8 +195,9 @@ def run_c3(c, steps, warmup):
     a16 = c.f16_normal((n, n), 1, 1.0)
     b16 = c.f16_normal((n, n), 2, 0.02)
     out = c.empty((n, n))
-    log(f"c3: {warmup} warmup + {steps} timed fp16 GEMM 8192^3 launches")
-    ms = timed(lambda: c.G.gemm(a16, b16, out, stream_ptr=c.sp), steps, warmup, c.stream)
+    log(f"c3: {warmup} warmup launches (then at least {MIN_WARM_MS:.0f} ms of untimed launches) + {steps} timed "
+        f"fp16 GEMM 8192^3 launches")
+    ms = timed(lambda: c.G.gemm(a16, b16, out, stream_ptr=c.sp), steps, warmup, c.stream, MIN_WARM_MS)
     flop = 2.0 * n ** 3
     tf = flop / (ms * 1e-3) / 1e12
     assert c.torch.isfinite(out[:64]).all().item()
@@ -253,6 +289,80 @@ def cpu_baseline_sparse(c, kind, rows):
             "ms_full_matrix": round(dt * 1e3 * M / rows, 2),
             "sample": f"oracle restatement of the reference's single-threaded CSR {kind} loop on rows 0..{rows - 1} "
                       f"of the {M}-row C5 matrix ({end} stored entries), {dt:.2f} s"}
+
+
+def cpu_parallel_sparse(c, kind):
+    """The same CSR loop with its rows split over the host threads (OpenMP; each row as the
+    reference computes it, bit-identical), on the whole C5 matrix."""
+    from oracle import oracle as O
+
+    rp, col, val = c.csr_host
+    M = rp.size - 1
+    nnz = int(rp[-1])
+    threads = O.threads()
+    if kind == "spmm":
+        N = 256
+        D = O.normal((M, N), 42, 108)
+        O.spmm_f32_par(rp[:1025], col[:int(rp[1024])], val[:int(rp[1024])], D, threads)  # page in, spin up
+        t0 = time.perf_counter()
+        O.spmm_f32_par(rp, col, val, D, threads)
+        dt = time.perf_counter() - t0
+        b_s = 4 * (M + 1) + 8 * nnz + 4 * nnz * N + 4 * M * N
+    else:
+        x = O.normal((M,), 42, 109)
+        O.spmv_f32_par(rp, col, val, x, threads)
+        t0 = time.perf_counter()
+        O.spmv_f32_par(rp, col, val, x, threads)
+        dt = time.perf_counter() - t0
+        b_s = 4 * (M + 1) + 12 * nnz + 4 * M
+    return {"value": round(b_s / dt / 1e9, 2), "unit": "GB/s (streamed-bytes model)", "cores": threads,
+            "kind": "port", "ms_full_matrix": round(dt * 1e3, 3),
+            "sample": f"the reference's CSR {kind} loop split by rows over {threads} OpenMP threads, whole C5 matrix "
+                      f"({nnz} stored entries)"}
+
+
+def run_part1_sparse(c, kind, steps, kernel_ms):
+    """C5 through the reference-compatible entry point (perform_sparse_dense_matmul or
+    perform_sparse_matvec) as the unchanged Go caller makes it: values in a GPUPtr buffer,
+    row pointers and column indices as host arrays on every call. The first call uploads
+    and validates the index arrays; later calls reuse the copy kept with the values
+    buffer. Wall clock per synchronous call, against the device-API kernel time."""
+    import numpy as np
+
+    G = c.G
+    rp, col, val = c.csr_host
+    M = rp.size - 1
+    N = 256 if kind == "spmm" else 1
+    from oracle import oracle as O
+
+    dense = O.normal((M, N), 42, 110) if kind == "spmm" else O.normal((M,), 42, 111)
+    bv, bd, bo = G.Buffer.from_array(val), G.Buffer.from_array(dense), G.Buffer(M * N * 4)
+    if kind == "spmm":
+        args = lambda: (bv.handle, rp.ctypes.data, rp.size, col.ctypes.data, col.size, M, M, val.size, bd.handle, M,
+                        N, bo.handle, M, N, None)
+        name = "perform_sparse_dense_matmul"
+    else:
+        args = lambda: (bv.handle, rp.ctypes.data, rp.size, col.ctypes.data, col.size, M, M, val.size, bd.handle, M,
+                        bo.handle, M, None)
+        name = "perform_sparse_matvec"
+    t0 = time.perf_counter()
+    G.call(name, *args())
+    first = (time.perf_counter() - t0) * 1e3
+    for _ in range(3):
+        G.call(name, *args())
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        G.call(name, *args())
+    steady = (time.perf_counter() - t0) * 1e3 / steps
+    out = bo.to_array((M, N) if kind == "spmm" else (M,))
+    assert np.isfinite(out[:16]).all()
+    for b in (bv, bd, bo):
+        b.release()
+    log(f"{kind} via {name}: first call {first:.2f} ms, steady {steady:.4f} ms (kernel {kernel_ms:.4f} ms)")
+    return {"first_call_ms": round(first, 3), "steady_ms": round(steady, 4),
+            "steady_over_kernel": round(steady / kernel_ms, 3),
+            "what": f"{name} with host index arrays (Go call sequence), wall clock per synchronous call; the first "
+                    f"call uploads and validates the indices, later calls reuse them"}
 
 
 def run_spmm(c, steps, warmup, csr):
@@ -369,14 +479,20 @@ def main():
         csr = csr_workload(c)
         if "spmm" in only:
             secondary["c5_spmm"] = run_spmm(c, steps2 * 2, 3, csr)
+            secondary["c5_spmm"]["part1_abi"] = run_part1_sparse(c, "spmm", steps2, secondary["c5_spmm"]["ms"])
             if not args.no_cpu:
                 secondary["c5_spmm"]["cpu_baseline"] = cpu_baseline_sparse(c, "spmm", 16384)
                 log(f"cpu_baseline spmm: {secondary['c5_spmm']['cpu_baseline']['value']} GB/s on 1 thread")
+                secondary["c5_spmm"]["cpu_parallel"] = cpu_parallel_sparse(c, "spmm")
+                log(f"cpu parallel spmm: {secondary['c5_spmm']['cpu_parallel']['value']} GB/s")
         if "spmv" in only:
             secondary["c5_spmv"] = run_spmv(c, steps2 * 4, 5, csr)
+            secondary["c5_spmv"]["part1_abi"] = run_part1_sparse(c, "spmv", steps2 * 4, secondary["c5_spmv"]["ms"])
             if not args.no_cpu:
                 secondary["c5_spmv"]["cpu_baseline"] = cpu_baseline_sparse(c, "spmv", 65536)
                 log(f"cpu_baseline spmv: {secondary['c5_spmv']['cpu_baseline']['value']} GB/s on 1 thread")
+                secondary["c5_spmv"]["cpu_parallel"] = cpu_parallel_sparse(c, "spmv")
+                log(f"cpu parallel spmv: {secondary['c5_spmv']['cpu_parallel']['value']} GB/s")
         del csr
         c.torch.cuda.empty_cache()
     if "e2e" in only:
@@ -392,6 +508,8 @@ def main():
         log(f"cpu_baseline: {cpu['value'] * 1e3:.2f} GFLOP/s")
         secondary["cpu_numpy_gemm"] = cpu_numpy_gemm(8192, args.cpu_rows)
         log(f"numpy float64 matmul: {secondary['cpu_numpy_gemm']['value'] * 1e3:.1f} GFLOP/s")
+        secondary["cpu_gemm_1thread"] = cpu_gemm_1thread(8192, 96)
+        log(f"cpu_baseline 1 thread: {secondary['cpu_gemm_1thread']['value'] * 1e3:.2f} GFLOP/s")
 
     roofline = None
     if head is not None:

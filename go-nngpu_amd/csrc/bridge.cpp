@@ -1,8 +1,11 @@
 // bridge.cpp — extern "C" entry points of libgonngpu.so (declared in include/gonngpu.h).
 // Part 1 keeps the reference bridge's names, signatures and return codes
 // (internal/cgo/metal_bridge*.m); Part 2 is the device-pointer API.
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
+#include <memory>
+#include <unordered_map>
 #include <vector>
 
 #include "common.h"
@@ -28,10 +31,113 @@ bool fits(const Buffer *b, long rows, long cols, size_t esz) {
   return gn::matrix_bytes(rows, cols, esz, &n) && n <= b->bytes;
 }
 
-// Uploads host CSR index arrays into device scratch, runs fn, and converts the
-// kernel's validation flags into the reference's error convention.
+// ---------------------------------------------------------------- CSR index cache
+// The Part-1 sparse entries receive the index arrays as host pointers on every call
+// (sparse-matrix.go:167-170), while the values already live in a GPUPtr buffer. The
+// device copy of the indices is kept with that values buffer: the first call uploads
+// and validates them, later calls with the same buffer, the same host arrays and the
+// same row pointers reuse the copy and skip the validation read-back. The entry goes
+// when the values buffer is released (a new EnsureGPU makes a new buffer and a new
+// entry), or when gn_csr_indices_changed is called for it. Row pointers are compared
+// on every call (4(rows+1) bytes); column indices changed in place under an unchanged
+// values buffer need gn_csr_indices_changed, just as changed values need a new upload.
+// GONNGPU_CSR_CACHE=0 turns the cache off (upload and validate on every call).
+struct CsrEntry {
+  const int *host_rp = nullptr, *host_col = nullptr;
+  long rows = 0, nnz = 0;
+  std::vector<int> rp_copy;
+  void *d_rp = nullptr, *d_col = nullptr;
+  std::atomic<bool> validated{false};
+  ~CsrEntry() {  // stream-ordered: after every call already enqueued with this entry
+    gn::dev_free(d_rp);
+    gn::dev_free(d_col);
+  }
+};
+
+std::mutex g_csr_mu;
+std::unordered_map<const Buffer *, std::shared_ptr<CsrEntry>> &csr_cache() {
+  static auto *m = new std::unordered_map<const Buffer *, std::shared_ptr<CsrEntry>>();
+  return *m;
+}
+
+bool csr_cache_enabled() {
+  static const bool on = [] {
+    const char *v = getenv("GONNGPU_CSR_CACHE");
+    return !(v && v[0] == '0');
+  }();
+  return on;
+}
+
+// The cached device copy of (rowptr, cols) for values buffer `key`, uploading it when
+// there is none or it no longer matches the caller's arrays.
+std::shared_ptr<CsrEntry> csr_entry(const Buffer *key, const int *rowptr, long rows, const int *cols, long nnz,
+                                    hipStream_t s, CError *err) {
+  const size_t rp_bytes = sizeof(int) * (size_t)(rows + 1);
+  {
+    std::lock_guard<std::mutex> lk(g_csr_mu);
+    auto it = csr_cache().find(key);
+    if (it != csr_cache().end()) {
+      std::shared_ptr<CsrEntry> e = it->second;
+      if (e->host_rp == rowptr && e->host_col == cols && e->rows == rows && e->nnz == nnz &&
+          memcmp(e->rp_copy.data(), rowptr, rp_bytes) == 0)
+        return e;
+    }
+  }
+  auto e = std::make_shared<CsrEntry>();
+  e->host_rp = rowptr;
+  e->host_col = cols;
+  e->rows = rows;
+  e->nnz = nnz;
+  e->rp_copy.assign(rowptr, rowptr + rows + 1);
+  e->d_rp = gn::dev_alloc(rp_bytes, err);
+  if (!e->d_rp) return nullptr;
+  if (nnz > 0) {
+    e->d_col = gn::dev_alloc(sizeof(int) * (size_t)nnz, err);
+    if (!e->d_col) return nullptr;
+  }
+  if (gn::upload(e->d_rp, rowptr, rp_bytes, s, err)) return nullptr;
+  if (nnz > 0 && gn::upload(e->d_col, cols, sizeof(int) * (size_t)nnz, s, err)) return nullptr;
+  std::lock_guard<std::mutex> lk(g_csr_mu);
+  csr_cache()[key] = e;  // replaces a stale entry (freed once its last user lets go)
+  return e;
+}
+
+void csr_cache_forget(const Buffer *key, const CsrEntry *only) {
+  std::lock_guard<std::mutex> lk(g_csr_mu);
+  auto it = csr_cache().find(key);
+  if (it != csr_cache().end() && (!only || it->second.get() == only)) csr_cache().erase(it);
+}
+
+// Uploads host CSR index arrays (or takes the cached copy kept with the values buffer
+// `values`, when there is one), runs fn, and converts the kernel's validation flags into
+// the reference's error convention.
 template <typename Fn>
-int with_csr(const int *rowptr, long rows, const int *cols, long nnz, hipStream_t s, CError *err, Fn fn) {
+int with_csr(const Buffer *values, const int *rowptr, long rows, const int *cols, long nnz, hipStream_t s,
+             CError *err, Fn fn) {
+  const auto bad = [&](int f0, int f1) {
+    if (f0) return set_error(err, -3, "malformed CSR: row pointers are not monotone within [0, nnz]");
+    if (f1) return set_error(err, -3, "malformed CSR: column index outside [0, cols)");
+    return 0;
+  };
+  if (values && csr_cache_enabled()) {
+    std::shared_ptr<CsrEntry> e = csr_entry(values, rowptr, rows, cols, nnz, s, err);
+    if (!e) return -3;
+    const int32_t *d_rp = static_cast<const int32_t *>(e->d_rp), *d_col = static_cast<const int32_t *>(e->d_col);
+    if (e->validated.load(std::memory_order_acquire)) return fn(d_rp, d_col, nullptr);
+    Scratch d_flags;
+    d_flags.p = gn::dev_alloc(2 * sizeof(int), err);
+    if (!d_flags.p) return -3;
+    if (int rc = gn::launch_zero_i32(static_cast<int *>(d_flags.p), 2, s, err)) return rc;
+    if (int rc = fn(d_rp, d_col, static_cast<int *>(d_flags.p))) return rc;
+    int flags[2] = {0, 0};
+    if (int rc = gn::download(flags, d_flags.p, sizeof(flags), s, err)) return rc;
+    if (int rc = bad(flags[0], flags[1])) {
+      csr_cache_forget(values, e.get());
+      return rc;
+    }
+    e->validated.store(true, std::memory_order_release);
+    return 0;
+  }
   Scratch d_rp, d_col, d_flags;
   d_rp.p = gn::dev_alloc(sizeof(int) * (size_t)(rows + 1), err);
   if (!d_rp.p) return -3;
@@ -50,9 +156,7 @@ int with_csr(const int *rowptr, long rows, const int *cols, long nnz, hipStream_
     return rc;
   int flags[2] = {0, 0};
   if (int rc = gn::download(flags, d_flags.p, sizeof(flags), s, err)) return rc;
-  if (flags[0]) return set_error(err, -3, "malformed CSR: row pointers are not monotone within [0, nnz]");
-  if (flags[1]) return set_error(err, -3, "malformed CSR: column index outside [0, cols)");
-  return 0;
+  return bad(flags[0], flags[1]);
 }
 
 // Device copy of a host array (n elements of T), released on scope exit.
@@ -101,6 +205,8 @@ int download_coo(const Scratch &ri, const Scratch &ci, const Scratch &vv, long n
 
 }  // namespace
 
+void gn::csr_cache_drop(const Buffer *b) { csr_cache_forget(b, nullptr); }
+
 extern "C" {
 
 // =========================================================================== Part 1
@@ -146,10 +252,10 @@ int release_gpu_buffer(GPUPtr gpuPtr) {
   if (!gpuPtr) return 0;
   Buffer *b = gn::as_buffer(gpuPtr);
   if (!b) return 0;
-  (void)hipDeviceSynchronize();  // no pending work may still reference the block
   void *d = b->dptr;
   if (gn::unregister_buffer(b)) {
-    gn::dev_free(d);
+    gn::csr_cache_drop(b);
+    gn::dev_free(d);  // stream-ordered: reused only after the library stream's work so far
     delete b;
   }
   return 0;
@@ -261,7 +367,7 @@ int perform_sparse_dense_matmul(GPUPtr aValuesPtr, int *aRowPtr, long aRowPtrLen
   if (!fits(b, bRows, bCols, 4) || !fits(c, resultRows, resultCols, 4) || (v && !fits(v, 1, aNNZ, 4)))
     return set_error(err, -2, "Buffer smaller than the matrix it describes.");
   const float *vals = v ? static_cast<const float *>(v->dptr) : nullptr;
-  return with_csr(aRowPtr, aRows, aColIndices, aNNZ, ctx->stream, err,
+  return with_csr(v, aRowPtr, aRows, aColIndices, aNNZ, ctx->stream, err,
                   [&](const int32_t *rp, const int32_t *col, int *flags) -> int {
                     int rc = gn::launch_spmm(aRows, bCols, aCols, aNNZ, rp, col, vals,
                                              static_cast<const float *>(b->dptr), bCols,
@@ -288,7 +394,7 @@ int perform_sparse_matvec(GPUPtr aValuesPtr, int *aRowPtr, long aRowPtrLen, int 
   if (!fits(x, 1, xSize, 4) || !fits(y, 1, resultSize, 4) || (v && !fits(v, 1, aNNZ, 4)))
     return set_error(err, -1, "Buffer smaller than the vector it describes.");
   const float *vals = v ? static_cast<const float *>(v->dptr) : nullptr;
-  return with_csr(aRowPtr, aRows, aColIndices, aNNZ, ctx->stream, err,
+  return with_csr(v, aRowPtr, aRows, aColIndices, aNNZ, ctx->stream, err,
                   [&](const int32_t *rp, const int32_t *col, int *flags) -> int {
                     int rc = gn::launch_spmv(aRows, aCols, aNNZ, rp, col, vals,
                                              static_cast<const float *>(x->dptr), static_cast<float *>(y->dptr),
@@ -422,7 +528,7 @@ int perform_dense_sparse_matmul(GPUPtr aMatrixPtr, long aRows, long aCols, GPUPt
                                   err);
   if (rc) return rc;
   const float *vals = bv ? static_cast<const float *>(bv->dptr) : nullptr;
-  rc = with_csr(bColPtr, bCols, bRowIndices, bNNZ, s, err,
+  rc = with_csr(bv, bColPtr, bCols, bRowIndices, bNNZ, s, err,
                 [&](const int32_t *cp, const int32_t *rows, int *flags) -> int {
                   int r = gn::launch_spmm(bCols, aRows, aCols, bNNZ, cp, rows, vals, static_cast<const float *>(at.p),
                                           aRows, static_cast<float *>(ct.p), aRows, flags, s, err);
@@ -540,7 +646,7 @@ int perform_sparse_to_dense(GPUPtr valuesPtr, int *rowPtr, long rowPtrLen, int *
     return set_error(err, -1, "Buffer smaller than the matrix it describes.");
   if (rows == 0 || cols == 0) return 0;
   const float *vals = v ? static_cast<const float *>(v->dptr) : nullptr;
-  return with_csr(rowPtr, rows, colIndices, nnz, ctx->stream, err,
+  return with_csr(v, rowPtr, rows, colIndices, nnz, ctx->stream, err,
                   [&](const int32_t *rp, const int32_t *col, int *flags) -> int {
                     int rc = gn::launch_csr_to_dense(rows, cols, nnz, rp, col, vals, static_cast<float *>(d->dptr),
                                                      flags, ctx->stream, err);
@@ -624,8 +730,19 @@ int gn_malloc(void **ptr, size_t bytes, CError *err) {
 
 int gn_free(void *ptr) {
   if (!ptr) return 0;
-  (void)hipDeviceSynchronize();
   gn::dev_free(ptr);
+  return 0;
+}
+
+int gn_csr_indices_changed(GPUPtr valuesPtr) {
+  Buffer *b = gn::as_buffer(valuesPtr);
+  if (b) gn::csr_cache_drop(b);
+  return 0;
+}
+
+int gn_free_async(void *ptr, void *stream) {
+  if (!ptr) return 0;
+  gn::dev_free_on(ptr, gn::resolve_stream(stream));
   return 0;
 }
 

@@ -43,11 +43,15 @@ hipStream_t resolve_stream(void *stream);  // NULL -> library stream
 // ---------------------------------------------------------------- allocator
 // Caching device allocator: size-binned free lists over hipMalloc, never returns
 // memory to the driver while the process lives (reuse keeps hipMalloc off hot paths).
+// Release is stream-ordered: dev_free_on(p, s) hands p to a new owner only after the
+// work enqueued on s before the call has completed; dev_free orders on the library
+// stream (every Part-1 call and every scratch block of the library runs there).
 void *dev_alloc(size_t bytes, CError *err);
+void dev_free_on(void *p, hipStream_t s);
 void dev_free(void *p);
 void memory_stats(long *cur, long *peak, long *n);
-// Device scratch owned by the library, one block per stream, grown on demand (after
-// synchronising the stream). lk holds a library mutex on return: keep it until every
+// Device scratch owned by the library, one block per stream, grown on demand (the old
+// block is released in the stream's order). lk holds a library mutex on return: keep it until every
 // kernel that uses the scratch is enqueued, so that another host thread cannot enqueue
 // work that reuses it in between (kernels on one stream run in order).
 void *stream_scratch(hipStream_t s, size_t bytes, std::unique_lock<std::mutex> &lk, CError *err);
@@ -65,6 +69,8 @@ struct Buffer {
 };
 constexpr uint64_t kBufferMagic = 0x676E6E6770754246ULL;  // "gnngpuBF"
 Buffer *as_buffer(GPUPtr p);  // nullptr if p is not a live handle
+// Drops the device copy of the CSR index arrays kept with values buffer b (bridge.cpp).
+void csr_cache_drop(const Buffer *b);
 
 // ---------------------------------------------------------------- kernel launchers
 // All launchers validate shapes on the host before any launch, then enqueue on s.

@@ -83,11 +83,22 @@ hipStream_t resolve_stream(void *stream) {
 }
 
 // ------------------------------------------------------------------ allocator
+// Size-binned caching allocator with stream-ordered release. A freed block is not reused
+// at once: dev_free_on records an event on the stream the block was last used on, and the
+// block waits in `pending` until that event has completed. Work enqueued before the free
+// therefore never sees the block handed to a new owner, without the device-wide
+// synchronisation a plain free would need.
 namespace {
+struct PendingBlock {
+  void *ptr;
+  hipEvent_t ev;
+};
 struct Pool {
   std::mutex mu;
-  std::unordered_map<size_t, std::vector<void *>> free_lists;  // rounded size -> blocks
+  std::unordered_map<size_t, std::vector<void *>> free_lists;  // rounded size -> ready blocks
+  std::unordered_map<size_t, std::vector<PendingBlock>> pending;  // rounded size -> blocks in flight
   std::unordered_map<void *, size_t> live;                     // block -> rounded size
+  std::vector<hipEvent_t> spare_events;
   long cur = 0, peak = 0;
   long fail_after = -1;  // fault injection: GONNGPU_FAIL_ALLOC_AFTER
   long n_calls = 0;
@@ -109,7 +120,33 @@ size_t round_size(size_t b) {
   return (b + g - 1) / g * g;
 }
 
+// Moves pending blocks of size r whose event has completed to the free list.
+void reclaim_locked(Pool &p, size_t r) {
+  auto it = p.pending.find(r);
+  if (it == p.pending.end()) return;
+  auto &v = it->second;
+  for (size_t i = 0; i < v.size();) {
+    if (hipEventQuery(v[i].ev) == hipSuccess) {
+      p.free_lists[r].push_back(v[i].ptr);
+      p.spare_events.push_back(v[i].ev);
+      v[i] = v.back();
+      v.pop_back();
+    } else {
+      (void)hipGetLastError();  // hipErrorNotReady is not an error here
+      ++i;
+    }
+  }
+}
+
+// Returns every cached block to the driver (after the work still using pending ones).
 void release_cached_locked(Pool &p) {
+  for (auto &kv : p.pending)
+    for (PendingBlock &b : kv.second) {
+      (void)hipEventSynchronize(b.ev);
+      p.free_lists[kv.first].push_back(b.ptr);
+      p.spare_events.push_back(b.ev);
+    }
+  p.pending.clear();
   for (auto &kv : p.free_lists)
     for (void *q : kv.second) (void)hipFree(q);
   p.free_lists.clear();
@@ -132,6 +169,10 @@ void *dev_alloc(size_t bytes, CError *err) {
   size_t r = round_size(bytes);
   void *ptr = nullptr;
   auto it = p.free_lists.find(r);
+  if (it == p.free_lists.end() || it->second.empty()) {
+    reclaim_locked(p, r);
+    it = p.free_lists.find(r);
+  }
   if (it != p.free_lists.end() && !it->second.empty()) {
     ptr = it->second.back();
     it->second.pop_back();
@@ -154,7 +195,7 @@ void *dev_alloc(size_t bytes, CError *err) {
   return ptr;
 }
 
-void dev_free(void *ptr) {
+void dev_free_on(void *ptr, hipStream_t s) {
   if (!ptr) return;
   Pool &p = pool();
   std::lock_guard<std::mutex> lk(p.mu);
@@ -163,8 +204,26 @@ void dev_free(void *ptr) {
   size_t r = it->second;
   p.live.erase(it);
   p.cur -= (long)r;
+  hipEvent_t ev = nullptr;
+  if (!p.spare_events.empty()) {
+    ev = p.spare_events.back();
+    p.spare_events.pop_back();
+  } else if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+    (void)hipGetLastError();
+    ev = nullptr;
+  }
+  if (ev && hipEventRecord(ev, s) == hipSuccess) {
+    p.pending[r].push_back(PendingBlock{ptr, ev});
+    return;
+  }
+  // No event: wait for the stream instead, then the block is free at once.
+  (void)hipGetLastError();
+  if (ev) p.spare_events.push_back(ev);
+  (void)hipStreamSynchronize(s);
   p.free_lists[r].push_back(ptr);
 }
+
+void dev_free(void *ptr) { dev_free_on(ptr, g_ctx.stream); }
 
 void memory_stats(long *cur, long *peak, long *n) {
   Pool &p = pool();
@@ -374,13 +433,7 @@ void *stream_scratch(hipStream_t s, size_t bytes, std::unique_lock<std::mutex> &
   StreamScratch &w = g_scratch[s];
   if (w.bytes < bytes) {
     if (w.ptr) {
-      // Kernels already enqueued on s may still read the old block.
-      hipError_t e = hipStreamSynchronize(s);
-      if (e != hipSuccess) {
-        hip_error(err, -6, "scratch: synchronize", e);
-        return nullptr;
-      }
-      dev_free(w.ptr);
+      dev_free_on(w.ptr, s);  // reused only after the kernels already enqueued on s
       w = StreamScratch{};
     }
     const size_t nb = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;

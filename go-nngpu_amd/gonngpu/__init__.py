@@ -74,6 +74,8 @@ SIGNATURES = {
     "gn_memory_stats": (None, [ctypes.POINTER(_L), ctypes.POINTER(_L), ctypes.POINTER(_L)]),
     "gn_malloc": (_I, [ctypes.POINTER(_VP), _SZ, _ERR]),
     "gn_free": (_I, [_VP]),
+    "gn_free_async": (_I, [_VP, _VP]),
+    "gn_csr_indices_changed": (_I, [_VP]),
     "gn_synchronize": (_I, [_VP, _ERR]),
     "gn_gemm": (_I, [_I, _I, _I, _L, _L, _L, _F, _VP, _L, _L, _VP, _L, _L, _F, _VP, _L, _L, _L, _VP, _I, _F, _VP,
                      _ERR]),

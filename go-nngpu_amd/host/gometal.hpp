@@ -422,21 +422,36 @@ class LinearLayer {
 std::shared_ptr<LinearLayer> NewLinearLayer(int inputSize, int outputSize, bool useBias, uint64_t seed = 1);
 
 // gonum-compatible dense wrapper (gpu/matrix/gonum-compat.go:9-110, :321-367, :744-827).
+//
+// T() returns a transposed view, as gonum's mat.Transpose does, instead of the reference's
+// materialised GPU transpose (gonum-compat.go:61-68): the view shares the tensor, and Dims,
+// At, Set and ToGonum read it transposed. Mul and GPUMatMul hand a view's tensor to the
+// GEMM with its transpose flag (the kernels read op(A) = A^T in place), so Mul(a.T(), b)
+// is one GEMM launch with no transpose kernel and no copy. GetTensor() of a view returns a
+// materialised transpose (a tensor of the view's shape); ReleaseGPU() of a view does
+// nothing (the view owns no device memory).
 class GPUDense : public mat::Matrix {
  public:
-  explicit GPUDense(TensorPtr t) : tensor_(std::move(t)) {}
+  explicit GPUDense(TensorPtr t, bool transposed = false) : tensor_(std::move(t)), trans_(transposed) {}
   void Dims(int &r, int &c) const override;
   double At(int i, int j) const override;         // panics on out-of-range indices
-  std::shared_ptr<mat::Matrix> T() const override;  // materialised GPU transpose
+  std::shared_ptr<mat::Matrix> T() const override;  // transposed view of the same tensor
   void Set(int i, int j, double v);
   void Mul(const mat::Matrix &a, const mat::Matrix &b);  // receiver := a*b (device-resident)
   std::shared_ptr<mat::Dense> ToGonum() const;
   void ReleaseGPU();
-  TensorPtr GetTensor() const { return tensor_; }
+  TensorPtr GetTensor() const;
+  bool IsTransposedView() const { return trans_; }
+  // The stored tensor and whether this matrix is its transpose (what the GEMM consumes).
+  const TensorPtr &Storage() const { return tensor_; }
 
  private:
   TensorPtr tensor_;
+  bool trans_ = false;
 };
+// C = op(A) * op(B) on the device, with op(X) = X^T when the flag is set: the GEMM reads
+// the stored operands in place (device-resident fp32 result).
+Result<TensorPtr> MatMulTransposed(Tensor &A, bool transA, Tensor &B, bool transB);
 std::shared_ptr<GPUDense> NewGPUDense(int rows, int cols, const std::vector<double> &data);
 std::shared_ptr<GPUDense> FromGonum(const mat::Matrix &m);
 std::shared_ptr<GPUDense> NewGPUDenseFromTensor(TensorPtr t);

@@ -3,6 +3,7 @@
 // (gpu/matrix/gonum-compat.go) and GPUSparse / GPUSparseMatMul
 // (gpu/matrix/sparse-gonum-compat.go). Failures panic, as the Go wrappers do.
 #include <cmath>
+#include <utility>
 
 #include "gometal.hpp"
 
@@ -85,6 +86,7 @@ std::shared_ptr<GPUDense> NewGPUDenseFromTensor(TensorPtr t) { return std::make_
 void GPUDense::Dims(int &r, int &c) const {
   r = tensor_->Shape[0];
   c = tensor_->Shape[1];
+  if (trans_) std::swap(r, c);
 }
 
 double GPUDense::At(int i, int j) const {
@@ -92,46 +94,79 @@ double GPUDense::At(int i, int j) const {
   int rows, cols;
   Dims(rows, cols);
   if (i < 0 || i >= rows || j < 0 || j >= cols) throw Panic("matrix index out of range");
-  return tensor_->Data[(size_t)i * cols + j];
+  const int ld = tensor_->Shape[1];
+  return trans_ ? tensor_->Data[(size_t)j * ld + i] : tensor_->Data[(size_t)i * ld + j];
 }
 
-std::shared_ptr<mat::Matrix> GPUDense::T() const {
-  auto [t, err] = Transpose(*tensor_);
-  if (err) panic(err);
-  return std::make_shared<GPUDense>(t);
-}
+std::shared_ptr<mat::Matrix> GPUDense::T() const { return std::make_shared<GPUDense>(tensor_, !trans_); }
 
 void GPUDense::Set(int i, int j, double v) {
   if (Error e = tensor_->RetrieveCPU()) panic(e);
   int rows, cols;
   Dims(rows, cols);
   if (i < 0 || i >= rows || j < 0 || j >= cols) throw Panic("matrix index out of range");
-  tensor_->Data[(size_t)i * cols + j] = (float)v;
+  const int ld = tensor_->Shape[1];
+  (trans_ ? tensor_->Data[(size_t)j * ld + i] : tensor_->Data[(size_t)i * ld + j]) = (float)v;
 }
+
+TensorPtr GPUDense::GetTensor() const {
+  if (!trans_) return tensor_;
+  auto [t, err] = Transpose(*tensor_);
+  if (err) panic(err);
+  return t;
+}
+
+namespace {
+// The stored tensor and transpose flag of a matrix operand: a GPUDense (or a view of one)
+// as it is, anything else converted by FromGonum (held in `keep`).
+Tensor &operand(const mat::Matrix &m, std::shared_ptr<GPUDense> &keep, bool &trans) {
+  if (const GPUDense *g = dynamic_cast<const GPUDense *>(&m)) {
+    trans = g->IsTransposedView();
+    return *g->Storage();
+  }
+  keep = FromGonum(m);
+  trans = false;
+  return *keep->Storage();
+}
+}  // namespace
 
 void GPUDense::Mul(const mat::Matrix &a, const mat::Matrix &b) {
-  // GPUDense operands are used as they are; anything else goes through FromGonum.
-  std::shared_ptr<GPUDense> ta, tb;
-  const GPUDense *ga = dynamic_cast<const GPUDense *>(&a);
-  const GPUDense *gb = dynamic_cast<const GPUDense *>(&b);
-  if (!ga) ta = FromGonum(a);
-  if (!gb) tb = FromGonum(b);
-  Tensor &A = ga ? *ga->tensor_ : *ta->tensor_;
-  Tensor &B = gb ? *gb->tensor_ : *tb->tensor_;
-  auto [result, err] = MatMul(A, B);
+  // GPUDense operands (and their T() views) are used as they are; anything else goes
+  // through FromGonum.
+  std::shared_ptr<GPUDense> ka, kb;
+  bool ta, tb;
+  Tensor &A = operand(a, ka, ta);
+  Tensor &B = operand(b, kb, tb);
+  auto [result, err] = MatMulTransposed(A, ta, B, tb);
   if (err) panic(err);
-  tensor_->ReleaseGPU();
+  if (!trans_) tensor_->ReleaseGPU();  // a view's tensor belongs to its parent
   tensor_ = result;  // device-resident until read
+  trans_ = false;
 }
 
-std::shared_ptr<mat::Dense> GPUDense::ToGonum() const { return to_dense(*tensor_); }
+std::shared_ptr<mat::Dense> GPUDense::ToGonum() const {
+  auto d = to_dense(*tensor_);
+  if (!trans_) return d;
+  int r, c;
+  Dims(r, c);
+  std::vector<double> t((size_t)r * (size_t)c);
+  for (int i = 0; i < r; ++i)
+    for (int j = 0; j < c; ++j) t[(size_t)i * c + j] = d->At(j, i);
+  return mat::NewDense(r, c, std::move(t));
+}
 
-void GPUDense::ReleaseGPU() { tensor_->ReleaseGPU(); }
+void GPUDense::ReleaseGPU() {
+  if (!trans_) tensor_->ReleaseGPU();
+}
 
 std::shared_ptr<mat::Dense> GPUMatMul(const mat::Matrix &a, const mat::Matrix &b) {
-  auto ga = FromGonum(a);
-  auto gb = FromGonum(b);
-  auto [result, err] = MatMul(*ga->GetTensor(), *gb->GetTensor());
+  // gonum-compat.go:342-367 converts both operands with FromGonum; GPUDense operands and
+  // their views are used in place instead (same values: FromGonum would copy them).
+  std::shared_ptr<GPUDense> ka, kb;
+  bool ta, tb;
+  Tensor &A = operand(a, ka, ta);
+  Tensor &B = operand(b, kb, tb);
+  auto [result, err] = MatMulTransposed(A, ta, B, tb);
   if (err) panic(err);
   auto out = to_dense(*result);
   result->ReleaseGPU();

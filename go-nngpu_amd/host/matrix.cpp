@@ -64,6 +64,27 @@ Result<TensorPtr> MatMul(Tensor &A, Tensor &B) {
   return {result, {}};
 }
 
+Result<TensorPtr> MatMulTransposed(Tensor &A, bool transA, Tensor &B, bool transB) {
+  if (!transA && !transB) return MatMul(A, B);
+  if (A.Shape.size() != 2 || B.Shape.size() != 2) return {nullptr, Errorf("MatMul requires 2D tensors (matrices)")};
+  const int M = transA ? A.Shape[1] : A.Shape[0], K = transA ? A.Shape[0] : A.Shape[1];
+  const int KB = transB ? B.Shape[1] : B.Shape[0], N = transB ? B.Shape[0] : B.Shape[1];
+  if (K != KB)
+    return {nullptr, Errorf("incompatible matrix dimensions for multiplication: A columns (%d) != B rows (%d)", K, KB)};
+  auto [result, rerr] = Tensor::NewDeviceResult({M, N});
+  if (rerr) return {nullptr, wrap("failed to create result tensor", rerr)};
+  if (Error e = A.EnsureGPU()) return {nullptr, wrap("failed to move tensor A to GPU", e)};
+  if (Error e = B.EnsureGPU()) return {nullptr, wrap("failed to move tensor B to GPU", e)};
+  if ((long)M * N == 0) return {result, {}};
+  CError ce{nullptr};
+  // The GEMM reads op(A) and op(B) in place: A stored [K, M] with transA, B [N, K] with transB.
+  int rc = gn_gemm(GN_F32, transA, transB, M, N, K, 1.0f, dptr(A), A.Shape[1], 0, dptr(B), B.Shape[1], 0, 0.0f,
+                   dptr(*result), N, 0, 1, nullptr, GN_ACT_NONE, 0.0f, nullptr, &ce);
+  if (rc == 0) rc = gn_synchronize(nullptr, &ce);
+  if (rc != 0) return {nullptr, op_error("GPU matrix multiplication", rc, ce)};
+  return {result, {}};
+}
+
 Result<TensorPtr> Transpose(Tensor &A) {
   if (A.Shape.size() != 2) return {nullptr, Errorf("Transpose requires 2D tensor (matrix)")};
   auto [result, rerr] = Tensor::NewDeviceResult({A.Shape[1], A.Shape[0]});

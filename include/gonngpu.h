@@ -59,7 +59,9 @@ int create_gpu_buffer(float *data, long length_bytes, GPUPtr *outGPUPtr, DeviceP
  * (metal_bridge_buffer.m:65-72), -4 copy failed. */
 int retrieve_gpu_buffer_data(GPUPtr gpuPtr, float *data, long length_bytes, CError *err);
 
-/* metal_bridge.h:25. Returns the allocation to the library's pool. NULL is a no-op. */
+/* metal_bridge.h:25. Returns the allocation to the library's pool, stream-ordered (see
+ * gn_free): it does not wait, and the memory is reused only after the library stream's
+ * work enqueued so far. NULL is a no-op. */
 int release_gpu_buffer(GPUPtr gpuPtr);
 
 /* metal_bridge.h:28-34. C[resultRows,resultCols] = A[aRows,aCols] * B[bRows,bCols],
@@ -93,6 +95,11 @@ int perform_batch_matmul_optimized(GPUPtr aPtr, GPUPtr bPtr, GPUPtr cPtr, long b
  * ActivationType codes (gpu/matrix/activation.go:20-29): 0 ReLU, 1 Sigmoid, 2 Tanh,
  * 4 LeakyReLU(alpha), 5 ELU(alpha), 6 Swish, 7 GELU (tanh form); any other code
  * (including 3 Softmax, which is not element-wise) is rejected with -1.
+ * Code 6 is always Swish. The reference's Go caller sends C.int(OpReLU) for a nil
+ * config.Activation (fused-operations.go:433), and OpReLU is 6 in the OpType enum
+ * (gradient.go:27-39), so that unchanged call would run Swish here. The call site
+ * must send ActivationType ReLU (0) for its documented "Default to ReLU"; the
+ * one-line Go change is part of the integration.
  * Codes: -1 invalid argument / NULL buffer / execution error (as the reference). */
 int perform_fused_linear_activation(GPUPtr input, long batch_size, long input_size, GPUPtr weight, long output_size,
                                     GPUPtr bias, int activation_type, float alpha, GPUPtr output, DevicePtr device,
@@ -102,6 +109,14 @@ int perform_fused_linear_activation(GPUPtr input, long batch_size, long input_si
  * pointers and column indices valid for the call, sparse-matrix.go:167-177) and B,
  * C dense row-major fp32. Sums duplicates and keeps explicit zeros exactly as the
  * reference loop (metal_bridge_sparse.m:117-133); nnz = 0 returns C = 0.
+ * Index residency: the device copy of the index arrays is kept with the values
+ * buffer. The first call uploads and validates them; later calls with the same
+ * values buffer, the same host arrays and equal row pointers reuse that copy (no
+ * upload, no validation read-back). The copy goes with release_gpu_buffer of the
+ * values buffer. Column indices changed in place while the values buffer lives need
+ * gn_csr_indices_changed(aValuesPtr) before the next call, as changed values need a
+ * new upload. The same holds for perform_sparse_matvec, perform_sparse_to_dense and
+ * the CSC arrays of perform_dense_sparse_matmul. GONNGPU_CSR_CACHE=0 disables it.
  * Codes: -1 NULL buffer, -2 inconsistent dimensions, -3 malformed CSR
  * (row pointers not monotone / out of [0,nnz], column index outside [0,aCols)),
  * -6 execution error. */
@@ -240,6 +255,11 @@ typedef enum { GN_ROUND_NEAREST_EVEN = 0, GN_ROUND_TOWARD_ZERO = 1 } gn_round;
 enum { GN_ACT_NONE = -1, GN_ACT_RELU = 0, GN_ACT_SIGMOID = 1, GN_ACT_TANH = 2, GN_ACT_LEAKY_RELU = 4,
        GN_ACT_ELU = 5, GN_ACT_SWISH = 6, GN_ACT_GELU = 7 };
 
+/* Drops the index arrays the Part-1 sparse entries keep with values buffer valuesPtr
+ * (see perform_sparse_dense_matmul): the next call uploads and validates them again.
+ * For callers that change a sparse tensor's index arrays in place. Always 0. */
+int gn_csr_indices_changed(GPUPtr valuesPtr);
+
 /* Library version string (static storage). */
 const char *gn_version(void);
 /* Initialises the device context once (thread-safe). 0 on success. */
@@ -252,9 +272,15 @@ long gn_buffer_bytes(GPUPtr buf);
 /* Live/peak bytes and live allocations of the library's device pool
  * (the GlobalMemoryPool statistics of tensor/tensor.go:65-77). */
 void gn_memory_stats(long *current_bytes, long *peak_bytes, long *num_allocations);
-/* Device memory from the library pool (async-safe caching allocator). */
+/* Device memory from the library pool (caching allocator). Release is stream-ordered:
+ * gn_free(ptr) hands the block to a new owner only after the work enqueued on the library
+ * stream before the call has finished; gn_free_async(ptr, stream) does the same for
+ * `stream` (NULL = the library stream). Neither waits. Work on any other stream that still
+ * uses the block must be complete, or ordered before the block's next user, when it is
+ * freed (the rule of every stream-ordered allocator). release_gpu_buffer follows gn_free. */
 int gn_malloc(void **ptr, size_t bytes, CError *err);
 int gn_free(void *ptr);
+int gn_free_async(void *ptr, void *stream);
 int gn_synchronize(void *stream, CError *err);
 
 /* General GEMM on device pointers:

@@ -278,6 +278,42 @@ void orc_spmm_csr_f32(long M, long N, const int32_t *rowptr, const int32_t *col,
   }
 }
 
+/* The same loops with the rows split over `threads` OpenMP threads: each row is computed
+ * exactly as in orc_spmm_csr_f32 / orc_spmv_csr_f32, so the results are bit-identical.
+ * The CPU baseline's parallel line (the reference runs them on one thread). */
+void orc_spmm_csr_f32_par(long M, long N, const int32_t *rowptr, const int32_t *col, const float *val,
+                          const float *D, long ldd, float *C, long ldc, int use_fma, int threads) {
+  if (threads <= 0) threads = 1;
+#pragma omp parallel for schedule(dynamic, 64) num_threads(threads)
+  for (long i = 0; i < M; ++i) {
+    float *crow = C + i * ldc;
+    for (long j = 0; j < N; ++j) crow[j] = 0.0f;
+    for (long k = rowptr[i]; k < rowptr[i + 1]; ++k) {
+      const float a = val[k];
+      const float *drow = D + (long)col[k] * ldd;
+      if (use_fma) {
+        for (long j = 0; j < N; ++j) crow[j] = fmaf(a, drow[j], crow[j]);
+      } else {
+        for (long j = 0; j < N; ++j) { float p = a * drow[j]; crow[j] = crow[j] + p; }
+      }
+    }
+  }
+}
+
+void orc_spmv_csr_f32_par(long M, const int32_t *rowptr, const int32_t *col, const float *val, const float *x,
+                          float *y, int use_fma, int threads) {
+  if (threads <= 0) threads = 1;
+#pragma omp parallel for schedule(dynamic, 256) num_threads(threads)
+  for (long i = 0; i < M; ++i) {
+    float sum = 0.0f;
+    for (long k = rowptr[i]; k < rowptr[i + 1]; ++k) {
+      if (use_fma) sum = fmaf(val[k], x[col[k]], sum);
+      else { float p = val[k] * x[col[k]]; sum = sum + p; }
+    }
+    y[i] = sum;
+  }
+}
+
 void orc_spmm_csr_f64(long M, long N, const int32_t *rowptr, const int32_t *col, const float *val,
                       const float *D, long ldd, double *C, long ldc, int threads) {
   if (threads <= 0) threads = 1;

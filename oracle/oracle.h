@@ -81,6 +81,11 @@ void orc_csr_to_dense(long rows, long cols, const int32_t *rowptr, const int32_t
 void orc_spmm_csr_f32(long M, long N, const int32_t *rowptr, const int32_t *col,
                       const float *val, const float *D, long ldd, float *C, long ldc, int fma);
 /* Same loop in float64 (the accuracy reference). */
+/* Row-parallel forms of the two loops above (bit-identical results; CPU baseline only). */
+void orc_spmm_csr_f32_par(long M, long N, const int32_t *rowptr, const int32_t *col, const float *val,
+                          const float *D, long ldd, float *C, long ldc, int use_fma, int threads);
+void orc_spmv_csr_f32_par(long M, const int32_t *rowptr, const int32_t *col, const float *val, const float *x,
+                          float *y, int use_fma, int threads);
 void orc_spmm_csr_f64(long M, long N, const int32_t *rowptr, const int32_t *col,
                       const float *val, const float *D, long ldd, double *C, long ldc, int threads);
 /* Restates perform_sparse_matvec, metal_bridge_sparse.m:325-339: y[i] = sequential

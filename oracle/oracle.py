@@ -55,6 +55,9 @@ def lib():
         "orc_spmm_csr_f64": (None, [_L, _L, _i32p, _i32p, _f32p, _f32p, _L, _f64p, _L, ctypes.c_int]),
         "orc_spmv_csr_f32": (None, [_L, _i32p, _i32p, _f32p, _f32p, _f32p, ctypes.c_int]),
         "orc_spmv_csr_f64": (None, [_L, _i32p, _i32p, _f32p, _f32p, _f64p]),
+        "orc_spmm_csr_f32_par": (None, [_L, _L, _i32p, _i32p, _f32p, _f32p, _L, _f32p, _L, ctypes.c_int,
+                                        ctypes.c_int]),
+        "orc_spmv_csr_f32_par": (None, [_L, _i32p, _i32p, _f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int]),
         "orc_act_f64": (ctypes.c_double, [ctypes.c_int, ctypes.c_double, ctypes.c_double]),
         "orc_softmax_rows_f64": (None, [_L, _L, _f32p, _f64p]),
         "orc_act_f32": (ctypes.c_float, [ctypes.c_int, ctypes.c_float, ctypes.c_float]),
@@ -179,6 +182,26 @@ def spmm_f32(rowptr, col, val, D, use_fma=True):
     lib().orc_spmm_csr_f32(M, N, np.ascontiguousarray(rowptr, np.int32), pad(col, np.int32), pad(val, np.float32),
                            D.reshape(-1), N, C.reshape(-1), N, int(use_fma))
     return C
+
+
+def spmm_f32_par(rowptr, col, val, D, nthreads, use_fma=True):
+    """spmm_f32 with the rows split over nthreads OpenMP threads (bit-identical)."""
+    M = rowptr.size - 1
+    D = np.ascontiguousarray(D, dtype=np.float32)
+    N = D.shape[1]
+    C = np.empty((M, N), dtype=np.float32)
+    lib().orc_spmm_csr_f32_par(M, N, np.ascontiguousarray(rowptr, np.int32), _pad(col, np.int32),
+                               _pad(val, np.float32), D.reshape(-1), N, C.reshape(-1), N, int(use_fma), nthreads)
+    return C
+
+
+def spmv_f32_par(rowptr, col, val, x, nthreads, use_fma=True):
+    """spmv_f32 with the rows split over nthreads OpenMP threads (bit-identical)."""
+    M = rowptr.size - 1
+    y = np.empty(max(M, 1), dtype=np.float32)
+    lib().orc_spmv_csr_f32_par(M, np.ascontiguousarray(rowptr, np.int32), _pad(col, np.int32), _pad(val, np.float32),
+                               _pad(x, np.float32), y, int(use_fma), nthreads)
+    return y[:M]
 
 
 def spmm_f64(rowptr, col, val, D, nthreads=None):

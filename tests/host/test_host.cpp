@@ -8,6 +8,7 @@
 #include <any>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <functional>
 #include <string>
@@ -716,6 +717,103 @@ void TestGPUDenseAndGPUMatMul() {
   CHECK(back->At(0, 0) == 42.0);
 }
 
+// T() views: Mul / GPUMatMul of transposed views run one GEMM with in-place transposes
+// (gonum's mat.Transpose semantics; the reference materialises, gonum-compat.go:61-68).
+void TestGPUDenseTransposeViews() {
+  // Ragged shapes in all four layouts against float64 of the stored operands.
+  {
+    const int M = 37, K = 53, N = 29;
+    for (int ta = 0; ta < 2; ++ta)
+      for (int tb = 0; tb < 2; ++tb) {
+        const int ar = ta ? K : M, ac = ta ? M : K, br = tb ? N : K, bc = tb ? K : N;
+        std::vector<float> af = uniform((size_t)ar * ac, 300 + 2 * ta + tb), bf = uniform((size_t)br * bc, 310 + 2 * ta + tb);
+        auto ga = matrix::NewGPUDense(ar, ac, std::vector<double>(af.begin(), af.end()));
+        auto gb = matrix::NewGPUDense(br, bc, std::vector<double>(bf.begin(), bf.end()));
+        std::shared_ptr<mat::Matrix> opA = ta ? ga->T() : std::shared_ptr<mat::Matrix>(ga);
+        std::shared_ptr<mat::Matrix> opB = tb ? gb->T() : std::shared_ptr<mat::Matrix>(gb);
+        int r, c;
+        opA->Dims(r, c);
+        CHECK(r == M && c == K);
+        std::vector<double> ref((size_t)M * N);
+        orc_gemm_f64(ta, tb, M, N, K, 1.0, af.data(), ac, bf.data(), bc, 0.0, ref.data(), N, 8);
+        auto g = matrix::NewGPUDense(M, N, std::vector<double>((size_t)M * N, 0.0));
+        g->Mul(*opA, *opB);
+        auto got = g->ToGonum();
+        std::vector<float> gf(got->RawData().begin(), got->RawData().end());
+        CHECK(rel(gf, ref) <= 1e-5);
+        auto viaGPUMatMul = matrix::GPUMatMul(*opA, *opB);
+        std::vector<float> mf(viaGPUMatMul->RawData().begin(), viaGPUMatMul->RawData().end());
+        CHECK(mf == gf);  // same kernel, same operands
+        // view semantics: At reads the parent transposed; T() of a view is the parent again
+        if (ta) {
+          CHECK(opA->At(3, 5) == (double)af[(size_t)5 * ac + 3]);
+          auto back = opA->T();
+          CHECK(back->At(5, 3) == (double)af[(size_t)5 * ac + 3]);
+        }
+      }
+  }
+  // C2 size: 4096^3 with the three transposed layouts, sampled rows against float64 and
+  // whole-output column sums against (1^T op(A)) op(B) in float64.
+  const int n = 4096;
+  std::vector<float> af = uniform((size_t)n * n, 320), bf = uniform((size_t)n * n, 321);
+  auto ga = matrix::NewGPUDense(n, n, std::vector<double>(af.begin(), af.end()));
+  auto gb = matrix::NewGPUDense(n, n, std::vector<double>(bf.begin(), bf.end()));
+  const long rows[6] = {0, 1, 777, 2048, 4000, 4095};
+  for (int v = 1; v < 4; ++v) {
+    const int ta = v >> 1, tb = v & 1;
+    auto g = matrix::NewGPUDense(n, n, std::vector<double>((size_t)n * n, 0.0));
+    g->Mul(ta ? *ga->T() : *ga, tb ? *gb->T() : *gb);
+    auto C = g->GetTensor();
+    CHECK_NOERR(C->RetrieveCPU());
+    std::vector<double> ref((size_t)6 * n);
+    orc_gemm_f64_rows(ta, tb, n, n, n, af.data(), n, bf.data(), n, rows, 6, ref.data(), n, 8);
+    std::vector<float> got((size_t)6 * n);
+    for (int i = 0; i < 6; ++i)
+      std::copy(C->Data.begin() + rows[i] * n, C->Data.begin() + (rows[i] + 1) * n, got.begin() + (size_t)i * n);
+    CHECK(rel(got, ref) <= 1e-5);
+    // column sums: s_j = sum_k (sum_i opA[i,k]) opB[k,j]
+    std::vector<double> colA(n, 0.0), colref(n, 0.0), colgot(n, 0.0);
+    for (int i = 0; i < n; ++i)
+      for (int k = 0; k < n; ++k) colA[k] += ta ? af[(size_t)k * n + i] : af[(size_t)i * n + k];
+    for (int k = 0; k < n; ++k)
+      for (int j = 0; j < n; ++j) colref[j] += colA[k] * (tb ? bf[(size_t)j * n + k] : bf[(size_t)k * n + j]);
+    for (int i = 0; i < n; ++i)
+      for (int j = 0; j < n; ++j) colgot[j] += C->Data[(size_t)i * n + j];
+    double num = 0, den = 0;
+    for (int j = 0; j < n; ++j) num += (colgot[j] - colref[j]) * (colgot[j] - colref[j]), den += colref[j] * colref[j];
+    CHECK(std::sqrt(num / den) <= 1e-5);
+  }
+}
+
+// Config C1 (256^3, U[-1,1]) through the gonum-compatible facade on the committed fixture
+// (tests/golden/gemm_256.npz, float64 product), unpacked by the Python runner into the
+// raw file named by GONNGPU_C1_FIXTURE: A, B (256^2 fp32 each), C (256^2 fp64).
+void TestGPUMatMulC1Golden() {
+  const char *path = std::getenv("GONNGPU_C1_FIXTURE");
+  CHECK(path != nullptr);
+  if (!path) return;
+  const int n = 256;
+  std::vector<float> af((size_t)n * n), bf((size_t)n * n);
+  std::vector<double> c64((size_t)n * n);
+  FILE *f = std::fopen(path, "rb");
+  CHECK(f != nullptr);
+  if (!f) return;
+  const bool ok = std::fread(af.data(), 4, af.size(), f) == af.size() && std::fread(bf.data(), 4, bf.size(), f) == bf.size() &&
+                  std::fread(c64.data(), 8, c64.size(), f) == c64.size();
+  std::fclose(f);
+  CHECK(ok);
+  auto da = mat::NewDense(n, n, std::vector<double>(af.begin(), af.end()));
+  auto db = mat::NewDense(n, n, std::vector<double>(bf.begin(), bf.end()));
+  auto C = matrix::GPUMatMul(*da, *db);
+  std::vector<float> cf(C->RawData().begin(), C->RawData().end());
+  CHECK(rel(cf, c64) <= 1e-5);
+  auto g = matrix::NewGPUDense(n, n, std::vector<double>((size_t)n * n, 0.0));
+  g->Mul(*da, *db);
+  auto back = g->ToGonum();
+  std::vector<float> gf(back->RawData().begin(), back->RawData().end());
+  CHECK(gf == cf);
+}
+
 void TestGPUSparseMatMulAndMatVec() {
   auto gs = matrix::NewGPUSparse(4, 3, {0, 1, 3, 3}, {2, 0, 1, 1}, {1.f, 2.f, 3.f, 4.f});  // (3,1) duplicated
   auto d = mat::NewDense(3, 2, {1, 2, 3, 4, 5, 6});
@@ -852,12 +950,21 @@ int main(int argc, char **argv) {
       {"TestFloat16Chaining", TestFloat16Chaining, true},
       {"TestLinearLayer", TestLinearLayer, true},
       {"TestGPUDenseAndGPUMatMul", TestGPUDenseAndGPUMatMul, true},
+      {"TestGPUDenseTransposeViews", TestGPUDenseTransposeViews, true},
+      {"TestGPUMatMulC1Golden", TestGPUMatMulC1Golden, true},
       {"TestGPUSparseMatMulAndMatVec", TestGPUSparseMatMulAndMatVec, true},
       {"TestSparseOps", TestSparseOps, true},
   };
+  // Optional test names after the mode select a subset (e.g. for a profiler run).
+  auto selected = [&](const char *name) {
+    if (argc <= 2) return true;
+    for (int i = 2; i < argc; ++i)
+      if (std::strcmp(argv[i], name) == 0) return true;
+    return false;
+  };
   int run = 0;
   for (const Case &c : cases) {
-    if (c.device && !gpu) continue;
+    if ((c.device && !gpu) || !selected(c.name)) continue;
     g_current = c.name;
     const int before = g_failures;
     std::printf("=== RUN %s\n", c.name);

@@ -98,3 +98,52 @@ def test_injected_allocation_failure_is_clean(dev):
     env = dict(os.environ, GONNGPU_FAIL_ALLOC_AFTER="1")
     out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
     assert out.returncode == 0 and "OK" in out.stdout, out.stderr[-2000:]
+
+
+def test_release_is_stream_ordered(dev):
+    """gn_free / release_gpu_buffer do not wait: a block freed while kernels on the library
+    stream still read it goes to a new owner only after they have finished. Here A is freed
+    right behind eight queued 4096^3 GEMMs that read it, a block of the same size is taken
+    at once and overwritten from another stream; the GEMMs' output must still equal the
+    product computed before."""
+    import ctypes
+
+    import torch
+
+    n = 4096
+    nbytes = n * n * 4
+
+    def malloc():
+        p = ctypes.c_void_p()
+        G.call("gn_malloc", ctypes.byref(p), nbytes)
+        return p.value
+
+    pa = malloc()
+    G.call("gn_fill_normal_f32", pa, n * n, 42, 901, 0.0, 1.0, None)
+    B = torch.empty((n, n), dtype=torch.float32, device=dev)
+    G.fill_normal(B, 42, 902)
+    torch.cuda.synchronize()
+    ref = torch.empty((n, n), dtype=torch.float32, device=dev)
+    out = torch.empty((n, n), dtype=torch.float32, device=dev)
+
+    def gemm(dst):  # on the library stream (NULL)
+        G.call("gn_gemm", G.GN_F32, 0, 0, n, n, n, 1.0, pa, n, 0, B.data_ptr(), n, 0, 0.0, dst.data_ptr(), n, 0, 1,
+               None, G.ACT_NONE, 0.0, None)
+
+    gemm(ref)
+    G.call("gn_synchronize", None)
+    for _ in range(8):
+        gemm(out)
+    G.call("gn_free", pa)  # A is still being read by the queued GEMMs
+    pz = malloc()
+    G.call("gn_fill_uniform_f32", pz, n * n, 7, 7, 100.0, 200.0, torch.cuda.current_stream().cuda_stream)
+    G.call("gn_synchronize", None)
+    torch.cuda.synchronize()
+    assert pz != pa, "a block still read by queued kernels was handed out again"
+    assert torch.equal(out, ref)
+    # once the work is done, the freed blocks are reused (no growth of the pool)
+    G.call("gn_free", pz)
+    G.call("gn_synchronize", None)
+    p2 = malloc()
+    assert p2 in (pa, pz)
+    G.call("gn_free_async", p2, torch.cuda.current_stream().cuda_stream)

@@ -49,6 +49,33 @@ def _gemm_dev(dev, A, B, tA, tB, dtype, **kw):
     return cd.cpu().numpy()
 
 
+def _nan_like(dev, M, N):
+    """An output buffer filled with NaN, so a tile the kernel never writes fails the checks."""
+    import torch
+
+    return torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+
+
+def _sum_invariants(A, B, C, tA=False, tB=False):
+    """Whole-output checks in float64 on the device: row sums C.1 = op(A)(op(B).1) and column
+    sums 1^T C = (1^T op(A)) op(B), each within 1e-5 relative (2-norm). A, B are the stored
+    device operands (already rounded to their input precision), C the fp32 result. Every
+    output element enters one row sum and one column sum, so a tile that is wrong, missing
+    or written to the wrong place fails one of them (NaN fails both)."""
+    import torch
+
+    a = A.double()
+    b = B.double()
+    opA = a.t() if tA else a
+    opB = b.t() if tB else b
+    c = C.double()
+    row_ref = opA @ opB.sum(dim=1)
+    col_ref = opA.sum(dim=0) @ opB
+    row_err = (torch.linalg.vector_norm(c.sum(dim=1) - row_ref) / torch.linalg.vector_norm(row_ref)).item()
+    col_err = (torch.linalg.vector_norm(c.sum(dim=0) - col_ref) / torch.linalg.vector_norm(col_ref)).item()
+    return row_err, col_err
+
+
 # ------------------------------------------------------------------ fp32
 @pytest.mark.parametrize("tA,tB", VARIANTS)
 def test_f32_golden_small_all_transposes(dev, tA, tB):
@@ -95,8 +122,17 @@ def test_f32_c2_4096_all_transposes(dev, tA, tB):
     n = 4096
     A = O.normal((n, n), 42, 11)
     B = O.normal((n, n), 42, 12)
+    import torch
+
     _say("C2", tA, tB)
-    C = _gemm_dev(dev, A, B, tA, tB, G.GN_F32)
+    ad = torch.from_numpy(_stored(A, tA)).to(dev)
+    bd = torch.from_numpy(_stored(B, tB)).to(dev)
+    cd = _nan_like(dev, n, n)
+    G.gemm(ad, bd, cd, transA=tA, transB=tB)
+    row_err, col_err = _sum_invariants(ad, bd, cd, tA, tB)
+    _say("C2 row/col-sum relative errors", tA, tB, row_err, col_err)
+    assert row_err <= 1e-5 and col_err <= 1e-5
+    C = cd.cpu().numpy()
     rows = np.random.default_rng(7).choice(n, 48, replace=False)
     ref = O.gemm_f64_rows(A, B, rows)
     err = O.rel_frob(C[rows], ref)
@@ -249,9 +285,12 @@ def test_f16_c3_8192(dev):
     b16 = torch.empty((n, n), dtype=torch.float16, device=dev)
     G.cast_f32_f16(ad, a16)
     G.cast_f32_f16(bd, b16)
-    C = torch.empty((n, n), dtype=torch.float32, device=dev)
+    C = _nan_like(dev, n, n)
     _say("C3 gemm")
     G.gemm(a16, b16, C)
+    row_err, col_err = _sum_invariants(a16, b16, C)
+    _say("C3 row/col-sum relative errors", row_err, col_err)
+    assert row_err <= 1e-5 and col_err <= 1e-5
     rows = np.random.default_rng(23).choice(n, 16, replace=False)
     A = ad.cpu().numpy()
     B = bd.cpu().numpy()
@@ -266,12 +305,29 @@ def test_f16_c3_8192(dev):
 @pytest.mark.parametrize("act", [G.ACT_RELU, G.ACT_GELU])
 def test_f16_c4_fused_linear(dev, act):
     """Config C4: Y = act(X W^T + b), X 512x4096, W 11008x4096 (fp16), b fp32."""
+    import torch
+
     X = O.normal((512, 4096), 42, 31)
     W = O.normal((11008, 4096), 42, 32, 0.0, 0.02)
     b = O.normal((11008,), 42, 33, 0.0, 0.01)
-    # _gemm_dev takes the logical K x N operand; W^T stored transposed is W itself.
-    Y = _gemm_dev(dev, X, W.T, False, True, G.GN_F16, bias=b, act=act)
+    x16 = torch.empty((512, 4096), dtype=torch.float16, device=dev)
+    w16 = torch.empty((11008, 4096), dtype=torch.float16, device=dev)
+    G.cast_f32_f16(torch.from_numpy(X).to(dev), x16)
+    G.cast_f32_f16(torch.from_numpy(W).to(dev), w16)
+    bd = torch.from_numpy(b).to(dev)
+    Yd = _nan_like(dev, 512, 11008)
+    G.gemm(x16, w16, Yd, transB=True, bias=bd, act=act)
+    # Whole output: the pre-activation's row / column sums (the epilogue's input) cannot be
+    # read back, so every element is compared with act(X16 W16^T + b) from a float64
+    # product of the same fp16 operands on the device (relative Frobenius error).
+    pre64 = x16.double() @ w16.double().t().contiguous() + bd.double()
+    ref64 = torch.relu(pre64) if act == G.ACT_RELU else torch.from_numpy(O.act_f64(act, pre64.cpu().numpy())).to(dev)
+    full_err = (torch.linalg.matrix_norm(Yd.double() - ref64) / torch.linalg.matrix_norm(ref64)).item()
+    _say("C4", act, "whole-output relFrob vs float64 of the fp16 operands", full_err)
+    assert full_err <= 1e-5
+    Y = Yd.cpu().numpy()
     assert Y.shape == (512, 11008)
+    assert np.isfinite(Y).all()
     rows = np.arange(0, 512, 37)
     pre = O.gemm_f64_rows(X, W, rows, transB=True) + b
     ref = O.act_f64(act, pre)
@@ -301,6 +357,33 @@ def test_fused_linear_reference_abi(dev):
     rc, msg = G.call_rc("perform_fused_linear_activation", bx.handle, 40, 96, bw.handle, 70, None, 3, 0.0, by.handle,
                         None)
     assert rc == -1
+
+
+def test_fused_linear_nil_activation_call_sequence(dev):
+    """The reference's FusedLinearActivation.Forward with config.Activation == nil sends
+    C.int(OpReLU) and alpha 0 (fused-operations.go:433-434). OpReLU is 6 in the OpType enum
+    (gradient.go:27-39), and code 6 of the ActivationType enum this entry reads is Swish
+    (activation.go:20-29). The unchanged call therefore runs Swish; the required one-line Go
+    edit (ActivationType ReLU, 0) runs ReLU, the comment's "Default to ReLU"."""
+    rng = np.random.default_rng(31)
+    X = rng.standard_normal((24, 64)).astype(np.float32)
+    W = rng.standard_normal((64, 40)).astype(np.float32)
+    b = rng.standard_normal(40).astype(np.float32)
+    bx, bw, bb, by = G.Buffer.from_array(X), G.Buffer.from_array(W), G.Buffer.from_array(b), G.Buffer(24 * 40 * 4)
+    op_relu = 6  # OpReLU: OpAdd, OpSub, OpMul, OpDiv, OpMatMul, OpTranspose, OpReLU
+    G.call("perform_fused_linear_activation", bx.handle, 24, 64, bw.handle, 40, bb.handle, op_relu, 0.0, by.handle,
+           None)
+    Y6 = by.to_array((24, 40))
+    swish = O.linear_f64(X, W, b, G.ACT_SWISH, 0)
+    assert O.rel_frob(Y6, swish) <= 1e-5
+    assert O.rel_frob(Y6, O.linear_f64(X, W, b, G.ACT_RELU, 0)) > 1e-2  # not ReLU: the Go edit is needed
+    G.call("perform_fused_linear_activation", bx.handle, 24, 64, bw.handle, 40, bb.handle, G.ACT_RELU, 0.0, by.handle,
+           None)
+    Y0 = by.to_array((24, 40))
+    assert O.rel_frob(Y0, O.linear_f64(X, W, b, G.ACT_RELU, 0)) <= 1e-5
+    assert (Y0 >= 0).all()
+    for buf in (bx, bw, bb, by):
+        buf.release()
 
 
 # ------------------------------------------------------------------ fp16 ring kernel (large aligned shapes)

@@ -491,3 +491,16 @@ def test_dense_to_coo_threshold_order_nan():
     np.testing.assert_array_equal(ci, cc)
     np.testing.assert_array_equal(vv, D[rr, cc])
     assert O.dense_to_coo(D, 0.5, max_nnz=3)[0] == -2
+
+
+def test_parallel_sparse_loops_equal_the_serial_ones():
+    """The CPU baseline's OpenMP row split computes each row exactly as the reference's
+    single-threaded loop does (metal_bridge_sparse.m:117-133, :325-339)."""
+    rp, col, val = O.random_csr(3000, 2000, 9.0, seed=5, distinct=False)
+    D = O.normal((2000, 40), 3, 1)
+    x = O.normal((2000,), 3, 2)
+    for fma in (True, False):
+        np.testing.assert_array_equal(O.spmm_f32_par(rp, col, val, D, 8, use_fma=fma),
+                                      O.spmm_f32(rp, col, val, D, use_fma=fma))
+        np.testing.assert_array_equal(O.spmv_f32_par(rp, col, val, x, 8, use_fma=fma),
+                                      O.spmv_f32(rp, col, val, x, use_fma=fma))

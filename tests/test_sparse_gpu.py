@@ -241,3 +241,59 @@ def test_spmv_long_rows_skew_unsorted_and_errors(dev, K, mean):
     rc, msg = G.call_rc("perform_sparse_matvec", bv.handle, rp.ctypes.data, rp.size, bad.ctypes.data, bad.size, M, K,
                         val.size, bx.handle, K, by.handle, M, None)
     assert rc == -3 and "column" in msg
+
+
+def test_spmm_index_cache_reuse_and_invalidation(dev):
+    """The Part-1 SpMM keeps the device copy of the index arrays with the values buffer:
+    the second call allocates and uploads nothing; new host arrays, changed row pointers
+    and gn_csr_indices_changed after an in-place column change are all seen; a malformed
+    structure is refused and not kept; release_gpu_buffer of the values drops the copy."""
+    rows, cols, N = 500, 700, 64
+    rp, col, val = O.random_csr(rows, cols, 12.0, seed=77)
+    D = O.normal((cols, N), 7, 1)
+    bv, bd, bc = G.Buffer.from_array(val), G.Buffer.from_array(D), G.Buffer(rows * N * 4)
+
+    def run(rp_, col_, expect_rc=0):
+        rc, msg = G.call_rc("perform_sparse_dense_matmul", bv.handle, rp_.ctypes.data, rp_.size, col_.ctypes.data,
+                            col_.size, rows, cols, val.size, bd.handle, cols, N, bc.handle, rows, N, None)
+        assert rc == expect_rc, (rc, msg)
+        return bc.to_array((rows, N)) if rc == 0 else None
+
+    n0 = G.memory_stats()[2]
+    C1 = run(rp, col)
+    n1 = G.memory_stats()[2]
+    assert n1 == n0 + 2  # the cached row pointers and column indices
+    C2 = run(rp, col)
+    assert G.memory_stats()[2] == n1  # nothing uploaded or allocated
+    np.testing.assert_array_equal(C1, O.spmm_f32(rp, col, val, D, use_fma=True))
+    np.testing.assert_array_equal(C2, C1)
+    # columns changed in place: announced with gn_csr_indices_changed
+    col[:] = (col + 13) % cols
+    assert G.load().gn_csr_indices_changed(bv.handle) == 0
+    np.testing.assert_array_equal(run(rp, col), O.spmm_f32(rp, col, val, D, use_fma=True))
+    # new host arrays are a new structure: seen without any call
+    col_new = ((col + 5) % cols).astype(np.int32)
+    np.testing.assert_array_equal(run(rp, col_new), O.spmm_f32(rp, col_new, val, D, use_fma=True))
+    # row pointers changed in place are compared on every call
+    k = int(np.argmax(np.diff(rp) > 0))  # a row with at least one entry
+    rp[k + 1] -= 1  # its last entry moves to the next row
+    np.testing.assert_array_equal(run(rp, col_new), O.spmm_f32(rp, col_new, val, D, use_fma=True))
+    assert G.memory_stats()[2] == n1  # each replaced copy was released
+    # a malformed structure is refused and not kept; the corrected one then runs
+    col_new[3] = cols + 4
+    assert G.load().gn_csr_indices_changed(bv.handle) == 0
+    run(rp, col_new, expect_rc=-3)
+    assert G.memory_stats()[2] == n0
+    col_new[3] = 0
+    np.testing.assert_array_equal(run(rp, col_new), O.spmm_f32(rp, col_new, val, D, use_fma=True))
+    # SpMV with the same values buffer shares the cached structure
+    x = O.normal((cols,), 8, 1)
+    bx, by = G.Buffer.from_array(x), G.Buffer(rows * 4)
+    G.call("perform_sparse_matvec", bv.handle, rp.ctypes.data, rp.size, col_new.ctypes.data, col_new.size, rows, cols,
+           val.size, bx.handle, cols, by.handle, rows, None)
+    assert O.rel_frob(by.to_array((rows,)), O.spmv_f64(rp, col_new, val, x)) <= 1e-5
+    nmid = G.memory_stats()[2]
+    bv.release()
+    assert G.memory_stats()[2] == nmid - 3  # the values and their cached index arrays
+    for b in (bd, bc, bx, by):
+        b.release()
