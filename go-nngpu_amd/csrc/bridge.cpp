@@ -777,6 +777,14 @@ int gn_activation_backward(const float *grad_out, const float *pre, long rows, l
                                  gn::resolve_stream(stream), err);
 }
 
+int gn_activation_backward_noalloc(const float *grad_out, const float *pre, long rows, long cols, int act,
+                                   float alpha, float scale, float *grad_in, float *grad_bias, void *stream,
+                                   CError *err) {
+  if (!gn::context(err)) return -1;
+  return gn::launch_act_backward_noalloc(grad_out, pre, rows, cols, act, alpha, scale, grad_in, grad_bias,
+                                         gn::resolve_stream(stream), err);
+}
+
 int gn_activation_forward(const float *in, float *out, long n, int act, float alpha, void *stream, CError *err) {
   if (!gn::context(err)) return -1;
   return gn::launch_act_forward(in, out, n, act, alpha, gn::resolve_stream(stream), err);

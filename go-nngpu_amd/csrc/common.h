@@ -103,6 +103,12 @@ int launch_act_forward(const float *in, float *out, long n, int act, float alpha
 int launch_softmax_rows(const float *in, float *out, long rows, long cols, hipStream_t s, CError *err);
 int launch_act_backward(const float *grad_out, const float *pre, long rows, long cols, int act, float alpha,
                         float scale, float *grad_in, float *grad_bias, hipStream_t s, CError *err);
+// The same computation with the partial column sums in the file-scope `scratch` array of
+// elementwise.hip (no allocation on any call); rejects shapes whose partials exceed it.
+int launch_act_backward_noalloc(const float *grad_out, const float *pre, long rows, long cols, int act, float alpha,
+                                float scale, float *grad_in, float *grad_bias, hipStream_t s, CError *err);
+// Looks up the address of that array on the current device (once per device); 0 on success.
+int noalloc_scratch_setup(CError *err);
 bool act_grad_supported(int act);
 int launch_spmm(long M, long N, long K, long nnz, const int32_t *rowptr, const int32_t *col, const float *val,
                 const float *D, long ldd, float *C, long ldc, int *flags, hipStream_t s, CError *err);

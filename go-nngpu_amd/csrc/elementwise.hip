@@ -250,39 +250,134 @@ __global__ void __launch_bounds__(256) colsum_finish_kernel(const float *__restr
 
 bool act_grad_supported(int act) { return act == -1 || act == 0 || act == 1 || act == 2 || (act >= 4 && act <= 7); }
 
-int launch_act_backward(const float *grad_out, const float *pre, long rows, long cols, int act, float alpha,
-                        float scale, float *grad_in, float *grad_bias, hipStream_t s, CError *err) {
+namespace {
+
+// Work split of the activation backward: (column block of 256, row chunk) workgroups, enough
+// of them to fill the GPU with at least 8 rows each. The column sums are added over the
+// chunks in a fixed order, so a given (rows, cols) always sums in the same order.
+struct ActBackwardPlan {
+  long colblocks, chunks, R;
+};
+
+int plan_act_backward(long rows, long cols, ActBackwardPlan &pl, CError *err) {
+  pl.colblocks = (cols + 255) / 256;
+  if (pl.colblocks > 0x7FFFFFFFL) return set_error(err, -1, "activation backward: too many columns");
+  long chunks = (4096 + pl.colblocks - 1) / pl.colblocks;
+  chunks = std::max(1L, std::min(chunks, (rows + 7) / 8));
+  pl.R = (rows + chunks - 1) / chunks;
+  pl.chunks = (rows + pl.R - 1) / pl.R;
+  return 0;
+}
+
+// Common argument checks; 1 when there is nothing to compute beyond the empty column sum.
+int check_act_backward(const float *grad_out, const float *pre, long rows, long cols, int act, float *grad_in,
+                       CError *err) {
   if (rows < 0 || cols < 0) return set_error(err, -1, "activation backward: negative size");
   if (!act_grad_supported(act)) return set_error(err, -1, "activation backward: unsupported activation %d", act);
-  if (cols == 0) return 0;
-  if (rows == 0) {  // an empty column sum is zero (a kernel, not a memset, so it can be captured)
-    if (!grad_bias) return 0;
-    hipLaunchKernelGGL(colsum_finish_kernel, dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, s, nullptr, 0L, cols,
-                       grad_bias);
-    hipError_t e = hipGetLastError();
-    return e == hipSuccess ? 0 : hip_error(err, -6, "activation backward launch", e);
-  }
+  if (cols == 0 || rows == 0) return 1;
   if (!grad_out || !pre || !grad_in) return set_error(err, -1, "activation backward: NULL pointer");
-  const long colblocks = (cols + 255) / 256;
-  if (colblocks > 0x7FFFFFFFL) return set_error(err, -1, "activation backward: too many columns");
-  // Enough (column block, row chunk) workgroups to fill the GPU, at least 8 rows each.
-  long chunks = (4096 + colblocks - 1) / colblocks;
-  chunks = std::max(1L, std::min(chunks, (rows + 7) / 8));
-  const long R = (rows + chunks - 1) / chunks;
-  chunks = (rows + R - 1) / R;
-  float *partial = nullptr;
-  std::unique_lock<std::mutex> lk;
-  if (grad_bias) {
-    partial = static_cast<float *>(stream_scratch(s, (size_t)chunks * cols * sizeof(float), lk, err));
-    if (!partial) return -3;
-  }
-  hipLaunchKernelGGL(act_backward_kernel, dim3((unsigned)colblocks, (unsigned)chunks), dim3(256), 0, s, grad_out, pre,
-                     rows, cols, act, alpha, scale, grad_in, partial, R);
+  return 0;
+}
+
+// An empty column sum is zero: a kernel, not a memset, so it can be captured.
+int zero_bias(long cols, float *grad_bias, hipStream_t s, CError *err) {
+  if (!grad_bias || cols == 0) return 0;
+  hipLaunchKernelGGL(colsum_finish_kernel, dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, s, nullptr, 0L, cols,
+                     grad_bias);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : hip_error(err, -6, "activation backward launch", e);
+}
+
+// The two kernels of the backward: element-wise gradient (plus per-chunk column sums into
+// `partial`, chunks x cols floats, when grad_bias is wanted), then the fixed-order sum.
+int enqueue_act_backward(const ActBackwardPlan &pl, const float *grad_out, const float *pre, long rows, long cols,
+                         int act, float alpha, float scale, float *grad_in, float *grad_bias, float *partial,
+                         hipStream_t s, CError *err) {
+  hipLaunchKernelGGL(act_backward_kernel, dim3((unsigned)pl.colblocks, (unsigned)pl.chunks), dim3(256), 0, s, grad_out,
+                     pre, rows, cols, act, alpha, scale, grad_in, grad_bias ? partial : nullptr, pl.R);
   if (grad_bias)
-    hipLaunchKernelGGL(colsum_finish_kernel, dim3((unsigned)colblocks), dim3(256), 0, s, partial, chunks, cols,
+    hipLaunchKernelGGL(colsum_finish_kernel, dim3((unsigned)pl.colblocks), dim3(256), 0, s, partial, pl.chunks, cols,
                        grad_bias);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? 0 : hip_error(err, -6, "activation backward launch", e);
+}
+
+// ------------------------------------------------------------------ allocation-free variant
+// Scratch of gn_activation_backward_noalloc: the per-chunk column sums live in this
+// file-scope device array instead of library-allocated memory. Each device the library runs
+// on holds its own copy (kNoAllocScratchBytes) until the process ends; calls on one device
+// share it, so calls that overlap on one device race. Host code never passes `scratch`
+// itself to a kernel (in host code the name is a stand-in, not a device address): it uses
+// the address hipGetSymbolAddress returns for the current device, kept per device below.
+constexpr size_t kNoAllocScratchFloats = size_t(1) << 21;  // 8 MiB
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+float *g_noalloc_ptr[kMaxDevices] = {};
+
+// Address of `scratch` on the current device (looked up once per device).
+float *noalloc_scratch(CError *err) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    hip_error(err, -1, "activation backward (no-alloc): hipGetDevice", e);
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error(err, -1, "activation backward (no-alloc): device %d beyond the %d supported", dev, kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  if (!g_noalloc_ptr[dev]) {
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      hip_error(err, -1, "activation backward (no-alloc): hipGetSymbolAddress(scratch)", e);
+      return nullptr;
+    }
+    g_noalloc_ptr[dev] = static_cast<float *>(ptr);
+  }
+  return g_noalloc_ptr[dev];
+}
+
+}  // namespace
+
+int noalloc_scratch_setup(CError *err) { return noalloc_scratch(err) ? 0 : -1; }
+
+int launch_act_backward(const float *grad_out, const float *pre, long rows, long cols, int act, float alpha,
+                        float scale, float *grad_in, float *grad_bias, hipStream_t s, CError *err) {
+  if (int rc = check_act_backward(grad_out, pre, rows, cols, act, grad_in, err))
+    return rc < 0 ? rc : zero_bias(cols, grad_bias, s, err);
+  ActBackwardPlan pl;
+  if (int rc = plan_act_backward(rows, cols, pl, err)) return rc;
+  float *partial = nullptr;
+  std::unique_lock<std::mutex> lk;
+  if (grad_bias) {
+    partial = static_cast<float *>(stream_scratch(s, (size_t)pl.chunks * (size_t)cols * sizeof(float), lk, err));
+    if (!partial) return -3;
+  }
+  return enqueue_act_backward(pl, grad_out, pre, rows, cols, act, alpha, scale, grad_in, grad_bias, partial, s, err);
+}
+
+int launch_act_backward_noalloc(const float *grad_out, const float *pre, long rows, long cols, int act, float alpha,
+                                float scale, float *grad_in, float *grad_bias, hipStream_t s, CError *err) {
+  if (int rc = check_act_backward(grad_out, pre, rows, cols, act, grad_in, err))
+    return rc < 0 ? rc : zero_bias(cols, grad_bias, s, err);
+  ActBackwardPlan pl;
+  if (int rc = plan_act_backward(rows, cols, pl, err)) return rc;
+  float *partial = nullptr;
+  if (grad_bias) {
+    const size_t need = (size_t)pl.chunks * (size_t)cols;
+    if (need > kNoAllocScratchFloats)
+      return set_error(err, -1,
+                       "activation backward (no-alloc): %ld columns need %zu floats of partial sums, more than the "
+                       "%zu-float scratch (at most %zu columns)",
+                       cols, need, kNoAllocScratchFloats, kNoAllocScratchFloats);
+    partial = noalloc_scratch(err);
+    if (!partial) return -1;
+  }
+  return enqueue_act_backward(pl, grad_out, pre, rows, cols, act, alpha, scale, grad_in, grad_bias, partial, s, err);
 }
 
 bool act_forward_supported(int act) { return act == -1 || act == 0 || act == 1 || act == 2 || (act >= 4 && act <= 7); }

@@ -67,6 +67,11 @@ static void init_context() {
     g_ctx_status = -1;
     return;
   }
+  // Device address of the allocation-free entry point's scratch array, looked up at set-up
+  // so that its calls do no lookup. A failure here affects only that entry point, which
+  // repeats the lookup and reports the error itself.
+  CError scratch_err{nullptr};
+  if (noalloc_scratch_setup(&scratch_err) != 0) free(scratch_err.message);
 }
 
 Context *context(CError *err) {

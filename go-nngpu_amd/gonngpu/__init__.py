@@ -82,6 +82,7 @@ SIGNATURES = {
     "gn_cast_f32_f16": (_I, [_VP, _VP, _SZ, _I, _VP, _ERR]),
     "gn_cast_f16_f32": (_I, [_VP, _VP, _SZ, _VP, _ERR]),
     "gn_activation_backward": (_I, [_VP, _VP, _L, _L, _I, _F, _F, _VP, _VP, _VP, _ERR]),
+    "gn_activation_backward_noalloc": (_I, [_VP, _VP, _L, _L, _I, _F, _F, _VP, _VP, _VP, _ERR]),
     "gn_transpose_f32": (_I, [_VP, _L, _L, _VP, _VP, _ERR]),
     "gn_activation_forward": (_I, [_VP, _VP, _L, _I, _F, _VP, _ERR]),
     "createMPSGraph": (_VP, []),

@@ -310,10 +310,30 @@ int gn_cast_f16_f32(const uint16_t *in, float *out, size_t n, void *stream, CErr
  * (:491-500), LeakyReLU/Sigmoid/Tanh/GELU backward (:501-520) and the bias gradient
  * ReduceSum(grad, axis 0) (:566-572); step 3 is two gn_gemm calls (NT for grad_input,
  * TN for grad_weight). grad_bias may be NULL; grad_in may alias grad_out. The column sums
- * are added in a fixed order (deterministic). Codes: -1 invalid argument, -3 scratch
- * allocation, -6 launch error. */
+ * are added in a fixed order (deterministic). The partial sums go into a per-stream
+ * scratch block that the library grows on demand (a larger call releases the old block
+ * and allocates a new one), so this call is not for HIP graph capture: a captured graph
+ * would keep a block a later, larger call replaces. gn_activation_backward_noalloc is the
+ * capturable form. Codes: -1 invalid argument, -3 scratch allocation, -6 launch error. */
 int gn_activation_backward(const float *grad_out, const float *pre, long rows, long cols, int act, float alpha,
                            float scale, float *grad_in, float *grad_bias, void *stream, CError *err);
+
+/* No counterpart in the reference. gn_activation_backward for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc. Same arguments and results, bit for bit (same work split and
+ * summation order). The partial column sums (chunks x cols floats) go into an 8 MiB
+ * device array of the library (each GPU holds its own copy until the process ends)
+ * instead of library-allocated scratch; no call allocates or frees memory. Call
+ * gn_init() at set-up: it creates the library context and looks up the array's address
+ * (the first call of any entry point does so otherwise). Limit: cols <= 2^21 when grad_bias is
+ * non-NULL, else -1 with a message. Every call on one GPU shares that array: calls that
+ * overlap on one GPU (concurrent streams, or several host threads) race and must be
+ * serialised by the caller. Every partial is written before it is read, so no clearing
+ * is needed between calls. Codes: -1 invalid argument or too many columns, -6 launch
+ * error. */
+int gn_activation_backward_noalloc(const float *grad_out, const float *pre, long rows, long cols, int act,
+                                   float alpha, float scale, float *grad_in, float *grad_bias, void *stream,
+                                   CError *err);
 
 /* out[cols,rows] = in[rows,cols]^T, fp32, LDS-tiled. */
 /* out = act(in) element-wise over n floats (the Part-1 activation forwards on device
