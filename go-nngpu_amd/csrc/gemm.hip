@@ -559,7 +559,7 @@ __device__ __forceinline__ void sched_interleave() {
 // Measured against a 4-stage ring of single K-tiles with one barrier per tile: NN
 // 1139 -> 1170, TN 1139 -> 1179, TT 1145 -> 1156, NT equal (TFLOP/s, 8192^3). Leaves
 // every DMA complete and every wave past a barrier, so the caller may reuse smem.
-template <int BM, int BN, int WM, int WN, bool TA, bool TB>
+template <int BM, int BN, int WM, int WN, bool TA, bool TB, int NS>
 __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long n0, long z, int nk, char *smem,
                                               float4_t (&acc)[BM / WM / 16][BN / WN / 16]) {
   constexpr int BK = 32;
@@ -573,7 +573,7 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
   constexpr int LPW = IPA + IPB;
   constexpr int RBA = BM * 2, RBB = BN * 2;  // LDS row bytes of MN-contiguous tiles (one k row)
   static_assert(CA % NW == 0 && CB % NW == 0 && IPA >= 1 && IPB >= 1, "DMA split");
-  static_assert(LPW < 64, "vmcnt range");
+  static_assert(NS >= 2 && (NS - 1) * LPW < 64, "ring slots within the vmcnt range");
   // Splitting each pair's DMA into two bursts (A at the barrier, B halfway through the
   // MFMAs) measured 2-4% faster at 256 x 256 with 8 waves (8192^3: NN 884 -> 851 us, NT
   // 872 -> 851 us) and 10% slower for the 4-wave 128 x 96 tiles of the C4 shape; four
@@ -709,15 +709,16 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
     __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - NIL, 0);
   };
 
-  issue(0, 0, 0, 2);
-  issue(0, 0, 1, 2);
-  issue(1, 1, 0, 2);
-  issue(1, 1, 1, 2);
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPW));
+#pragma unroll
+  for (int q = 0; q < NS; ++q) {  // the first NS pairs, one per slot
+    issue(q, q, 0, 2);
+    issue(q, q, 1, 2);
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 1) * LPW));
   __syncthreads();
   read_frags(0, 0, 0);
+  int cur = 0, nxt = 1;  // slot of pair pp, slot of pair pp + 1
   for (int pp = 0; pp < np; ++pp) {
-    const int cur = pp & 1;
     // even step: multiply tile 2pp, read tile 2pp+1 (same slot, already visible)
     __builtin_amdgcn_sched_barrier(0);
     // With the DMA in bursts, NT / TN / TT also split the even step's fragment reads over
@@ -737,9 +738,10 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
       mfma_set(0);
       interleave();
     }
-    // odd step: pair pp+1 lands; refill this pair's slot with pair pp+2
+    // odd step: pair pp+1 lands (the later NS - 2 pairs may still be in flight); refill this
+    // pair's slot with pair pp+NS
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * LPW));
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (kDmaParts > 1) {
@@ -749,22 +751,24 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
       // after 1/2 for NT / TN / TT (3/4 cost them 1-1.5%).
       constexpr int R0 = (!TA && !TB) ? 3 * FM / 4 : FM / 2;
       constexpr int NRH = (TA ? 2 : 1) * (FM / 2) + (TB ? 1 : 2) * (FN / 2);  // reads per part
-      issue(pp + 2, cur, 0, 2);
-      read_part(cur ^ 1, 0, 0, 0, 2);
+      issue(pp + NS, cur, 0, 2);
+      read_part(nxt, 0, 0, 0, 2);
       mfma_rows(1, 0, R0);
       sched_interleave<R0 * FN, NRH>();
       __builtin_amdgcn_sched_barrier(0);
-      issue(pp + 2, cur, 1, 2);
-      read_part(cur ^ 1, 0, 0, 1, 2);
+      issue(pp + NS, cur, 1, 2);
+      read_part(nxt, 0, 0, 1, 2);
       mfma_rows(1, R0, FM);
       sched_interleave<(FM - R0) * FN, NRH>();
     } else {
-      issue(pp + 2, cur, 0, 2);
-      issue(pp + 2, cur, 1, 2);
-      read_frags(cur ^ 1, 0, 0);
+      issue(pp + NS, cur, 0, 2);
+      issue(pp + NS, cur, 1, 2);
+      read_frags(nxt, 0, 0);
       mfma_set(1);
       interleave();
     }
+    cur = nxt;
+    nxt = nxt + 1 == NS ? 0 : nxt + 1;
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   __syncthreads();
@@ -772,11 +776,11 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
 
 // One workgroup per output tile, the whole K range. WPE: waves per SIMD the register
 // allocation is sized for.
-template <int BM, int BN, int WM, int WN, bool TA, bool TB, int WPE>
+template <int BM, int BN, int WM, int WN, bool TA, bool TB, int WPE, int NS>
 __global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 gemm_f16_ring_kernel(GemmParams p) {
   constexpr int FM = BM / WM / 16, FN = BN / WN / 16;
-  constexpr int RING = 4 * (BM + BN) * 32 * 2;  // two slots of two K-tiles of A and B
+  constexpr int RING = NS * 2 * (BM + BN) * 32 * 2;  // NS slots of two K-tiles of A and B
   __shared__ __attribute__((aligned(1024))) char smem[RING];
   int tm, tn;
   tile_coords(p, tm, tn);
@@ -786,7 +790,7 @@ gemm_f16_ring_kernel(GemmParams p) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
   const long m0 = (long)tm * BM, n0 = (long)tn * BN, z = blockIdx.z;
-  ring_mainloop<BM, BN, WM, WN, TA, TB>(p, m0, n0, z, (int)((p.K + 31) / 32), smem, acc);
+  ring_mainloop<BM, BN, WM, WN, TA, TB, NS>(p, m0, n0, z, (int)((p.K + 31) / 32), smem, acc);
   static_assert(WM * 16 * (BN + 4) * 4 <= RING, "epilogue staging exceeds the ring");
   store_tile_rows<BM, BN, WM, WN>(p, m0, n0, z, reinterpret_cast<float *>(smem), acc);
 }
@@ -810,12 +814,12 @@ hipError_t launch_f32(GemmParams p, long batch, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int BM, int BN, int WM, int WN, bool TA, bool TB, int WPE = 2>
+template <int BM, int BN, int WM, int WN, bool TA, bool TB, int WPE = 2, int NS = 2>
 hipError_t launch_f16_ring(GemmParams p, long batch, hipStream_t s) {
   p.tiles_m = (int)((p.M + BM - 1) / BM);
   p.tiles_n = (int)((p.N + BN - 1) / BN);
   dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
-  hipLaunchKernelGGL((gemm_f16_ring_kernel<BM, BN, WM, WN, TA, TB, WPE>), grid, dim3(WM * WN * 64), 0, s, p);
+  hipLaunchKernelGGL((gemm_f16_ring_kernel<BM, BN, WM, WN, TA, TB, WPE, NS>), grid, dim3(WM * WN * 64), 0, s, p);
   return hipGetLastError();
 }
 
@@ -835,6 +839,17 @@ hipError_t pick_f16(const GemmParams &p, long batch, hipStream_t s) {
     const long tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
     if (tiles128 >= 128 && ring_offsets_fit(p)) {
       if constexpr (TB) {
+        // 128 x 192 tiles, 8 waves, one workgroup per CU and a ring of three K-tile pairs
+        // (120 KiB): two pairs in flight instead of one. When they fill at least 3/4 of the
+        // CUs in as many rounds as two co-resident 128 x 96 workgroups per CU would take,
+        // they win by the deeper prefetch (the 512 x 11008 x 4096 linear layer, 232 tiles:
+        // 49.0 -> 46.9 us ReLU, 51.0 -> 47.9 us GELU on one box, 50.1 -> 49.1 / 52.8 -> 50.5 on
+        // another). Only for a K-contiguous B: 384-byte MN-contiguous rows would not take the
+        // 32-byte block swizzle of the transposing reads.
+        const long tiles192 = ((p.M + 127) / 128) * ((p.N + 191) / 192) * batch;
+        const long tiles96x = ((p.M + 127) / 128) * ((p.N + 95) / 96) * batch;
+        if (tiles192 >= 192 && (tiles192 + 255) / 256 <= (tiles96x + 511) / 512)
+          return launch_f16_ring<128, 192, 2, 4, TA, TB, 2, 3>(p, batch, s);
         // Two workgroups of these tiles share a CU, so the CU holding the most tiles
         // needs ceil(ceil(tiles / 256) / 2) rounds. 128x96 tiles (a K-contiguous B
         // allows N-tiles of 96) run at ~0.85x the per-CU rate of 128x128 and often

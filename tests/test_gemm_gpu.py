@@ -523,6 +523,37 @@ def test_f16_128x96_tiles_ragged(dev, tA):
 
 
 
+@pytest.mark.parametrize("tA", [False, True])
+def test_f16_ring_128x192_three_slots_ragged(dev, tA):
+    """K-contiguous B with enough 128x192 tiles for the 8-wave, three-slot ring (the C4 path):
+    M = 1000 and N = 5000 leave partial tiles in both directions, K = 1000 a partial K-tile
+    pair; alpha, beta, bias and GELU in the epilogue. Every output element is compared with a
+    float64 product of the same fp16 operands on the device, and NaN marks unwritten tiles."""
+    import torch
+
+    rng = np.random.default_rng(61)
+    M, N, K = 1000, 5000, 1000
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    a16 = torch.from_numpy(_stored(A, tA)).to(dev).half()
+    b16 = torch.from_numpy(np.ascontiguousarray(B.T)).to(dev).half()  # K-contiguous B: stored [N, K]
+    bd = torch.from_numpy(bias).to(dev)
+    for trial, beta in enumerate((0.0, 0.25)):
+        Cd = torch.from_numpy(C0).to(dev) if beta else _nan_like(dev, M, N)
+        G.gemm(a16, b16, Cd, transA=tA, transB=True, alpha=0.5, beta=beta, bias=bd, act=G.ACT_GELU)
+        opA = a16.double().t() if tA else a16.double()
+        pre = 0.5 * (opA @ b16.double().t().contiguous()) + bd.double()
+        if beta:
+            pre = pre + beta * torch.from_numpy(C0).to(dev).double()
+        ref = torch.from_numpy(O.act_f64(G.ACT_GELU, pre.cpu().numpy())).to(dev)
+        err = (torch.linalg.matrix_norm(Cd.double() - ref) / torch.linalg.matrix_norm(ref)).item()
+        _say("128x192 ring", tA, beta, err)
+        assert err <= 1e-5
+        assert torch.isfinite(Cd).all().item()
+
+
 def test_f16_register_staged_when_ring_offsets_overflow(dev):
     """A leading dimension of 2^21 halves or more overflows the ring kernels' 32-bit DMA
     offsets, so the register-staged kernel takes the 128x128 tiles. Its result equals the
