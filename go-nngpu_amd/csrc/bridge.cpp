@@ -73,16 +73,16 @@ bool csr_cache_enabled() {
 std::shared_ptr<CsrEntry> csr_entry(const Buffer *key, const int *rowptr, long rows, const int *cols, long nnz,
                                     hipStream_t s, CError *err) {
   const size_t rp_bytes = sizeof(int) * (size_t)(rows + 1);
+  std::shared_ptr<CsrEntry> cached;
   {
     std::lock_guard<std::mutex> lk(g_csr_mu);
     auto it = csr_cache().find(key);
-    if (it != csr_cache().end()) {
-      std::shared_ptr<CsrEntry> e = it->second;
-      if (e->host_rp == rowptr && e->host_col == cols && e->rows == rows && e->nnz == nnz &&
-          memcmp(e->rp_copy.data(), rowptr, rp_bytes) == 0)
-        return e;
-    }
+    if (it != csr_cache().end()) cached = it->second;
   }
+  // Entries are immutable once published, so the comparison needs no lock.
+  if (cached && cached->host_rp == rowptr && cached->host_col == cols && cached->rows == rows &&
+      cached->nnz == nnz && memcmp(cached->rp_copy.data(), rowptr, rp_bytes) == 0)
+    return cached;
   auto e = std::make_shared<CsrEntry>();
   e->host_rp = rowptr;
   e->host_col = cols;

@@ -286,6 +286,13 @@ def test_spmm_index_cache_reuse_and_invalidation(dev):
     assert G.memory_stats()[2] == n0
     col_new[3] = 0
     np.testing.assert_array_equal(run(rp, col_new), O.spmm_f32(rp, col_new, val, D, use_fma=True))
+    # values scaled in place (perform_sparse_scalar_multiply) are read on the next call: the
+    # cache holds the index arrays only
+    G.call("perform_sparse_scalar_multiply", bv.handle, rp.ctypes.data, rp.size, col_new.ctypes.data, col_new.size,
+           rows, cols, val.size, -2.0, None)
+    np.testing.assert_array_equal(run(rp, col_new), O.spmm_f32(rp, col_new, val * np.float32(-2.0), D, use_fma=True))
+    G.call("perform_sparse_scalar_multiply", bv.handle, rp.ctypes.data, rp.size, col_new.ctypes.data, col_new.size,
+           rows, cols, val.size, -0.5, None)
     # SpMV with the same values buffer shares the cached structure
     x = O.normal((cols,), 8, 1)
     bx, by = G.Buffer.from_array(x), G.Buffer(rows * 4)
