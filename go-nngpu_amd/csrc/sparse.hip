@@ -3,12 +3,15 @@
 // Replaces the reference's single-threaded CPU loops perform_sparse_dense_matmul
 // (internal/cgo/metal_bridge_sparse.m:117-133) and perform_sparse_matvec (:325-339).
 //
-// SpMM: a group of LPR lanes owns one CSR row (LPR = 64 for N >= 256: one wave64 per
-// row). Lane l of the group accumulates columns 4l..4l+3 (+4*LPR per chunk), so every
-// stored entry triggers one fully coalesced gather of a D-row segment (1 KiB per wave
-// for N = 256). Each output is accumulated in CSR order with one fma per entry, which
-// reproduces the reference loop's summation order exactly (bit-identical to an fmaf
-// restatement of it). Row pointers and column indices are validated in the kernel:
+// SpMM: with 16-byte aligned rows and N >= 32, spmm_band_kernel splits the columns into
+// 32-float bands (one 128-byte line of a D row) and runs the bands one after another, so
+// the D lines gathered at any time fit the L2 far better than whole 1 KiB D rows do: the
+// kernel is bound by L2 refills from the Infinity Cache, and banding cuts them by a
+// quarter at N = 256. Narrower or unaligned products use a group of LPR lanes per CSR
+// row, lane l accumulating columns 4l..4l+3 (or column l). Each output is accumulated in
+// CSR order with one fma per entry, which reproduces the reference loop's summation
+// order exactly (bit-identical to an fmaf restatement of it, in every kernel).
+// Row pointers and column indices are validated in the kernel:
 // an invalid row pointer pair empties the row and raises flags[0]; an out-of-range
 // column skips that entry and raises flags[1]. No access ever leaves its array.
 //
@@ -127,6 +130,84 @@ __global__ void __launch_bounds__(kBlock) spmm_scalar_kernel(long M, long N, lon
   }
 }
 
+// Column-banded SpMM for N >= 32 (16-byte aligned D and C rows). The output columns are
+// cut into bands of kBandCols = 32 floats, one 128-byte L2 line of each D row; 8 lanes
+// own a (row, band) pair, 4 columns each, so a wave covers 8 rows of one band and each
+// gather instruction touches 8 whole lines. Workgroups run band-major (all row blocks of
+// band 0, then band 1, ...), so the workgroups resident at any time gather from one or
+// two bands of D: an 8 MiB working set per band at N = 256 instead of all of D. The
+// entries of a row are consumed in CSR order in batches of kBandUnroll, whose index
+// loads and gathers are all issued before the first fma; a row's last entries go one
+// at a time. Every output is the same fma chain as in spmm_vec4_kernel.
+constexpr int kBandCols = 32;
+constexpr int kBandLanes = kBandCols / 4;
+constexpr int kBandRowsPerBlock = (kBlock / 64) * (64 / kBandLanes);
+constexpr int kBandUnroll = 16;
+
+__global__ void __launch_bounds__(kBlock) spmm_band_kernel(long M, long N, long K, long nnz, long row_blocks,
+                                                           const int32_t *__restrict__ rowptr,
+                                                           const int32_t *__restrict__ col,
+                                                           const float *__restrict__ val,
+                                                           const float *__restrict__ D, long ldd,
+                                                           float *__restrict__ C, long ldc, int *flags) {
+  const int lane = threadIdx.x & 63;
+  const int li = lane % kBandLanes;
+  const long band = blockIdx.x / row_blocks;
+  const long row = (blockIdx.x % row_blocks) * kBandRowsPerBlock + (threadIdx.x >> 6) * (64 / kBandLanes) +
+                   lane / kBandLanes;
+  const long c0 = band * kBandCols + 4 * li;
+  // No cross-lane operations follow, so lanes past the last row or column leave here.
+  if (row >= M || c0 >= N) return;
+  int s, e;
+  row_bounds(rowptr, row, nnz, s, e, flags, li == 0);
+  float4_t acc = {0.f, 0.f, 0.f, 0.f};
+  bool bad_col = false;
+  int k = s;
+  for (; k + kBandUnroll <= e; k += kBandUnroll) {
+    int cc[kBandUnroll];
+    float vv[kBandUnroll];
+    float4_t dd[kBandUnroll];
+#pragma unroll
+    for (int u = 0; u < kBandUnroll; ++u) {
+      cc[u] = col[k + u];
+      vv[u] = val[k + u];
+    }
+    unsigned ok = 0;  // bit u: entry k+u has a column inside D
+#pragma unroll
+    for (int u = 0; u < kBandUnroll; ++u) {
+      if ((unsigned)cc[u] < (unsigned long)K) {
+        dd[u] = *reinterpret_cast<const float4_t *>(D + (long)cc[u] * ldd + c0);
+        ok |= 1u << u;
+      }
+    }
+    bad_col |= ok != (1u << kBandUnroll) - 1;
+#pragma unroll
+    for (int u = 0; u < kBandUnroll; ++u) {
+      if (ok & (1u << u)) {
+        acc[0] = __builtin_fmaf(vv[u], dd[u][0], acc[0]);
+        acc[1] = __builtin_fmaf(vv[u], dd[u][1], acc[1]);
+        acc[2] = __builtin_fmaf(vv[u], dd[u][2], acc[2]);
+        acc[3] = __builtin_fmaf(vv[u], dd[u][3], acc[3]);
+      }
+    }
+  }
+  for (; k < e; ++k) {
+    const int c = col[k];
+    if ((unsigned)c < (unsigned long)K) {
+      const float v = val[k];
+      const float4_t d = *reinterpret_cast<const float4_t *>(D + (long)c * ldd + c0);
+      acc[0] = __builtin_fmaf(v, d[0], acc[0]);
+      acc[1] = __builtin_fmaf(v, d[1], acc[1]);
+      acc[2] = __builtin_fmaf(v, d[2], acc[2]);
+      acc[3] = __builtin_fmaf(v, d[3], acc[3]);
+    } else {
+      bad_col = true;
+    }
+  }
+  if (bad_col && flags) flags[1] = 1;
+  *reinterpret_cast<float4_t *>(C + row * ldc + c0) = acc;
+}
+
 template <int LPR>
 __global__ void __launch_bounds__(kBlock) spmv_kernel(long M, long K, long nnz, const int32_t *__restrict__ rowptr,
                                                       const int32_t *__restrict__ col,
@@ -166,6 +247,15 @@ int launch_spmm(long M, long N, long K, long nnz, const int32_t *rowptr, const i
   if (ldd < N || ldc < N) return set_error(err, -1, "spmm: leading dimension smaller than N");
   if (nnz > 0x7FFFFFFFL || M > 0x7FFFFFF0L) return set_error(err, -1, "spmm: exceeds int32 CSR indexing");
   const bool vec = N % 4 == 0 && ldd % 4 == 0 && ldc % 4 == 0 && (uintptr_t)D % 16 == 0 && (uintptr_t)C % 16 == 0;
+  if (vec && N >= kBandCols) {
+    const long row_blocks = (M + kBandRowsPerBlock - 1) / kBandRowsPerBlock;
+    const long bands = (N + kBandCols - 1) / kBandCols;
+    if (row_blocks > 0x7FFFFFFFL / bands) return set_error(err, -1, "spmm: too many rows");
+    hipLaunchKernelGGL(spmm_band_kernel, dim3((unsigned)(row_blocks * bands)), dim3(kBlock), 0, s, M, N, K, nnz,
+                       row_blocks, rowptr, col, val, D, ldd, C, ldc, flags);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : hip_error(err, -6, "spmm launch", e);
+  }
   const int lpr = next_pow2_lanes(vec ? (N + 3) / 4 : N);
   const long rows_per_block = (kBlock / 64) * (64 / lpr);
   const long blocks = (M + rows_per_block - 1) / rows_per_block;

@@ -59,6 +59,67 @@ def test_spmm_widths_bit_exact(dev, N):
     np.testing.assert_array_equal(C, O.spmm_f32(rp, col, val, D, use_fma=True))
 
 
+def _shuffle_rows(rp, col, seed):
+    rng = np.random.default_rng(seed)
+    col = col.copy()
+    for r in range(rp.size - 1):
+        rng.shuffle(col[rp[r]:rp[r + 1]])
+    return col
+
+
+@pytest.mark.parametrize("N,ldd,ldc,order", [(32, 32, 32, "sorted"), (36, 40, 36, "unsorted"),
+                                             (96, 96, 100, "duplicates"), (256, 256, 256, "sorted"),
+                                             (260, 272, 264, "unsorted")])
+def test_spmm_column_bands_long_rows_bit_exact(dev, N, ldd, ldc, order):
+    """Rows long enough for several full 16-entry batches plus a tail, a partial last
+    column band (N % 32 != 0), pitches wider than N, unsorted or repeated columns; the
+    device-pointer entry. Columns past N in C keep their contents."""
+    import torch
+
+    M, K = 1000, 3000
+    rp, col, val = O.random_csr(M, K, 45.0, seed=N, distinct=order != "duplicates")
+    if order == "unsorted":
+        col = _shuffle_rows(rp, col, N)
+    assert (rp[1:] - rp[:-1]).max() >= 48
+    D = O.normal((K, N), 7, N)
+    ref = O.spmm_f32(rp, col, val, D, use_fma=True)
+    d = [torch.from_numpy(a).to(dev) for a in (rp, col, val)]
+    Dd = torch.zeros((K, ldd), dtype=torch.float32, device=dev)
+    Dd[:, :N] = torch.from_numpy(D).to(dev)
+    Cd = torch.full((M, ldc), float("nan"), dtype=torch.float32, device=dev)
+    flags = torch.zeros(2, dtype=torch.int32, device=dev)
+    G.spmm_csr(M, N, K, val.size, d[0], d[1], d[2], Dd, Cd, flags, ldd=ldd, ldc=ldc)
+    assert flags.cpu().tolist() == [0, 0]
+    C = Cd.cpu().numpy()
+    np.testing.assert_array_equal(C[:, :N], ref)
+    assert np.isnan(C[:, N:]).all()
+
+
+def test_spmm_column_bands_skip_bad_columns_in_full_batches(dev):
+    """An out-of-range column inside a full 16-entry batch and another in a row's tail
+    are skipped (the rest of the row keeps CSR order) and reported in flags[1]."""
+    import torch
+
+    M, K, N = 64, 500, 64
+    rp, col, val = O.random_csr(M, K, 40.0, seed=9)
+    lens = rp[1:] - rp[:-1]
+    assert lens[3] >= 16 and lens[7] >= 33
+    bad = col.copy()
+    drop = [rp[3] + 5, rp[7] + lens[7] - 1]  # batch entry of row 3, last (tail) entry of row 7
+    bad[drop[0]], bad[drop[1]] = K + 5, -1
+    keep = np.ones(col.size, bool)
+    keep[drop] = False
+    rp_keep = np.concatenate([[0], np.cumsum([keep[rp[r]:rp[r + 1]].sum() for r in range(M)])]).astype(np.int32)
+    D = O.normal((K, N), 8, 1)
+    ref = O.spmm_f32(rp_keep, col[keep], val[keep], D, use_fma=True)
+    d = [torch.from_numpy(a).to(dev) for a in (rp, bad, val, D)]
+    Cd = torch.empty((M, N), dtype=torch.float32, device=dev)
+    flags = torch.zeros(2, dtype=torch.int32, device=dev)
+    G.spmm_csr(M, N, K, val.size, d[0], d[1], d[2], d[3], Cd, flags)
+    assert flags.cpu().tolist() == [0, 1]
+    np.testing.assert_array_equal(Cd.cpu().numpy(), ref)
+
+
 def test_spmm_with_duplicates_unsorted_columns(dev):
     rp, col, val = O.random_csr(300, 50, 20.0, seed=3, distinct=False)  # many duplicate columns
     D = O.normal((50, 256), 6, 1)
