@@ -25,7 +25,7 @@ semantics) on a bounded row sample of the headline problem, on the host cores.
 C ABI, PCIe included: upload fp32 A and B (create_gpu_buffer), cast both to fp16 on
 the device, GEMM, download C (retrieve_gpu_buffer_data), wall-clock per step.
 
-`--only a,b,...` runs a subset of {c3, c2, c4, spmm, spmv, e2e, copy} (used by the
+`--only a,b,...` runs a subset of {c3, c2, c1, c4, spmm, spmv, e2e, copy} (used by the
 rocprofv3 passes that produce profiles/); `copy` is a 1 GiB device copy used to
 calibrate the HBM byte counters.
 """
@@ -45,7 +45,7 @@ PEAK_F16_TFLOPS = 2516.6  # dense MFMA fp16, 256 CU x 4096 flop/clk x 2.4 GHz
 PEAK_F32_TFLOPS = 157.3   # fp32 MFMA
 MIN_WARM_MS = 50.0        # least untimed GPU time before each timed leg (see timed())
 PEAK_HBM_GBS = 8000.0
-ALL = ("c3", "c2", "c4", "spmm", "spmv", "e2e", "copy")
+ALL = ("c3", "c2", "c1", "c4", "spmm", "spmv", "e2e", "copy")
 
 
 def log(*a):
@@ -232,6 +232,41 @@ def run_c2(c, steps, warmup):
     return res
 
 
+def run_c1(c, steps, warmup):
+    """C1: fp32 256^3, entries U[-1,1]. The kernel time through the device API (back-to-back
+    launches, HIP events) and the wall clock of the synchronous Part-1 call
+    perform_mps_matrix_multiplication on GPUPtr buffers, as the gonum facade's Mul makes it."""
+    import numpy as np
+
+    from gonngpu import synth
+
+    G, n = c.G, 256
+    A, B, C = c.empty((n, n)), c.empty((n, n)), c.empty((n, n))
+    c.G.fill_uniform(A, 42, 11, stream_ptr=c.sp)
+    c.G.fill_uniform(B, 42, 12, stream_ptr=c.sp)
+    ms = timed(lambda: c.G.gemm(A, B, C, stream_ptr=c.sp), steps, warmup, c.stream, MIN_WARM_MS)
+    ha, hb = synth.host_uniform((n, n), 13), synth.host_uniform((n, n), 14)
+    ba, bb, bc = G.Buffer.from_array(ha), G.Buffer.from_array(hb), G.Buffer(n * n * 4)
+    call = lambda: G.call("perform_mps_matrix_multiplication", ba.handle, n, n, bb.handle, n, n, bc.handle, n, n,
+                          None)
+    for _ in range(max(3, warmup)):
+        call()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        call()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    out = bc.to_array((n, n))
+    assert np.isfinite(out).all()
+    for b in (ba, bb, bc):
+        b.release()
+    tf = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+    log(f"c1 256^3 fp32: kernel {ms * 1e3:.1f} us ({tf:.2f} TFLOP/s), perform_mps_matrix_multiplication "
+        f"{wall * 1e3:.1f} us per synchronous call")
+    return {"kernel_us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 3), "part1_call_us": round(wall * 1e3, 1),
+            "what": "device-API kernel time (back-to-back launches) and the synchronous Part-1 call's wall clock "
+                    "(launch + completion wait) on resident GPUPtr buffers"}
+
+
 def run_c4(c, steps, warmup):
     X16 = c.f16_normal((512, 4096), 5, 1.0)
     W16 = c.f16_normal((11008, 4096), 6, 0.02)
@@ -333,9 +368,9 @@ def run_part1_sparse(c, kind, steps, kernel_ms):
     rp, col, val = c.csr_host
     M = rp.size - 1
     N = 256 if kind == "spmm" else 1
-    from oracle import oracle as O
+    from gonngpu import synth
 
-    dense = O.normal((M, N), 42, 110) if kind == "spmm" else O.normal((M,), 42, 111)
+    dense = synth.host_normal((M, N), 110) if kind == "spmm" else synth.host_normal((M,), 111)
     bv, bd, bo = G.Buffer.from_array(val), G.Buffer.from_array(dense), G.Buffer(M * N * 4)
     if kind == "spmm":
         args = lambda: (bv.handle, rp.ctypes.data, rp.size, col.ctypes.data, col.size, M, M, val.size, bd.handle, M,
@@ -411,12 +446,12 @@ def run_e2e(c, steps, warmup):
     """C3 from host fp32 arrays: upload, device fp16 cast, GEMM, download (wall clock)."""
     import numpy as np
 
-    from oracle import oracle as O
+    from gonngpu import synth
 
     G = c.G
     n = 8192
-    A = O.normal((n, n), 42, 201)
-    B = O.normal((n, n), 42, 202, 0.0, 0.02)
+    A = synth.host_normal((n, n), 201)
+    B = synth.host_normal((n, n), 202, 0.0, 0.02)
     Cout = np.empty((n, n), dtype=np.float32)
 
     def step():
@@ -483,6 +518,8 @@ def main():
     if "c2" in only:
         secondary.update(run_c2(c, steps2, 3))
         c.torch.cuda.empty_cache()
+    if "c1" in only:
+        secondary["c1_f32_256"] = run_c1(c, steps2 * 20, 20)
     if "c4" in only:
         secondary.update(run_c4(c, steps2 * 4, 5))
         c.torch.cuda.empty_cache()

@@ -18,3 +18,13 @@ def csr_uniform(M, K, mean_row, seed):
     np.cumsum(np.bincount(rows, minlength=M), out=rowptr[1:])
     val = rng.uniform(-1.0, 1.0, size=col.size).astype(np.float32)
     return rowptr.astype(np.int32), col, val
+
+
+def host_normal(shape, seed, mean=0.0, std=1.0):
+    """float32 N(mean, std^2) host array (numpy's generator; for inputs that start on the host)."""
+    return np.random.default_rng(seed).normal(mean, std, size=shape).astype(np.float32)
+
+
+def host_uniform(shape, seed, lo=-1.0, hi=1.0):
+    """float32 U[lo, hi) host array."""
+    return np.random.default_rng(seed).uniform(lo, hi, size=shape).astype(np.float32)
