@@ -2,9 +2,9 @@
 SparseMatVec, FusedLinearActivation, ForwardFloat16, LinearLayer, GPUDense, GPUSparse)
 through the C ABI, checked against the oracle. Runs the compiled test binary in --gpu
 mode in one process."""
+import importlib.util
 import os
 
-import numpy as np
 import pytest
 
 from test_host_cpu import HERE, run_host_tests
@@ -12,14 +12,17 @@ from test_host_cpu import HERE, run_host_tests
 pytestmark = pytest.mark.gpu
 
 
+def _c1_fixture_writer():
+    spec = importlib.util.spec_from_file_location("write_c1_fixture", os.path.join(HERE, "host", "write_c1_fixture.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.write
+
+
 def test_host_api_gpu(tmp_path):
     # Config C1's committed fixture as raw arrays for TestGPUMatMulC1Golden.
-    z = np.load(os.path.join(HERE, "golden", "gemm_256.npz"))
     raw = tmp_path / "c1.bin"
-    with open(raw, "wb") as f:
-        f.write(np.ascontiguousarray(z["A"], dtype=np.float32).tobytes())
-        f.write(np.ascontiguousarray(z["B"], dtype=np.float32).tobytes())
-        f.write(np.ascontiguousarray(z["C64"], dtype=np.float64).tobytes())
+    _c1_fixture_writer()(str(raw))
     os.environ["GONNGPU_C1_FIXTURE"] = str(raw)
     try:
         text = run_host_tests("--gpu")
