@@ -220,6 +220,19 @@ struct TileLoader {
       *reinterpret_cast<u32x4_t *>(lds + r * P + c) = reg[j];
     }
   }
+  // Transposed store: element (r, c + e) of the tile goes to lds[(c + e) * P + r].
+  template <int P>
+  __device__ __forceinline__ void store_t(T *lds) const {
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int v = threadIdx.x + j * NT;
+      const int r = v / VPR;
+      const int c = (v % VPR) * EPV;
+      const T *e = reinterpret_cast<const T *>(&reg[j]);
+#pragma unroll
+      for (int q = 0; q < EPV; ++q) lds[(c + q) * P + r] = e[q];
+    }
+  }
   // Same-layout store for an MN-contiguous fp16 tile that frag_tr reads: the
   // 16-half column block is XOR-swizzled by bit 3 of the row (frag_tr undoes it).
   template <int P>
@@ -353,17 +366,23 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f16_kernel(GemmParams p) {
 //  * an M/N-contiguous operand keeps its memory layout (k rows of BM or BN floats,
 //    pitch + 4, so the 4 rows 4g + s of one step fall on distinct banks) and each lane
 //    reads one float per step. Storing it transposed instead would turn every 16-byte
-//    tile store into four 4-byte LDS writes.
+//    tile store into four 4-byte LDS writes;
+//  * except NT with BK = 16: both operands K-contiguous put bank conflicts on both
+//    16-byte fragment reads (25 M conflict cycles per operand at 4096^3), so both tiles
+//    are stored transposed (four 4-byte writes, conflict-free for these loaders) and read
+//    as M/N-contiguous ones: 4096^3 NT 1045 -> 1020 us; NN, TN and TT do not gain.
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VEC>
 __global__ void __launch_bounds__(WM * WN * 64) gemm_f32_kernel(GemmParams p) {
   constexpr int NT = WM * WN * 64;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 16, FN = WTN / 16;
   static_assert(BK % 16 == 0, "tile shape");
-  constexpr int PA = TA ? BM + 4 : BK + 4;  // LDS pitches (floats)
-  constexpr int PB = TB ? BK + 4 : BN + 4;
-  constexpr int A_ELEMS = TA ? BK * PA : BM * PA;
-  constexpr int B_ELEMS = TB ? BN * PB : BK * PB;
+  constexpr bool XT = !TA && TB && BK == 16;  // NT: both tiles stored transposed
+  constexpr bool MA = TA || XT, MB = !TB || XT;  // tile is M/N-contiguous in LDS
+  constexpr int PA = MA ? BM + 4 : BK + 4;  // LDS pitches (floats)
+  constexpr int PB = MB ? BN + 4 : BK + 4;
+  constexpr int A_ELEMS = MA ? BK * PA : BM * PA;
+  constexpr int B_ELEMS = MB ? BK * PB : BN * PB;
   __shared__ __attribute__((aligned(16))) float smem[2 * (A_ELEMS + B_ELEMS)];
 
   int tm, tn;
@@ -389,8 +408,13 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32_kernel(GemmParams p) {
   auto store_tiles = [&](int stage) {
     float *as = smem + stage * (A_ELEMS + B_ELEMS);
     float *bs = as + A_ELEMS;
-    la.template store<PA>(as);
-    lb.template store<PB>(bs);
+    if constexpr (XT) {
+      la.template store_t<PA>(as);
+      lb.template store_t<PB>(bs);
+    } else {
+      la.template store<PA>(as);
+      lb.template store<PB>(bs);
+    }
   };
 
   float4_t acc[FM][FN];
@@ -418,7 +442,7 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32_kernel(GemmParams p) {
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         const int r = wm * WTM + i * 16 + li;
-        if (TA) {
+        if (MA) {
 #pragma unroll
           for (int s = 0; s < 4; ++s) af[i][s] = as[(kc + 4 * lg + s) * PA + r];
         } else {
@@ -428,7 +452,7 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32_kernel(GemmParams p) {
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         const int c = wn * WTN + j * 16 + li;
-        if (TB) {
+        if (!MB) {
           bf[j] = *reinterpret_cast<const float4_t *>(bs + c * PB + kc + 4 * lg);
         } else {
 #pragma unroll
