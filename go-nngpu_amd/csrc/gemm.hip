@@ -7,9 +7,10 @@
 // kernels (metal_bridge_kernels.m:28-110) and the fused_linear_activation kernel
 // (default.metal:459-509).
 //
-// Two kernel families share the epilogue and the tile order: gemm_f16_ring_kernel
-// (large aligned fp16 problems; described at its definition) and the register-staged
-// gemm_f16_kernel / gemm_f32_kernel for every other shape, structured as follows
+// Two kernel families share the epilogue and the tile order: the DMA-ring kernels
+// gemm_f16_ring_kernel and gemm_f32_ring_kernel (large fp16 and fp32 problems; described
+// at their definitions) and the register-staged gemm_f16_kernel / gemm_f32_kernel for
+// every other shape, structured as follows
 // (one workgroup per BM x BN output tile, WM x WN waves, 64 lanes each):
 //  * global -> VGPR prefetch of the next BK slice overlaps the MFMAs of the current
 //    one; LDS is double buffered, one barrier per BK slice;
@@ -819,6 +820,181 @@ gemm_f16_ring_kernel(GemmParams p) {
   store_tile_rows<BM, BN, WM, WN>(p, m0, n0, z, reinterpret_cast<float *>(smem), acc);
 }
 
+// ------------------------------------------------------------------ fp32 DMA-ring kernel
+// The fp16 ring's structure for fp32 operands. A K-tile is 16 floats (64 bytes per row,
+// as a 32-half fp16 K-tile), so K-contiguous tiles use the same 1 KiB chunks of 8 rows x
+// one K-tile pair (kc8 layout) and one ds_read_b128 per fragment gives lane (i, g) the
+// four k = 4g..4g+3 that MFMA steps s = 0..3 take. MN-contiguous tiles keep their k rows
+// (BM or BN floats, 512 or 1024 bytes) with the 16-byte block index XORed by
+// msw32(k): the rows k and k + 4 that one 32-lane phase of a fragment read touches
+// (lane groups g = 0, 1 at step s) land 16 banks apart; each lane reads its four k
+// with ds_read_b32.
+__device__ __forceinline__ int msw32(int k) { return ((k >> 2) & 1) << 2; }
+
+template <int BM, int BN, int WM, int WN, bool TA, bool TB, int NS>
+__device__ __forceinline__ void ring_mainloop_f32(const GemmParams &p, long m0, long n0, long z, int nk, char *smem,
+                                                  float4_t (&acc)[BM / WM / 16][BN / WN / 16]) {
+  constexpr int BK = 16;
+  constexpr int NW = WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 16, FN = WTN / 16;
+  constexpr int OPA = BM * BK * 4, OPB = BN * BK * 4;  // bytes of one K-tile of A / B
+  constexpr int SLOT = 2 * (OPA + OPB);
+  constexpr int CA = 2 * OPA / 1024, CB = 2 * OPB / 1024;
+  constexpr int IPA = CA / NW, IPB = CB / NW;
+  constexpr int LPW = IPA + IPB;
+  constexpr int RBA = BM * 4, RBB = BN * 4;  // bytes of one k row of an MN-contiguous tile
+  static_assert(CA % NW == 0 && CB % NW == 0 && IPA >= 1 && IPB >= 1, "DMA split");
+  static_assert(NS >= 2 && (NS - 1) * LPW < 64, "ring slots within the vmcnt range");
+  static_assert((!TA || RBA == 512 || RBA == 1024) && (TB || RBB == 512 || RBB == 1024),
+                "MN-contiguous k rows of 128 or 256 floats");
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wm = wave / WN, wn = wave % WN;
+
+  BufRsrc ra, rb;
+  unsigned voa[IPA], vob[IPB];
+  // Lane offset of chunk c and the k (0..2 BK - 1 within the pair) it covers.
+  auto plan = [&](bool kcontig, int c, int nchunks, int rb_bytes, long ld, long lim, unsigned &vo, int &kl) {
+    if (kcontig) {  // chunk c: rows 8c..8c+7, the pair's 32 k (128 bytes) each
+      const int row = 8 * c + (lane >> 3), q = kc8_octet(row, lane & 7);
+      kl = 4 * q;
+      vo = lim > row ? (unsigned)((long)row * ld * 4 + 16 * q) : kOutOfRange;
+      return;
+    }
+    // chunk cl of tile h: k rows cl * (1024 / rb_bytes) ..; lane L fills slot L % bpr of
+    // its row with block (L % bpr) ^ msw32(k)
+    const int h = c / (nchunks / 2), cl = c % (nchunks / 2);
+    const int bpr = rb_bytes / 16;
+    const int k = cl * (1024 / rb_bytes) + lane / bpr, b = (lane % bpr) ^ msw32(k);
+    kl = BK * h + k;
+    vo = lim > 4 * b ? (unsigned)((long)(BK * h + k) * ld * 4 + 16 * b) : kOutOfRange;
+  };
+  {
+    const float *A = static_cast<const float *>(p.A) + z * p.strideA;
+    const float *B = static_cast<const float *>(p.B) + z * p.strideB;
+    ra = make_rsrc(TA ? A + m0 : A + m0 * p.lda);
+    rb = make_rsrc(TB ? B + n0 * p.ldb : B + n0);
+  }
+  {
+    int kl;
+#pragma unroll
+    for (int i = 0; i < IPA; ++i) plan(!TA, wave * IPA + i, CA, RBA, p.lda, p.M - m0, voa[i], kl);
+#pragma unroll
+    for (int i = 0; i < IPB; ++i) plan(TB, wave * IPB + i, CB, RBB, p.ldb, p.N - n0, vob[i], kl);
+  }
+  const long a_step = TA ? 2L * BK * p.lda * 4 : 2L * BK * 4;
+  const long b_step = TB ? 2L * BK * 4 : 2L * BK * p.ldb * 4;
+  const unsigned sbase = lds_offset(smem);
+  const int np = max(1, (nk + 1) >> 1);
+
+  // The caller guarantees K % (2 BK) == 0, so a pair is either whole or past the end of
+  // K. Pairs past the end (the ring refills of the last NS steps, and the prologue's when
+  // np < NS) still issue their LPW copies, which the vmcnt waits count, but with the
+  // out-of-range offset: they read zeros and touch no memory.
+  auto issue = [&](int pp, int slot) {
+    const bool live = pp < np;
+    const unsigned st = sbase + (unsigned)(slot * SLOT);
+#pragma unroll
+    for (int i = 0; i < IPA; ++i)
+      dma16(ra, live ? voa[i] : kOutOfRange, __builtin_amdgcn_readfirstlane(st + (wave * IPA + i) * 1024));
+#pragma unroll
+    for (int i = 0; i < IPB; ++i)
+      dma16(rb, live ? vob[i] : kOutOfRange, __builtin_amdgcn_readfirstlane(st + 2 * OPA + (wave * IPB + i) * 1024));
+    rsrc_advance(ra, a_step);
+    rsrc_advance(rb, b_step);
+  };
+
+  // K-contiguous: rows row0..row0+15 of K-tile h; MN-contiguous: columns col0..col0+15.
+  auto frag_k = [&](const char *base, int row0, int h) -> float4_t {
+    const int row = row0 + (lane & 15);
+    return *reinterpret_cast<const float4_t *>(base + (row >> 3) * 1024 + 16 * kc8_slot(row, 4 * h + (lane >> 4)));
+  };
+  // MN-contiguous fragment j of a wave: lane (i, g) reads column wave_off + 16 j + i of k
+  // rows 4g..4g+3. msw32(4g + s) = 4 (g & 1) flips bit 0 of j, so the byte offset is
+  // lane_base(g, i) + 64 (j ^ (g & 1)) + s * rowb: one base for even j, one for odd j.
+  auto mn_bases = [&](int wave_off, int rowb, int &even, int &odd) {
+    const int i = lane & 15, g = lane >> 4;
+    const int base = 4 * wave_off + 16 * (i >> 2) + 4 * (i & 3) + 4 * g * rowb;
+    even = base + 64 * (g & 1);
+    odd = base - 64 * (g & 1);
+  };
+  int mna_e = 0, mna_o = 0, mnb_e = 0, mnb_o = 0;
+  if (TA) mn_bases(wm * WTM, RBA, mna_e, mna_o);
+  if (!TB) mn_bases(wn * WTN, RBB, mnb_e, mnb_o);
+  auto frag_mn = [&](const char *region, int j, int even, int odd, int rowb) -> float4_t {
+    const char *p0 = region + ((j & 1) ? odd : even) + 64 * j;
+    float4_t f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) f[s] = *reinterpret_cast<const float *>(p0 + s * rowb);
+    return f;
+  };
+
+  float4_t fa[2][FM], fb[2][FN];
+  auto read_frags = [&](int slot, int h, int set) {
+    const char *sa = smem + slot * SLOT + (TA ? h * OPA : 0);
+    const char *sb = smem + slot * SLOT + 2 * OPA + (TB ? 0 : h * OPB);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) fa[set][i] = TA ? frag_mn(sa, i, mna_e, mna_o, RBA) : frag_k(sa, wm * WTM + i * 16, h);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) fb[set][j] = TB ? frag_k(sb, wn * WTN + j * 16, h) : frag_mn(sb, j, mnb_e, mnb_o, RBB);
+  };
+  constexpr int NDS = (TA ? 4 : 1) * FM + (TB ? 1 : 4) * FN;  // LDS read instructions per K-tile
+  auto mfma_set = [&](int set) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[set][i][s], fb[set][j][s], acc[i][j], 0, 0, 0);
+  };
+
+#pragma unroll
+  for (int q = 0; q < NS; ++q) issue(q, q);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 1) * LPW));
+  __syncthreads();
+  read_frags(0, 0, 0);
+  int cur = 0, nxt = 1;
+  for (int pp = 0; pp < np; ++pp) {
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(cur, 1, 1);
+    mfma_set(0);
+    sched_interleave<4 * FM * FN, NDS>();
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * LPW));
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(pp + NS, cur);
+    read_frags(nxt, 0, 0);
+    mfma_set(1);
+    sched_interleave<4 * FM * FN, NDS>();
+    cur = nxt;
+    nxt = nxt + 1 == NS ? 0 : nxt + 1;
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  __syncthreads();
+}
+
+template <int BM, int BN, int WM, int WN, bool TA, bool TB, int WPE, int NS>
+__global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+gemm_f32_ring_kernel(GemmParams p) {
+  constexpr int FM = BM / WM / 16, FN = BN / WN / 16;
+  constexpr int RING = NS * 2 * (BM + BN) * 16 * 4;  // NS slots of two K-tiles of A and B
+  __shared__ __attribute__((aligned(1024))) char smem[RING];
+  int tm, tn;
+  tile_coords(p, tm, tn);
+  float4_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+  const long m0 = (long)tm * BM, n0 = (long)tn * BN, z = blockIdx.z;
+  ring_mainloop_f32<BM, BN, WM, WN, TA, TB, NS>(p, m0, n0, z, (int)((p.K + 15) / 16), smem, acc);
+  static_assert(WM * 16 * (BN + 4) * 4 <= RING, "epilogue staging exceeds the ring");
+  store_tile_rows<BM, BN, WM, WN>(p, m0, n0, z, reinterpret_cast<float *>(smem), acc);
+}
+
 // ------------------------------------------------------------------ dispatch
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VEC>
 hipError_t launch_f16(GemmParams p, long batch, hipStream_t s) {
@@ -844,6 +1020,15 @@ hipError_t launch_f16_ring(GemmParams p, long batch, hipStream_t s) {
   p.tiles_n = (int)((p.N + BN - 1) / BN);
   dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
   hipLaunchKernelGGL((gemm_f16_ring_kernel<BM, BN, WM, WN, TA, TB, WPE, NS>), grid, dim3(WM * WN * 64), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int BM, int BN, int WM, int WN, bool TA, bool TB, int WPE = 2, int NS = 2>
+hipError_t launch_f32_ring(GemmParams p, long batch, hipStream_t s) {
+  p.tiles_m = (int)((p.M + BM - 1) / BM);
+  p.tiles_n = (int)((p.N + BN - 1) / BN);
+  dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
+  hipLaunchKernelGGL((gemm_f32_ring_kernel<BM, BN, WM, WN, TA, TB, WPE, NS>), grid, dim3(WM * WN * 64), 0, s, p);
   return hipGetLastError();
 }
 
@@ -898,9 +1083,18 @@ hipError_t pick_f32(const GemmParams &p, long batch, hipStream_t s) {
   if constexpr (!VEC) {
     return launch_f32<64, 64, 16, 2, 2, TA, TB, VEC>(p, batch, s);
   } else {
-    // 256 x 256 tiles with 16 waves of 64 x 64 once they fill the CUs (4096^3: 132-135
-    // TFLOP/s NN, 125-128 NT, against 125 / 120 for 128 x 128 tiles, measured).
+    // 256 x 256 tiles once they fill the CUs. The DMA ring (whole K-tile pairs, so K a
+    // multiple of 32) for NN, NT (2 x 4 waves of 128 x 64) and TT (4 x 2 waves of 64 x 128:
+    // its A fragments are the MN-contiguous ones, so they take the shorter wave side):
+    // 4096^3 NN 1020 -> 958 us, NT 1025 -> 944, TT 1023 -> 954, bit-identical. TN, both
+    // operands MN-contiguous, spills registers in either wave shape (1039 / 1074 us) and
+    // stays on the register-staged kernel with 16 waves of 64 x 64, as do K that are not
+    // multiples of 32 (4096^3: 132-135 TFLOP/s against 125 / 120 for 128 x 128 tiles).
     const long tiles256 = ((p.M + 255) / 256) * ((p.N + 255) / 256) * batch;
+    if (tiles256 >= 256 && p.K % 32 == 0 && ring_offsets_fit(p)) {
+      if constexpr (!TA) return launch_f32_ring<256, 256, 2, 4, TA, TB>(p, batch, s);
+      if constexpr (TA && TB) return launch_f32_ring<256, 256, 4, 2, TA, TB>(p, batch, s);
+    }
     if (tiles256 >= 256) return launch_f32<256, 256, 16, 4, 4, TA, TB, VEC>(p, batch, s);
     const long tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
     if (tiles128 >= 256) return launch_f32<128, 128, 32, 2, 2, TA, TB, VEC>(p, batch, s);

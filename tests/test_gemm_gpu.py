@@ -141,6 +141,62 @@ def test_f32_c2_4096_all_transposes(dev, tA, tB):
     assert np.isfinite(C).all()
 
 
+@pytest.mark.parametrize("K", [32, 96])
+def test_f32_ring_ragged_all_transposes_bit_identical(dev, K):
+    """fp32 shapes that fill the CUs with 256x256 tiles: the DMA ring for NN, NT and TT, the
+    register-staged kernel for TN. M and N are not multiples of 256 and K is one or three
+    32-deep K-tile pairs, so rows and columns past M, N must read as zeros and the pairs the
+    ring issues past the end of K must not be used. Every tile is checked (NaN start, row and
+    column sums), sampled rows against float64, and all four layouts agree bit for bit."""
+    import torch
+
+    rng = np.random.default_rng(K)
+    M, N = 4000, 4160
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    outs = []
+    for tA, tB in VARIANTS:
+        _say("f32 ring ragged", K, tA, tB)
+        ad = torch.from_numpy(_stored(A, tA)).to(dev)
+        bd = torch.from_numpy(_stored(B, tB)).to(dev)
+        cd = _nan_like(dev, M, N)
+        G.gemm(ad, bd, cd, transA=tA, transB=tB)
+        row_err, col_err = _sum_invariants(ad, bd, cd, tA, tB)
+        assert row_err <= 1e-5 and col_err <= 1e-5, (tA, tB, row_err, col_err)
+        outs.append(cd.cpu().numpy())
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])
+    rows = np.concatenate([np.arange(0, 8), rng.choice(M, 16, replace=False), np.arange(M - 8, M)])
+    err = O.rel_frob(outs[0][rows], O.gemm_f64_rows(A, B, rows))
+    _say("f32 ring ragged relFrob", K, err)
+    assert err <= 1e-5
+
+
+@pytest.mark.parametrize("tA,tB", [(False, True), (True, True)])
+def test_f32_ring_batched_alpha_beta_bias_act(dev, tA, tB):
+    """Batched strides and the alpha / beta / bias / GELU epilogue on the fp32 ring
+    (4 x 2048^2 x 128: 256 tiles of 256x256)."""
+    import torch
+
+    rng = np.random.default_rng(43)
+    bs, M, N, K = 4, 2048, 2048, 128
+    A = rng.standard_normal((bs, M, K)).astype(np.float32)
+    B = rng.standard_normal((bs, K, N)).astype(np.float32)
+    C0 = rng.standard_normal((bs, M, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    As = np.ascontiguousarray(A.transpose(0, 2, 1)) if tA else A
+    Bs = np.ascontiguousarray(B.transpose(0, 2, 1)) if tB else B
+    ad, bd = torch.from_numpy(As).to(dev), torch.from_numpy(Bs).to(dev)
+    C = torch.from_numpy(C0).to(dev)
+    G.gemm(ad, bd, C, transA=tA, transB=tB, batch=bs, strideA=M * K, strideB=K * N, strideC=M * N, alpha=0.5,
+           beta=0.25, bias=torch.from_numpy(bias).to(dev), act=G.ACT_GELU)
+    Cn = C.cpu().numpy()
+    rows = rng.choice(M, 12, replace=False)
+    for z in range(bs):
+        pre = 0.5 * O.gemm_f64_rows(A[z], B[z], rows) + 0.25 * C0[z][rows].astype(np.float64) + bias
+        assert O.rel_frob(Cn[z][rows], O.act_f64(G.ACT_GELU, pre)) <= 1e-5, z
+
+
 def test_f32_transpose_variants_bit_identical(dev):
     """All four load paths feed MFMA the same operands in the same order."""
     rng = np.random.default_rng(5)
