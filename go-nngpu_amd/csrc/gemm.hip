@@ -930,14 +930,17 @@ __device__ __forceinline__ void ring_mainloop_f32(const GemmParams &p, long m0, 
     return f;
   };
 
-  float4_t fa[2][FM], fb[2][FN];
+  constexpr int NSET = (TA && !TB) ? 1 : 2;
+  float4_t fa[NSET][FM], fb[NSET][FN];
   auto read_frags = [&](int slot, int h, int set) {
     const char *sa = smem + slot * SLOT + (TA ? h * OPA : 0);
     const char *sb = smem + slot * SLOT + 2 * OPA + (TB ? 0 : h * OPB);
 #pragma unroll
-    for (int i = 0; i < FM; ++i) fa[set][i] = TA ? frag_mn(sa, i, mna_e, mna_o, RBA) : frag_k(sa, wm * WTM + i * 16, h);
+    for (int i = 0; i < FM; ++i)
+      fa[set % NSET][i] = TA ? frag_mn(sa, i, mna_e, mna_o, RBA) : frag_k(sa, wm * WTM + i * 16, h);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) fb[set][j] = TB ? frag_k(sb, wn * WTN + j * 16, h) : frag_mn(sb, j, mnb_e, mnb_o, RBB);
+    for (int j = 0; j < FN; ++j)
+      fb[set % NSET][j] = TB ? frag_k(sb, wn * WTN + j * 16, h) : frag_mn(sb, j, mnb_e, mnb_o, RBB);
   };
   constexpr int NDS = (TA ? 4 : 1) * FM + (TB ? 1 : 4) * FN;  // LDS read instructions per K-tile
   auto mfma_set = [&](int set) {
@@ -947,9 +950,64 @@ __device__ __forceinline__ void ring_mainloop_f32(const GemmParams &p, long m0, 
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[set][i][s], fb[set][j][s], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[set % NSET][i][s], fb[set % NSET][j][s], acc[i][j], 0, 0, 0);
   };
 
+  if constexpr (TA && !TB) {
+    // Both operands MN-contiguous: one fragment set, refilled a component at a time. The
+    // step-s MFMAs of a K-tile are the last readers of component s, so the next K-tile's
+    // component s is read right after them (4 ds_read_b32 per fragment either way).
+    auto read_comp = [&](int slot, int h, int s) {
+      const char *sa = smem + slot * SLOT + h * OPA;
+      const char *sb = smem + slot * SLOT + 2 * OPA + h * OPB;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        fa[0][i][s] = *reinterpret_cast<const float *>(sa + ((i & 1) ? mna_o : mna_e) + 64 * i + s * RBA);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        fb[0][j][s] = *reinterpret_cast<const float *>(sb + ((j & 1) ? mnb_o : mnb_e) + 64 * j + s * RBB);
+    };
+    // The step-s MFMAs run beside the reads of the next K-tile's component s - 1, whose
+    // registers the step-(s-1) MFMAs have released; component 3 follows the last MFMAs.
+    auto step = [&](int slot_next, int h_next) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[0][i][s], fb[0][j][s], acc[i][j], 0, 0, 0);
+        if (s > 0) {
+          read_comp(slot_next, h_next, s - 1);
+          sched_interleave<FM * FN, FM + FN>();
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      read_comp(slot_next, h_next, 3);
+    };
+#pragma unroll
+    for (int q = 0; q < NS; ++q) issue(q, q);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 1) * LPW));
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 4; ++s) read_comp(0, 0, s);
+    int cur = 0, nxt = 1;
+    for (int pp = 0; pp < np; ++pp) {
+      __builtin_amdgcn_sched_barrier(0);
+      step(cur, 1);  // multiply K-tile 2pp, read 2pp+1 (same slot)
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * LPW));
+      __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+      issue(pp + NS, cur);
+      step(nxt, 0);  // multiply K-tile 2pp+1, read the next pair's first (past the last pair: zeros)
+      cur = nxt;
+      nxt = nxt + 1 == NS ? 0 : nxt + 1;
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __syncthreads();
+    return;
+  }
 #pragma unroll
   for (int q = 0; q < NS; ++q) issue(q, q);
   __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 1) * LPW));
@@ -1084,16 +1142,15 @@ hipError_t pick_f32(const GemmParams &p, long batch, hipStream_t s) {
     return launch_f32<64, 64, 16, 2, 2, TA, TB, VEC>(p, batch, s);
   } else {
     // 256 x 256 tiles once they fill the CUs. The DMA ring (whole K-tile pairs, so K a
-    // multiple of 32) for NN, NT (2 x 4 waves of 128 x 64) and TT (4 x 2 waves of 64 x 128:
-    // its A fragments are the MN-contiguous ones, so they take the shorter wave side):
-    // 4096^3 NN 1020 -> 958 us, NT 1025 -> 944, TT 1023 -> 954, bit-identical. TN, both
-    // operands MN-contiguous, spills registers in either wave shape (1039 / 1074 us) and
-    // stays on the register-staged kernel with 16 waves of 64 x 64, as do K that are not
-    // multiples of 32 (4096^3: 132-135 TFLOP/s against 125 / 120 for 128 x 128 tiles).
+    // multiple of 32): NN with 2 x 4 waves of 128 x 64; NT, TN and TT with 4 x 2 waves of
+    // 64 x 128 (an MN-contiguous A takes the shorter wave side; TN streams its fragments a
+    // component at a time). 4096^3, same box, bit-identical: NN 1014 -> 954 us, NT 1020 ->
+    // 942, TN 1010 -> 941, TT 1017 -> 949. Other K stay on the register-staged kernel with
+    // 16 waves of 64 x 64 (4096^3: 132-135 TFLOP/s against 125 / 120 for 128 x 128 tiles).
     const long tiles256 = ((p.M + 255) / 256) * ((p.N + 255) / 256) * batch;
     if (tiles256 >= 256 && p.K % 32 == 0 && ring_offsets_fit(p)) {
-      if constexpr (!TA) return launch_f32_ring<256, 256, 2, 4, TA, TB>(p, batch, s);
-      if constexpr (TA && TB) return launch_f32_ring<256, 256, 4, 2, TA, TB>(p, batch, s);
+      if constexpr (!TA && !TB) return launch_f32_ring<256, 256, 2, 4, TA, TB>(p, batch, s);
+      else return launch_f32_ring<256, 256, 4, 2, TA, TB>(p, batch, s);
     }
     if (tiles256 >= 256) return launch_f32<256, 256, 16, 4, 4, TA, TB, VEC>(p, batch, s);
     const long tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
