@@ -825,10 +825,12 @@ gemm_f16_ring_kernel(GemmParams p) {
 // as a 32-half fp16 K-tile), so K-contiguous tiles use the same 1 KiB chunks of 8 rows x
 // one K-tile pair (kc8 layout) and one ds_read_b128 per fragment gives lane (i, g) the
 // four k = 4g..4g+3 that MFMA steps s = 0..3 take. MN-contiguous tiles keep their k rows
-// (BM or BN floats, 512 or 1024 bytes) with the 16-byte block index XORed by
+// (BM or BN floats, 256 to 1024 bytes) with the 16-byte block index XORed by
 // msw32(k): the rows k and k + 4 that one 32-lane phase of a fragment read touches
 // (lane groups g = 0, 1 at step s) land 16 banks apart; each lane reads its four k
-// with ds_read_b32.
+// with ds_read_b32. Copies are whole 16-byte blocks checked by their first element, so
+// every contiguous extent (K of a K-contiguous operand, M or N of an MN-contiguous one)
+// must be a multiple of 4 floats, as the dispatch's vector path guarantees.
 __device__ __forceinline__ int msw32(int k) { return ((k >> 2) & 1) << 2; }
 
 template <int BM, int BN, int WM, int WN, bool TA, bool TB, int NS>
@@ -846,8 +848,8 @@ __device__ __forceinline__ void ring_mainloop_f32(const GemmParams &p, long m0, 
   constexpr int RBA = BM * 4, RBB = BN * 4;  // bytes of one k row of an MN-contiguous tile
   static_assert(CA % NW == 0 && CB % NW == 0 && IPA >= 1 && IPB >= 1, "DMA split");
   static_assert(NS >= 2 && (NS - 1) * LPW < 64, "ring slots within the vmcnt range");
-  static_assert((!TA || RBA == 512 || RBA == 1024) && (TB || RBB == 512 || RBB == 1024),
-                "MN-contiguous k rows of 128 or 256 floats");
+  static_assert((!TA || RBA == 256 || RBA == 512 || RBA == 1024) && (TB || RBB == 256 || RBB == 512 || RBB == 1024),
+                "MN-contiguous k rows of 64, 128 or 256 floats");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int wm = wave / WN, wn = wave % WN;
@@ -1141,20 +1143,32 @@ hipError_t pick_f32(const GemmParams &p, long batch, hipStream_t s) {
   if constexpr (!VEC) {
     return launch_f32<64, 64, 16, 2, 2, TA, TB, VEC>(p, batch, s);
   } else {
-    // 256 x 256 tiles once they fill the CUs. The DMA ring (whole K-tile pairs, so K a
-    // multiple of 32): NN with 2 x 4 waves of 128 x 64; NT, TN and TT with 4 x 2 waves of
-    // 64 x 128 (an MN-contiguous A takes the shorter wave side; TN streams its fragments a
-    // component at a time). 4096^3, same box, bit-identical: NN 1014 -> 954 us, NT 1020 ->
-    // 942, TN 1010 -> 941, TT 1017 -> 949. Other K stay on the register-staged kernel with
-    // 16 waves of 64 x 64 (4096^3: 132-135 TFLOP/s against 125 / 120 for 128 x 128 tiles).
+    // The DMA ring whenever K is a multiple of 32 (whole K-tile pairs), at the largest tile
+    // that still gives 256 tiles, else 64 x 64; the vector path's alignment (every
+    // contiguous extent a multiple of 4 floats) keeps its 16-byte copies inside the operands.
+    //  * 256 x 256: NN with 2 x 4 waves of 128 x 64; NT, TN and TT with 4 x 2 waves of 64 x 128
+    //    (an MN-contiguous A takes the shorter wave side; TN streams its fragments a component
+    //    at a time). 4096^3, same box, bit-identical: NN 1014 -> 954 us, NT 1020 -> 942, TN
+    //    1010 -> 941, TT 1017 -> 949;
+    //  * 128 x 128, 2 x 2 waves, two workgroups per CU: 2048^3 154-165 -> 131-136 us;
+    //  * 64 x 64, 2 x 2 waves: 1024^3 35 -> 23-25 us, 512^3 18.5 -> 12 us, 256^3 10.8 -> 7.7 us.
+    // Other K take the register-staged kernel with the same tile choice (256 x 256 with 16
+    // waves of 64 x 64: 4096^3 132-135 TFLOP/s against 125 / 120 for 128 x 128 tiles).
+    const bool ring = p.K % 32 == 0 && ring_offsets_fit(p);
     const long tiles256 = ((p.M + 255) / 256) * ((p.N + 255) / 256) * batch;
-    if (tiles256 >= 256 && p.K % 32 == 0 && ring_offsets_fit(p)) {
-      if constexpr (!TA && !TB) return launch_f32_ring<256, 256, 2, 4, TA, TB>(p, batch, s);
-      else return launch_f32_ring<256, 256, 4, 2, TA, TB>(p, batch, s);
+    if (tiles256 >= 256) {
+      if (ring) {
+        if constexpr (!TA && !TB) return launch_f32_ring<256, 256, 2, 4, TA, TB>(p, batch, s);
+        else return launch_f32_ring<256, 256, 4, 2, TA, TB>(p, batch, s);
+      }
+      return launch_f32<256, 256, 16, 4, 4, TA, TB, VEC>(p, batch, s);
     }
-    if (tiles256 >= 256) return launch_f32<256, 256, 16, 4, 4, TA, TB, VEC>(p, batch, s);
     const long tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
-    if (tiles128 >= 256) return launch_f32<128, 128, 32, 2, 2, TA, TB, VEC>(p, batch, s);
+    if (tiles128 >= 256) {
+      if (ring) return launch_f32_ring<128, 128, 2, 2, TA, TB>(p, batch, s);
+      return launch_f32<128, 128, 32, 2, 2, TA, TB, VEC>(p, batch, s);
+    }
+    if (ring) return launch_f32_ring<64, 64, 2, 2, TA, TB>(p, batch, s);
     return launch_f32<64, 64, 16, 2, 2, TA, TB, VEC>(p, batch, s);
   }
 }

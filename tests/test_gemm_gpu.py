@@ -172,6 +172,49 @@ def test_f32_ring_ragged_all_transposes_bit_identical(dev, K):
     assert err <= 1e-5
 
 
+@pytest.mark.parametrize("M,N,K", [(2000, 2100, 96), (300, 500, 64), (68, 132, 96), (4, 4, 32)])
+def test_f32_ring_small_tiles_all_transposes_bit_identical(dev, M, N, K):
+    """The fp32 ring at 128x128 tiles (>= 256 of them: 2000 x 2100) and 64x64 tiles (fewer),
+    ragged M, N and K of one or three 32-deep K-tile pairs: NaN start, row and column sums,
+    rows against float64, and all four layouts bit for bit."""
+    import torch
+
+    rng = np.random.default_rng(M + N + K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    outs = []
+    for tA, tB in VARIANTS:
+        _say("f32 ring small tiles", M, N, K, tA, tB)
+        ad = torch.from_numpy(_stored(A, tA)).to(dev)
+        bd = torch.from_numpy(_stored(B, tB)).to(dev)
+        cd = _nan_like(dev, M, N)
+        G.gemm(ad, bd, cd, transA=tA, transB=tB)
+        row_err, col_err = _sum_invariants(ad, bd, cd, tA, tB)
+        assert row_err <= 1e-5 and col_err <= 1e-5, (tA, tB, row_err, col_err)
+        outs.append(cd.cpu().numpy())
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])
+    rows = np.unique(np.concatenate([np.arange(0, min(M, 6)), rng.choice(M, min(M, 10), replace=False),
+                                     np.arange(max(0, M - 6), M)]))
+    assert O.rel_frob(outs[0][rows], O.gemm_f64_rows(A, B, rows)) <= 1e-5
+
+
+def test_f32_ring_small_tiles_batched(dev):
+    """Batched strides on the 64x64 fp32 ring (3 x 128^2 x 64: 12 tiles)."""
+    import torch
+
+    rng = np.random.default_rng(47)
+    bs, M, N, K = 3, 128, 128, 64
+    A = rng.standard_normal((bs, M, K)).astype(np.float32)
+    B = rng.standard_normal((bs, K, N)).astype(np.float32)
+    C = torch.full((bs, M, N), float("nan"), dtype=torch.float32, device=dev)
+    G.gemm(torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev), C, batch=bs, strideA=M * K, strideB=K * N,
+           strideC=M * N)
+    Cn = C.cpu().numpy()
+    for z in range(bs):
+        assert O.rel_frob(Cn[z], A[z].astype(np.float64) @ B[z]) <= 1e-5, z
+
+
 @pytest.mark.parametrize("tA,tB", [(False, True), (True, True)])
 def test_f32_ring_batched_alpha_beta_bias_act(dev, tA, tB):
     """Batched strides and the alpha / beta / bias / GELU epilogue on the fp32 ring
