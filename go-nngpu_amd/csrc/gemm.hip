@@ -856,11 +856,11 @@ __device__ __forceinline__ void ring_mainloop_f32(const GemmParams &p, long m0, 
 
   BufRsrc ra, rb;
   unsigned voa[IPA], vob[IPB];
-  // Lane offset of chunk c and the k (0..2 BK - 1 within the pair) it covers.
-  auto plan = [&](bool kcontig, int c, int nchunks, int rb_bytes, long ld, long lim, unsigned &vo, int &kl) {
+  // Byte offset (from the pair's start) of this lane's 16-byte copy in chunk c; rows or
+  // columns past M (or N) get the out-of-range offset.
+  auto plan = [&](bool kcontig, int c, int nchunks, int rb_bytes, long ld, long lim, unsigned &vo) {
     if (kcontig) {  // chunk c: rows 8c..8c+7, the pair's 32 k (128 bytes) each
       const int row = 8 * c + (lane >> 3), q = kc8_octet(row, lane & 7);
-      kl = 4 * q;
       vo = lim > row ? (unsigned)((long)row * ld * 4 + 16 * q) : kOutOfRange;
       return;
     }
@@ -869,7 +869,6 @@ __device__ __forceinline__ void ring_mainloop_f32(const GemmParams &p, long m0, 
     const int h = c / (nchunks / 2), cl = c % (nchunks / 2);
     const int bpr = rb_bytes / 16;
     const int k = cl * (1024 / rb_bytes) + lane / bpr, b = (lane % bpr) ^ msw32(k);
-    kl = BK * h + k;
     vo = lim > 4 * b ? (unsigned)((long)(BK * h + k) * ld * 4 + 16 * b) : kOutOfRange;
   };
   {
@@ -878,13 +877,10 @@ __device__ __forceinline__ void ring_mainloop_f32(const GemmParams &p, long m0, 
     ra = make_rsrc(TA ? A + m0 : A + m0 * p.lda);
     rb = make_rsrc(TB ? B + n0 * p.ldb : B + n0);
   }
-  {
-    int kl;
 #pragma unroll
-    for (int i = 0; i < IPA; ++i) plan(!TA, wave * IPA + i, CA, RBA, p.lda, p.M - m0, voa[i], kl);
+  for (int i = 0; i < IPA; ++i) plan(!TA, wave * IPA + i, CA, RBA, p.lda, p.M - m0, voa[i]);
 #pragma unroll
-    for (int i = 0; i < IPB; ++i) plan(TB, wave * IPB + i, CB, RBB, p.ldb, p.N - n0, vob[i], kl);
-  }
+  for (int i = 0; i < IPB; ++i) plan(TB, wave * IPB + i, CB, RBB, p.ldb, p.N - n0, vob[i]);
   const long a_step = TA ? 2L * BK * p.lda * 4 : 2L * BK * 4;
   const long b_step = TB ? 2L * BK * 4 : 2L * BK * p.ldb * 4;
   const unsigned sbase = lds_offset(smem);
