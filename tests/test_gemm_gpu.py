@@ -199,6 +199,31 @@ def test_f32_ring_small_tiles_all_transposes_bit_identical(dev, M, N, K):
     assert O.rel_frob(outs[0][rows], O.gemm_f64_rows(A, B, rows)) <= 1e-5
 
 
+@pytest.mark.parametrize("M,N,K,pad", [(300, 500, 64, 4), (2000, 2100, 32, 8)])
+def test_f32_ring_padded_leading_dims(dev, M, N, K, pad):
+    """Leading dimensions wider than the rows (views into wider buffers, still 16-byte
+    aligned) on the fp32 ring, all four layouts: the copies step by lda / ldb, not by the
+    logical extent, and the columns past the view are never read."""
+    import torch
+
+    rng = np.random.default_rng(M + pad)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    ref_rows = np.unique(np.concatenate([np.arange(0, 6), rng.choice(M, 10, replace=False), np.arange(M - 6, M)]))
+    ref = O.gemm_f64_rows(A, B, ref_rows)
+    for tA, tB in VARIANTS:
+        As, Bs = _stored(A, tA), _stored(B, tB)
+        aw = torch.full((As.shape[0], As.shape[1] + pad), float("nan"), dtype=torch.float32, device=dev)
+        bw = torch.full((Bs.shape[0], Bs.shape[1] + pad), float("nan"), dtype=torch.float32, device=dev)
+        aw[:, :As.shape[1]] = torch.from_numpy(As).to(dev)
+        bw[:, :Bs.shape[1]] = torch.from_numpy(Bs).to(dev)
+        cd = _nan_like(dev, M, N)
+        G.gemm(aw[:, :As.shape[1]], bw[:, :Bs.shape[1]], cd, transA=tA, transB=tB)
+        C = cd.cpu().numpy()
+        assert np.isfinite(C).all(), (tA, tB)
+        assert O.rel_frob(C[ref_rows], ref) <= 1e-5, (tA, tB)
+
+
 def test_f32_ring_small_tiles_batched(dev):
     """Batched strides on the 64x64 fp32 ring (3 x 128^2 x 64: 12 tiles)."""
     import torch
