@@ -888,20 +888,33 @@ __device__ __forceinline__ void ring_mainloop_f32(const GemmParams &p, long m0, 
 
   // The caller guarantees K % (2 BK) == 0, so a pair is either whole or past the end of
   // K. Pairs past the end (the ring refills of the last NS steps, and the prologue's when
-  // np < NS) still issue their LPW copies, which the vmcnt waits count, but with the
-  // out-of-range offset: they read zeros and touch no memory.
-  auto issue = [&](int pp, int slot) {
+  // np < NS) still issue their LPW copies, which the vmcnt waits count, but through
+  // descriptors with num_records 0: every offset is out of range, so they read zeros and
+  // touch no memory. (A wave-uniform switch: per-lane offset selects would need temporary
+  // VGPRs beside the fragments.)
+  // Part q of NQ issues the wave's copies d (A's IPA, then B's IPB) with d * NQ / LPW == q;
+  // the last part advances both descriptors.
+  auto issue_part = [&](int pp, int slot, int q, int NQ) {
     const bool live = pp < np;
+    BufRsrc da = ra, db = rb;
+    if (!live) {
+      da.r.z = 0;
+      db.r.z = 0;
+    }
     const unsigned st = sbase + (unsigned)(slot * SLOT);
 #pragma unroll
     for (int i = 0; i < IPA; ++i)
-      dma16(ra, live ? voa[i] : kOutOfRange, __builtin_amdgcn_readfirstlane(st + (wave * IPA + i) * 1024));
+      if (i * NQ / LPW == q) dma16(da, voa[i], __builtin_amdgcn_readfirstlane(st + (wave * IPA + i) * 1024));
 #pragma unroll
     for (int i = 0; i < IPB; ++i)
-      dma16(rb, live ? vob[i] : kOutOfRange, __builtin_amdgcn_readfirstlane(st + 2 * OPA + (wave * IPB + i) * 1024));
-    rsrc_advance(ra, a_step);
-    rsrc_advance(rb, b_step);
+      if ((IPA + i) * NQ / LPW == q)
+        dma16(db, vob[i], __builtin_amdgcn_readfirstlane(st + 2 * OPA + (wave * IPB + i) * 1024));
+    if (q == NQ - 1) {
+      rsrc_advance(ra, a_step);
+      rsrc_advance(rb, b_step);
+    }
   };
+  auto issue = [&](int pp, int slot) { issue_part(pp, slot, 0, 1); };
 
   // K-contiguous: rows row0..row0+15 of K-tile h; MN-contiguous: columns col0..col0+15.
   auto frag_k = [&](const char *base, int row0, int h) -> float4_t {
@@ -930,25 +943,32 @@ __device__ __forceinline__ void ring_mainloop_f32(const GemmParams &p, long m0, 
 
   constexpr int NSET = (TA && !TB) ? 1 : 2;
   float4_t fa[NSET][FM], fb[NSET][FN];
-  auto read_frags = [&](int slot, int h, int set) {
+  // Part q of NQ reads the fragments i (of A) and j (of B) with i * NQ / FM == q and
+  // j * NQ / FN == q.
+  auto read_frags_part = [&](int slot, int h, int set, int q, int NQ) {
     const char *sa = smem + slot * SLOT + (TA ? h * OPA : 0);
     const char *sb = smem + slot * SLOT + 2 * OPA + (TB ? 0 : h * OPB);
 #pragma unroll
     for (int i = 0; i < FM; ++i)
-      fa[set % NSET][i] = TA ? frag_mn(sa, i, mna_e, mna_o, RBA) : frag_k(sa, wm * WTM + i * 16, h);
+      if (i * NQ / FM == q)
+        fa[set % NSET][i] = TA ? frag_mn(sa, i, mna_e, mna_o, RBA) : frag_k(sa, wm * WTM + i * 16, h);
 #pragma unroll
     for (int j = 0; j < FN; ++j)
-      fb[set % NSET][j] = TB ? frag_k(sb, wn * WTN + j * 16, h) : frag_mn(sb, j, mnb_e, mnb_o, RBB);
+      if (j * NQ / FN == q)
+        fb[set % NSET][j] = TB ? frag_k(sb, wn * WTN + j * 16, h) : frag_mn(sb, j, mnb_e, mnb_o, RBB);
   };
+  auto read_frags = [&](int slot, int h, int set) { read_frags_part(slot, h, set, 0, 1); };
   constexpr int NDS = (TA ? 4 : 1) * FM + (TB ? 1 : 4) * FN;  // LDS read instructions per K-tile
+  auto mfma_step = [&](int set, int s) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[set % NSET][i][s], fb[set % NSET][j][s], acc[i][j], 0, 0, 0);
+  };
   auto mfma_set = [&](int set) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[set % NSET][i][s], fb[set % NSET][j][s], acc[i][j], 0, 0, 0);
+    for (int s = 0; s < 4; ++s) mfma_step(set, s);
   };
 
   if constexpr (TA && !TB) {
@@ -967,9 +987,10 @@ __device__ __forceinline__ void ring_mainloop_f32(const GemmParams &p, long m0, 
     };
     // The step-s MFMAs run beside the reads of the next K-tile's component s - 1, whose
     // registers the step-(s-1) MFMAs have released; component 3 follows the last MFMAs.
-    auto step = [&](int slot_next, int h_next) {
+    auto step = [&](int slot_next, int h_next, int refill_pp, int refill_slot) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
+        if (refill_pp >= 0) issue_part(refill_pp, refill_slot, s, 4);
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -992,13 +1013,14 @@ __device__ __forceinline__ void ring_mainloop_f32(const GemmParams &p, long m0, 
     int cur = 0, nxt = 1;
     for (int pp = 0; pp < np; ++pp) {
       __builtin_amdgcn_sched_barrier(0);
-      step(cur, 1);  // multiply K-tile 2pp, read 2pp+1 (same slot)
+      step(cur, 1, -1, 0);  // multiply K-tile 2pp, read 2pp+1 (same slot)
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * LPW));
       __syncthreads();
       __builtin_amdgcn_sched_barrier(0);
-      issue(pp + NS, cur);
-      step(nxt, 0);  // multiply K-tile 2pp+1, read the next pair's first (past the last pair: zeros)
+      // multiply K-tile 2pp+1 and read the next pair's first (past the last pair: zeros),
+      // refilling this pair's slot with pair pp + NS a quarter per MFMA step
+      step(nxt, 0, pp + NS, cur);
       cur = nxt;
       nxt = nxt + 1 == NS ? 0 : nxt + 1;
     }
@@ -1020,11 +1042,20 @@ __device__ __forceinline__ void ring_mainloop_f32(const GemmParams &p, long m0, 
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * LPW));
     __syncthreads();
+    // The odd step in four parts, one per MFMA step: a quarter of the refill of this
+    // pair's slot with pair pp + NS, a quarter of the next pair's first fragments, and the
+    // step's MFMAs. Issued together after the barrier, the refill's copies held back every
+    // wave's MFMAs while the CU's address unit took them in (4096^3 NN 952 -> 921 us, NT
+    // 940 -> 908 us spread this way).
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue_part(pp + NS, cur, q, 4);
+      read_frags_part(nxt, 0, 0, q, 4);
+      mfma_step(1, q);
+      sched_interleave<FM * FN, NDS / 4>();
+    }
     __builtin_amdgcn_sched_barrier(0);
-    issue(pp + NS, cur);
-    read_frags(nxt, 0, 0);
-    mfma_set(1);
-    sched_interleave<4 * FM * FN, NDS>();
     cur = nxt;
     nxt = nxt + 1 == NS ? 0 : nxt + 1;
   }
