@@ -776,15 +776,34 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
       // after 1/2 for NT / TN / TT (3/4 cost them 1-1.5%).
       constexpr int R0 = (!TA && !TB) ? 3 * FM / 4 : FM / 2;
       constexpr int NRH = (TA ? 2 : 1) * (FM / 2) + (TB ? 1 : 2) * (FN / 2);  // reads per part
-      issue(pp + NS, cur, 0, 2);
-      read_part(nxt, 0, 0, 0, 2);
-      mfma_rows(1, 0, R0);
-      sched_interleave<R0 * FN, NRH>();
-      __builtin_amdgcn_sched_barrier(0);
-      issue(pp + NS, cur, 1, 2);
-      read_part(nxt, 0, 0, 1, 2);
-      mfma_rows(1, R0, FM);
-      sched_interleave<(FM - R0) * FN, NRH>();
+      if constexpr (FM >= 8) {
+        // Each burst follows the first MFMA row of its region, so the SIMD's MFMA pipe has
+        // work while the CU's address unit takes the copies in (8192^3: NT 831 -> 821, TN
+        // 845 -> 835, TT 848 -> 837, NN 835 -> 832 us; the 4-row C4 tiles lost 3% with it).
+        mfma_rows(1, 0, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(pp + NS, cur, 0, 2);
+        read_part(nxt, 0, 0, 0, 2);
+        mfma_rows(1, 1, R0);
+        sched_interleave<(R0 - 1) * FN, NRH>();
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_rows(1, R0, R0 + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(pp + NS, cur, 1, 2);
+        read_part(nxt, 0, 0, 1, 2);
+        mfma_rows(1, R0 + 1, FM);
+        sched_interleave<(FM - R0 - 1) * FN, NRH>();
+      } else {
+        issue(pp + NS, cur, 0, 2);
+        read_part(nxt, 0, 0, 0, 2);
+        mfma_rows(1, 0, R0);
+        sched_interleave<R0 * FN, NRH>();
+        __builtin_amdgcn_sched_barrier(0);
+        issue(pp + NS, cur, 1, 2);
+        read_part(nxt, 0, 0, 1, 2);
+        mfma_rows(1, R0, FM);
+        sched_interleave<(FM - R0) * FN, NRH>();
+      }
     } else {
       issue(pp + NS, cur, 0, 2);
       issue(pp + NS, cur, 1, 2);
