@@ -869,6 +869,9 @@ __device__ __forceinline__ void ring_mainloop_f32(const GemmParams &p, long m0, 
   static_assert(NS >= 2 && (NS - 1) * LPW < 64, "ring slots within the vmcnt range");
   static_assert((!TA || RBA == 256 || RBA == 512 || RBA == 1024) && (TB || RBB == 256 || RBB == 512 || RBB == 1024),
                 "MN-contiguous k rows of 64, 128 or 256 floats");
+  // mn_bases folds the swizzle into fragment j's parity, which holds when a wave's first
+  // column (or row) of an MN-contiguous operand starts a 32-float group.
+  static_assert((!TA || WTM % 32 == 0) && (TB || WTN % 32 == 0), "MN-contiguous wave offsets in 32-float groups");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int wm = wave / WN, wn = wave % WN;
@@ -1189,32 +1192,47 @@ hipError_t pick_f32(const GemmParams &p, long batch, hipStream_t s) {
   if constexpr (!VEC) {
     return launch_f32<64, 64, 16, 2, 2, TA, TB, VEC>(p, batch, s);
   } else {
-    // The DMA ring whenever K is a multiple of 32 (whole K-tile pairs), at the largest tile
-    // that still gives 256 tiles, else 64 x 64; the vector path's alignment (every
-    // contiguous extent a multiple of 4 floats) keeps its 16-byte copies inside the operands.
-    //  * 256 x 256: NN with 2 x 4 waves of 128 x 64; NT, TN and TT with 4 x 2 waves of 64 x 128
-    //    (an MN-contiguous A takes the shorter wave side; TN streams its fragments a component
-    //    at a time). 4096^3, same box, bit-identical: NN 1014 -> 954 us, NT 1020 -> 942, TN
-    //    1010 -> 941, TT 1017 -> 949;
-    //  * 128 x 128, 2 x 2 waves, two workgroups per CU: 2048^3 154-165 -> 131-136 us;
-    //  * 64 x 64, 2 x 2 waves: 1024^3 35 -> 23-25 us, 512^3 18.5 -> 12 us, 256^3 10.8 -> 7.7 us.
-    // Other K take the register-staged kernel with the same tile choice (256 x 256 with 16
-    // waves of 64 x 64: 4096^3 132-135 TFLOP/s against 125 / 120 for 128 x 128 tiles).
+    // The DMA ring whenever K is a multiple of 32 (whole K-tile pairs); the vector path's
+    // alignment (every contiguous extent a multiple of 4 floats) keeps its 16-byte copies
+    // inside the operands. Tiles:
+    //  * 256 x 256, 8 waves, one workgroup per CU: NN with 2 x 4 waves of 128 x 64; NT, TN and
+    //    TT with 4 x 2 waves of 64 x 128 (an MN-contiguous A takes the shorter wave side; TN
+    //    streams its fragments a component at a time);
+    //  * 128 x 128: 8 waves (2 x 4, or 4 x 2 for a K-contiguous B) when one round holds every
+    //    tile, else 4 waves with two workgroups per CU;
+    //  * 64 x 64, 4 waves, up to five workgroups per CU.
+    // Each candidate's time is modelled as its rounds (ceil(tiles / 256), the CU count) times
+    // the tile's area over the tile's per-CU efficiency with the CU kept busy. The efficiencies
+    // are fits to n^3 problems from 2048 to 6144 in all four layouts (256: 0.95; 128: 0.93,
+    // 0.89 for a single round of 8-wave tiles; 64: 0.88), and the model picks the measured
+    // best at every size tried: 64 x 64 at 2560..5120 (5120^3: 1920 us against 2040 for 128 x
+    // 128 and 2302 for 256 x 256), 128 x 128 at 2048 and 6144 (3145 us against 3269 and
+    // 4155), 256 x 256 at 4096 and 8192.
+    // Other K take the register-staged kernel with the largest tile that still gives 256 tiles
+    // (256 x 256 with 16 waves of 64 x 64: 4096^3 132-135 TFLOP/s against 125 / 120 for 128 x
+    // 128 tiles).
     const bool ring = p.K % 32 == 0 && ring_offsets_fit(p);
     const long tiles256 = ((p.M + 255) / 256) * ((p.N + 255) / 256) * batch;
-    if (tiles256 >= 256) {
-      if (ring) {
+    const long tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
+    if (ring) {
+      const long tiles64 = ((p.M + 63) / 64) * ((p.N + 63) / 64) * batch;
+      auto cost = [](long tiles, double area, double eff) { return (double)((tiles + 255) / 256) * area / eff; };
+      const double c256 = cost(tiles256, 256.0 * 256.0, 0.95);
+      const double c128 = cost(tiles128, 128.0 * 128.0, tiles128 <= 256 ? 0.89 : 0.93);
+      const double c64 = cost(tiles64, 64.0 * 64.0, 0.88);
+      if (c256 <= c128 && c256 <= c64) {
         if constexpr (!TA && !TB) return launch_f32_ring<256, 256, 2, 4, TA, TB>(p, batch, s);
         else return launch_f32_ring<256, 256, 4, 2, TA, TB>(p, batch, s);
       }
-      return launch_f32<256, 256, 16, 4, 4, TA, TB, VEC>(p, batch, s);
+      if (c128 <= c64) {
+        if (tiles128 > 256) return launch_f32_ring<128, 128, 2, 2, TA, TB>(p, batch, s);
+        if constexpr (TB) return launch_f32_ring<128, 128, 4, 2, TA, TB>(p, batch, s);
+        else return launch_f32_ring<128, 128, 2, 4, TA, TB>(p, batch, s);
+      }
+      return launch_f32_ring<64, 64, 2, 2, TA, TB>(p, batch, s);
     }
-    const long tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
-    if (tiles128 >= 256) {
-      if (ring) return launch_f32_ring<128, 128, 2, 2, TA, TB>(p, batch, s);
-      return launch_f32<128, 128, 32, 2, 2, TA, TB, VEC>(p, batch, s);
-    }
-    if (ring) return launch_f32_ring<64, 64, 2, 2, TA, TB>(p, batch, s);
+    if (tiles256 >= 256) return launch_f32<256, 256, 16, 4, 4, TA, TB, VEC>(p, batch, s);
+    if (tiles128 >= 256) return launch_f32<128, 128, 32, 2, 2, TA, TB, VEC>(p, batch, s);
     return launch_f32<64, 64, 16, 2, 2, TA, TB, VEC>(p, batch, s);
   }
 }

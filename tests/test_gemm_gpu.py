@@ -143,15 +143,15 @@ def test_f32_c2_4096_all_transposes(dev, tA, tB):
 
 @pytest.mark.parametrize("K", [32, 96])
 def test_f32_ring_ragged_all_transposes_bit_identical(dev, K):
-    """fp32 shapes that fill the CUs with 256x256 tiles: the DMA ring for NN, NT and TT, the
-    register-staged kernel for TN. M and N are not multiples of 256 and K is one or three
-    32-deep K-tile pairs, so rows and columns past M, N must read as zeros and the pairs the
-    ring issues past the end of K must not be used. Every tile is checked (NaN start, row and
-    column sums), sampled rows against float64, and all four layouts agree bit for bit."""
+    """fp32 shapes that fill the CUs with one round of 256x256 ring tiles (16 x 16 of them). M
+    and N are not multiples of 256 and K is one or three 32-deep K-tile pairs, so rows and
+    columns past M, N must read as zeros and the pairs the ring issues past the end of K must
+    not be used. Every tile is checked (NaN start, row and column sums), sampled rows against
+    float64, and all four layouts agree bit for bit."""
     import torch
 
     rng = np.random.default_rng(K)
-    M, N = 4000, 4160
+    M, N = 4000, 4000
     A = rng.standard_normal((M, K)).astype(np.float32)
     B = rng.standard_normal((K, N)).astype(np.float32)
     outs = []
@@ -172,11 +172,13 @@ def test_f32_ring_ragged_all_transposes_bit_identical(dev, K):
     assert err <= 1e-5
 
 
-@pytest.mark.parametrize("M,N,K", [(2000, 2100, 96), (300, 500, 64), (68, 132, 96), (4, 4, 32)])
+@pytest.mark.parametrize("M,N,K", [(2000, 2010, 96), (2000, 4000, 96), (2000, 2100, 96), (300, 500, 64), (68, 132, 96),
+                                   (4, 4, 32)])
 def test_f32_ring_small_tiles_all_transposes_bit_identical(dev, M, N, K):
-    """The fp32 ring at 128x128 tiles (>= 256 of them: 2000 x 2100) and 64x64 tiles (fewer),
-    ragged M, N and K of one or three 32-deep K-tile pairs: NaN start, row and column sums,
-    rows against float64, and all four layouts bit for bit."""
+    """The fp32 ring's smaller tiles with ragged M, N and K of one or three 32-deep K-tile
+    pairs: 128x128 with 8 waves (2000 x 2010: 256 tiles, one round), 128x128 with 4 waves
+    (2000 x 4000: 512 tiles, two per CU), 64x64 (the other shapes; 2000 x 2100 has 1056 of
+    them). NaN start, row and column sums, rows against float64, all four layouts bit for bit."""
     import torch
 
     rng = np.random.default_rng(M + N + K)
