@@ -1152,36 +1152,57 @@ hipError_t pick_f16(const GemmParams &p, long batch, hipStream_t s) {
     return launch_f16<64, 64, 64, 2, 2, TA, TB, VEC>(p, batch, s);
   } else {
     const long tiles256 = ((p.M + 255) / 256) * ((p.N + 255) / 256) * batch;
-    if (tiles256 >= 256 && ring_offsets_fit(p)) return launch_f16_ring<256, 256, 2, 4, TA, TB>(p, batch, s);
-    if (tiles256 >= 512) return launch_f16<256, 256, 64, 2, 4, TA, TB, VEC>(p, batch, s);
     const long tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
     if (tiles128 >= 128 && ring_offsets_fit(p)) {
+      // The ring kernel's tile from a time model. A round is 256 tiles (one per CU) for the
+      // one-workgroup-per-CU tiles (256x256 and 128x192, 8 waves; 128x128 with 8 waves when
+      // one round holds every tile) and 512 for the two-per-CU ones (128x128 and 128x96, 4
+      // waves). Each tile type takes a measured time per round, relative to a round of
+      // 256x256 tiles at the same K: 128x192 0.509, 128x128 8-wave 0.508; two co-resident
+      // 128x128 0.638 (0.52 for one alone), 128x96 0.542 (0.43 alone, estimated). A last,
+      // partial round costs its fill fraction but at least 0.75 of a full one: with fewer
+      // CUs busy the power-limited clock rises (3072^3: 144 tiles of 256x256 on 256 CUs take
+      // 0.75 of a full round's time), so a 256x256 round that is half full still beats twice
+      // the 128x128 tiles. The model picks the measured best of these tiles at n^3 from 1536
+      // to 6144 and at M x 11008 x 4096 for M = 512..2048, NT and TT (3072^3: 63 us against
+      // 82 us for the earlier 128x128 choice; 1536 x 11008 x 4096 NT: 147 us against 179 us
+      // for 256x256; the 512 x 11008 x 4096 linear layer: 128x192).
+      auto one = [](long t, double r) {
+        const long u = t % 256;
+        return (double)(t / 256) * r + (u ? r * fmax(0.75, u / 256.0) : 0.0);
+      };
+      auto two = [](long t, double r2, double r1) {
+        const long u = t % 512;
+        return (double)(t / 512) * r2 +
+               (u == 0 ? 0.0 : u <= 256 ? r1 * fmax(0.75, u / 256.0) : r2 * fmax(0.75, u / 512.0));
+      };
+      double best = one(tiles256, 1.0);
+      int pick = 0;
+      const double c128 = tiles128 <= 256 ? one(tiles128, 0.508) : two(tiles128, 0.638, 0.52);
+      if (c128 < best) best = c128, pick = 1;
       if constexpr (TB) {
-        // 128 x 192 tiles, 8 waves, one workgroup per CU and a ring of three K-tile pairs
-        // (120 KiB): two pairs in flight instead of one. When they fill at least 3/4 of the
-        // CUs in as many rounds as two co-resident 128 x 96 workgroups per CU would take,
-        // they win by the deeper prefetch (the 512 x 11008 x 4096 linear layer, 232 tiles:
-        // 49.0 -> 46.9 us ReLU, 51.0 -> 47.9 us GELU on one box, 50.1 -> 49.1 / 52.8 -> 50.5 on
-        // another). Only for a K-contiguous B: 384-byte MN-contiguous rows would not take the
-        // 32-byte block swizzle of the transposing reads.
+        // 128 x 192 and 128 x 96 only for a K-contiguous B: 384- and 192-byte MN-contiguous
+        // rows would not take the 32-byte block swizzle of the transposing reads.
         const long tiles192 = ((p.M + 127) / 128) * ((p.N + 191) / 192) * batch;
-        const long tiles96x = ((p.M + 127) / 128) * ((p.N + 95) / 96) * batch;
-        if (tiles192 >= 192 && (tiles192 + 255) / 256 <= (tiles96x + 511) / 512)
-          return launch_f16_ring<128, 192, 2, 4, TA, TB, 2, 3>(p, batch, s);
-        // Two workgroups of these tiles share a CU, so the CU holding the most tiles
-        // needs ceil(ceil(tiles / 256) / 2) rounds. 128x96 tiles (a K-contiguous B
-        // allows N-tiles of 96) run at ~0.85x the per-CU rate of 128x128 and often
-        // need fewer rounds per unit of work: the 512 x 11008 linear layer takes
-        // 460 tiles of 128x96 in one round (55 us) against 344 of 128x128 (60 us);
-        // at 4096^3 (1376 against 1024 tiles) 128x128 wins.
-        auto rounds = [](long t) { return (double)(((t + 255) / 256 + 1) / 2); };
         const long tiles96 = ((p.M + 127) / 128) * ((p.N + 95) / 96) * batch;
-        const double c128 = rounds(tiles128) * (128.0 * 128.0);
-        const double c96 = rounds(tiles96) * (128.0 * 96.0) / 0.85;
-        if (c96 < c128) return launch_f16_ring<128, 96, 2, 2, TA, TB>(p, batch, s);
+        const double c192 = one(tiles192, 0.509), c96 = two(tiles96, 0.542, 0.43);
+        if (c192 < best) best = c192, pick = 2;
+        if (c96 < best) best = c96, pick = 3;
       }
-      return launch_f16_ring<128, 128, 2, 2, TA, TB>(p, batch, s);
+      if (pick == 0) return launch_f16_ring<256, 256, 2, 4, TA, TB>(p, batch, s);
+      if (pick == 1) {
+        if (tiles128 <= 256) return launch_f16_ring<128, 128, 2, 4, TA, TB>(p, batch, s);
+        return launch_f16_ring<128, 128, 2, 2, TA, TB>(p, batch, s);
+      }
+      if constexpr (TB) {
+        // 128 x 192: 8 waves, one workgroup per CU and a ring of three K-tile pairs (120 KiB),
+        // two pairs in flight (the 512 x 11008 x 4096 linear layer: 49.0 -> 46.9 us ReLU
+        // against two-slot 128 x 96 tiles)
+        if (pick == 2) return launch_f16_ring<128, 192, 2, 4, TA, TB, 2, 3>(p, batch, s);
+        return launch_f16_ring<128, 96, 2, 2, TA, TB>(p, batch, s);
+      }
     }
+    if (tiles256 >= 512) return launch_f16<256, 256, 64, 2, 4, TA, TB, VEC>(p, batch, s);
     if (tiles128 >= 128) return launch_f16<128, 128, 64, 2, 2, TA, TB, VEC>(p, batch, s);
     return launch_f16<64, 64, 64, 2, 2, TA, TB, VEC>(p, batch, s);
   }

@@ -513,13 +513,15 @@ def test_fused_linear_nil_activation_call_sequence(dev):
 
 
 # ------------------------------------------------------------------ fp16 ring kernel (large aligned shapes)
+@pytest.mark.parametrize("M,N", [(4000, 4000), (2500, 2600)])
 @pytest.mark.parametrize("tA,tB", VARIANTS)
-def test_f16_ring_ragged_all_transposes(dev, tA, tB):
-    """Shapes large enough for the buffer->LDS ring kernel (>= 256 tiles of 256x256) with
-    M, N not multiples of 256 and K not a multiple of the 32-deep K tile: out-of-range
-    rows, columns and the K tail must read as zeros."""
+def test_f16_ring_ragged_all_transposes(dev, tA, tB, M, N):
+    """The ring kernel at 256x256 tiles (4000 x 4000: one round of 256) and at 128x128 tiles
+    with two workgroups per CU (2500 x 2600: 420 tiles), M, N not multiples of the tile and K
+    not a multiple of the 32-deep K tile: out-of-range rows, columns and the K tail must read
+    as zeros."""
     rng = np.random.default_rng(31)
-    M, N, K = 4000, 4104, 1000
+    K = 1000
     A = rng.standard_normal((M, K)).astype(np.float32)
     B = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
     C = _gemm_dev(dev, A, B, tA, tB, G.GN_F16)
@@ -547,7 +549,7 @@ def test_f16_ring_odd_k_tiles_all_layouts(dev, K):
     and TT equal the NN result bit for bit (same summation order per element), and TN
     meets the oracle within the fp16-input bar."""
     rng = np.random.default_rng(K)
-    M, N = 4096, 4104
+    M, N = 4096, 4000
     A = rng.standard_normal((M, K)).astype(np.float32)
     B = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
     c_tn = _gemm_dev(dev, A, B, True, False, G.GN_F16)
@@ -587,8 +589,8 @@ def test_f16_ring_batched_and_epilogue(dev):
 # ------------------------------------------------------------------ fp16, fewer 256x256 tiles than CUs
 @pytest.mark.parametrize("tA,tB", VARIANTS)
 def test_f16_few_tiles_ragged_all_transposes(dev, tA, tB):
-    """3 x 12 tiles of 256: the 128-wide ring kernels take it (128x128 tiles for NN and
-    TN, 128x96 for NT and TT), with M, N ragged and an 8-deep K tail (K = 5000)."""
+    """3 x 12 tiles of 256: the 128-wide ring kernels take it (128x128 tiles with 8 waves for
+    NN and TN, 128x96 for NT and TT), with M, N ragged and an 8-deep K tail (K = 5000)."""
     rng = np.random.default_rng(43)
     M, N, K = 704, 3000, 5000
     A = rng.standard_normal((M, K)).astype(np.float32)
@@ -633,10 +635,10 @@ def test_f16_deterministic_batched_epilogue(dev):
 
 @pytest.mark.parametrize("tA", [False, True])
 def test_f16_128x96_tiles_ragged(dev, tA):
-    """K-contiguous B with a tile count that favours 128x96 tiles (the linear-layer shape
-    class): N = 5000 leaves a partial 96-wide tile, M = 520 a partial 128-row tile."""
+    """K-contiguous B with a tile count that favours 128x96 tiles (168 of them, fewer than one
+    per CU): N = 2000 leaves a partial 96-wide tile, M = 1000 a partial 128-row tile."""
     rng = np.random.default_rng(59)
-    M, N, K = 520, 5000, 1032
+    M, N, K = 1000, 2000, 1032
     A = rng.standard_normal((M, K)).astype(np.float32)
     B = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
     C = _gemm_dev(dev, A, B, tA, True, G.GN_F16)
