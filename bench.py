@@ -419,13 +419,13 @@ def run_spmm(c, steps, warmup, csr):
            "bytes_compulsory": b_c, "traffic": traffic,
            "note": "streamed bytes count every D-row gather (an effective bandwidth: the gathers are "
                    "served by L2 and the Infinity Cache, so it can exceed the HBM peak); the measured rate "
-                   "is the L2 refill traffic per launch (FETCH_SIZE + WRITE_SIZE, Infinity Cache hits "
-                   "included) over the kernel time"}
+                   "is the L2 refill traffic per call (FETCH_SIZE + WRITE_SIZE summed over the call's two "
+                   "kernel launches, Infinity Cache hits included) over the call's time"}
     if traffic:
         refill = traffic / (ms * 1e-3) / 1e9
         out["GB/s_l2_refill"] = round(refill, 1)
         out["frac_8TBps_l2_refill"] = round(refill / PEAK_HBM_GBS, 4)
-        log(f"spmm: {refill:.0f} GB/s of measured L2 refill traffic ({traffic / 1e9:.2f} GB per launch)")
+        log(f"spmm: {refill:.0f} GB/s of measured L2 refill traffic ({traffic / 1e9:.2f} GB per call)")
     return out
 
 

@@ -7,7 +7,10 @@
 // 32-float bands (one 128-byte line of a D row) and runs the bands one after another, so
 // the D lines gathered at any time fit the L2 far better than whole 1 KiB D rows do: the
 // kernel is bound by L2 refills from the Infinity Cache, and banding cuts them by a
-// quarter at N = 256. Narrower or unaligned products use a group of LPR lanes per CSR
+// quarter at N = 256. From 65536 entries up, spmm_band_half_kernel does the same in two
+// launches over the first and second half of each row's entries (the partial sum goes
+// through C), which halves the D rows each launch gathers from when columns are sorted and
+// cuts the refills by another quarter. Narrower or unaligned products use a group of LPR lanes per CSR
 // row, lane l accumulating columns 4l..4l+3 (or column l). Each output is accumulated in
 // CSR order with one fma per entry, which reproduces the reference loop's summation
 // order exactly (bit-identical to an fmaf restatement of it, in every kernel).
@@ -143,6 +146,7 @@ constexpr int kBandCols = 32;
 constexpr int kBandLanes = kBandCols / 4;
 constexpr int kBandRowsPerBlock = (kBlock / 64) * (64 / kBandLanes);
 constexpr int kBandUnroll = 16;
+constexpr long kSplitMinNnz = 1L << 16;  // below this, one launch of spmm_band_kernel
 
 __global__ void __launch_bounds__(kBlock) spmm_band_kernel(long M, long N, long K, long nnz, long row_blocks,
                                                            const int32_t *__restrict__ rowptr,
@@ -208,6 +212,81 @@ __global__ void __launch_bounds__(kBlock) spmm_band_kernel(long M, long N, long 
   *reinterpret_cast<float4_t *>(C + row * ldc + c0) = acc;
 }
 
+// The band kernel in two launches, each row's entries split at their midpoint: launch 0 sums
+// entries s .. m-1 into C, launch 1 loads that partial and adds entries m .. e-1, so each
+// output still takes one fma per entry in CSR order (the partial is stored exactly). With
+// sorted columns the first half of a row's entries gathers from the low rows of D, so the
+// D lines either launch reaches at a time are about half a band. Batches of 16 entries may
+// read indices and values past the row's end (never past nnz) and mask them, so no row ends
+// in a one-entry-at-a-time tail; only the last entries of the arrays take it.
+template <bool SECOND>
+__global__ void __launch_bounds__(kBlock) spmm_band_half_kernel(long M, long N, long K, long nnz, long row_blocks,
+                                                                const int32_t *__restrict__ rowptr,
+                                                                const int32_t *__restrict__ col,
+                                                                const float *__restrict__ val,
+                                                                const float *__restrict__ D, long ldd,
+                                                                float *__restrict__ C, long ldc, int *flags) {
+  const int lane = threadIdx.x & 63;
+  const int li = lane % kBandLanes;
+  const long band = blockIdx.x / row_blocks;
+  const long row = (blockIdx.x % row_blocks) * kBandRowsPerBlock + (threadIdx.x >> 6) * (64 / kBandLanes) +
+                   lane / kBandLanes;
+  const long c0 = band * kBandCols + 4 * li;
+  if (row >= M || c0 >= N) return;
+  int s, e;
+  row_bounds(rowptr, row, nnz, s, e, flags, li == 0 && !SECOND);
+  const int m = s + ((e - s) >> 1);
+  const int lo = SECOND ? m : s, hi = SECOND ? e : m;
+  float4_t acc = {0.f, 0.f, 0.f, 0.f};
+  if (SECOND) acc = *reinterpret_cast<const float4_t *>(C + row * ldc + c0);
+  bool bad_col = false;
+  int k = lo;
+  for (; k < hi && k + kBandUnroll <= nnz; k += kBandUnroll) {
+    int cc[kBandUnroll];
+    float vv[kBandUnroll];
+    float4_t dd[kBandUnroll];
+#pragma unroll
+    for (int u = 0; u < kBandUnroll; ++u) {
+      cc[u] = col[k + u];
+      vv[u] = val[k + u];
+    }
+    const int f = hi - k < kBandUnroll ? hi - k : kBandUnroll;  // entries of this range in the batch
+    unsigned ok = 0;
+#pragma unroll
+    for (int u = 0; u < kBandUnroll; ++u) {
+      if (u < f && (unsigned)cc[u] < (unsigned long)K) {
+        dd[u] = *reinterpret_cast<const float4_t *>(D + (long)cc[u] * ldd + c0);
+        ok |= 1u << u;
+      }
+    }
+    bad_col |= ok != (f == kBandUnroll ? (1u << kBandUnroll) - 1 : (1u << f) - 1);
+#pragma unroll
+    for (int u = 0; u < kBandUnroll; ++u) {
+      if (ok & (1u << u)) {
+        acc[0] = __builtin_fmaf(vv[u], dd[u][0], acc[0]);
+        acc[1] = __builtin_fmaf(vv[u], dd[u][1], acc[1]);
+        acc[2] = __builtin_fmaf(vv[u], dd[u][2], acc[2]);
+        acc[3] = __builtin_fmaf(vv[u], dd[u][3], acc[3]);
+      }
+    }
+  }
+  for (; k < hi; ++k) {  // within 16 entries of the end of the arrays
+    const int c = col[k];
+    if ((unsigned)c < (unsigned long)K) {
+      const float v = val[k];
+      const float4_t d = *reinterpret_cast<const float4_t *>(D + (long)c * ldd + c0);
+      acc[0] = __builtin_fmaf(v, d[0], acc[0]);
+      acc[1] = __builtin_fmaf(v, d[1], acc[1]);
+      acc[2] = __builtin_fmaf(v, d[2], acc[2]);
+      acc[3] = __builtin_fmaf(v, d[3], acc[3]);
+    } else {
+      bad_col = true;
+    }
+  }
+  if (bad_col && flags) flags[1] = 1;
+  *reinterpret_cast<float4_t *>(C + row * ldc + c0) = acc;
+}
+
 template <int LPR>
 __global__ void __launch_bounds__(kBlock) spmv_kernel(long M, long K, long nnz, const int32_t *__restrict__ rowptr,
                                                       const int32_t *__restrict__ col,
@@ -251,8 +330,19 @@ int launch_spmm(long M, long N, long K, long nnz, const int32_t *rowptr, const i
     const long row_blocks = (M + kBandRowsPerBlock - 1) / kBandRowsPerBlock;
     const long bands = (N + kBandCols - 1) / kBandCols;
     if (row_blocks > 0x7FFFFFFFL / bands) return set_error(err, -1, "spmm: too many rows");
-    hipLaunchKernelGGL(spmm_band_kernel, dim3((unsigned)(row_blocks * bands)), dim3(kBlock), 0, s, M, N, K, nnz,
-                       row_blocks, rowptr, col, val, D, ldd, C, ldc, flags);
+    const dim3 g((unsigned)(row_blocks * bands)), b(kBlock);
+    if (nnz >= kSplitMinNnz) {
+      // Two launches (rows split at their entries' midpoint). C5 (65536^2, 4.3 M entries, N =
+      // 256): 463 -> 383 us; 16 entries per row 218 -> 144 us; N = 32 65 -> 54 us; K = 16384
+      // 313 -> 280 us; K = 131072 580 -> 563 us; bit-identical to one launch in every case.
+      hipLaunchKernelGGL(spmm_band_half_kernel<false>, g, b, 0, s, M, N, K, nnz, row_blocks, rowptr, col, val, D, ldd,
+                         C, ldc, flags);
+      hipLaunchKernelGGL(spmm_band_half_kernel<true>, g, b, 0, s, M, N, K, nnz, row_blocks, rowptr, col, val, D, ldd,
+                         C, ldc, flags);
+    } else {
+      hipLaunchKernelGGL(spmm_band_kernel, g, b, 0, s, M, N, K, nnz, row_blocks, rowptr, col, val, D, ldd, C, ldc,
+                         flags);
+    }
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : hip_error(err, -6, "spmm launch", e);
   }

@@ -120,6 +120,56 @@ def test_spmm_column_bands_skip_bad_columns_in_full_batches(dev):
     np.testing.assert_array_equal(Cd.cpu().numpy(), ref)
 
 
+def _with_row_lengths(rp, col, val, lengths):
+    """The CSR with the first rows cut to the given lengths (entries dropped from their ends)."""
+    keep = np.ones(col.size, bool)
+    for r, n in enumerate(lengths):
+        keep[rp[r] + n:rp[r + 1]] = False
+    rp2 = np.concatenate([[0], np.cumsum([keep[rp[r]:rp[r + 1]].sum() for r in range(rp.size - 1)])]).astype(np.int32)
+    return rp2, col[keep], val[keep]
+
+
+@pytest.mark.parametrize("N,ldd,ldc,order", [(32, 32, 32, "sorted"), (100, 104, 100, "unsorted"),
+                                             (256, 256, 260, "duplicates")])
+def test_spmm_two_launch_split_bit_exact(dev, N, ldd, ldc, order):
+    """From 65536 stored entries the band path runs in two launches, over the first and the
+    second half of each row's entries, with the partial sum passing through C. Rows of 0, 1,
+    2 and 3 entries, unsorted or repeated columns, pitches wider than N, a partial last band,
+    the last entries of the arrays (inside the final 16-entry batch), and out-of-range
+    columns in either half of a row and in the arrays' last entry: bit for bit against the
+    fmaf restatement of the reference loop (bad entries skipped), flags[1] raised."""
+    import torch
+
+    M, K = 2500, 3000
+    rp, col, val = O.random_csr(M, K, 40.0, seed=N + 1, distinct=order != "duplicates")
+    rp, col, val = _with_row_lengths(rp, col, val, [0, 1, 2, 3, 0])
+    if order == "unsorted":
+        col = _shuffle_rows(rp, col, N)
+    assert col.size >= 1 << 16
+    lens = rp[1:] - rp[:-1]
+    long_row = int(np.argmax(lens))
+    bad = col.copy()
+    drop = [rp[long_row] + 3, rp[long_row] + lens[long_row] * 3 // 4, rp[3] + 2, col.size - 1]
+    bad[drop[0]], bad[drop[1]], bad[drop[2]], bad[drop[3]] = K, -7, K + 100, 2 * K
+    keep = np.ones(col.size, bool)
+    keep[drop] = False
+    rp_keep = np.concatenate([[0], np.cumsum([keep[rp[r]:rp[r + 1]].sum() for r in range(M)])]).astype(np.int32)
+    D = O.normal((K, N), 9, N)
+    ref = O.spmm_f32(rp_keep, col[keep], val[keep], D, use_fma=True)
+    d = [torch.from_numpy(a).to(dev) for a in (rp, bad, val)]
+    Dd = torch.zeros((K, ldd), dtype=torch.float32, device=dev)
+    Dd[:, :N] = torch.from_numpy(D).to(dev)
+    Cd = torch.full((M, ldc), float("nan"), dtype=torch.float32, device=dev)
+    flags = torch.zeros(2, dtype=torch.int32, device=dev)
+    _say("spmm two-launch split", N, ldd, ldc, order, col.size)
+    G.spmm_csr(M, N, K, val.size, d[0], d[1], d[2], Dd, Cd, flags, ldd=ldd, ldc=ldc)
+    assert flags.cpu().tolist() == [0, 1]
+    C = Cd.cpu().numpy()
+    np.testing.assert_array_equal(C[:, :N], ref)
+    assert np.isnan(C[:, N:]).all()
+    assert np.all(C[[0, 4], :N] == 0)
+
+
 def test_spmm_with_duplicates_unsorted_columns(dev):
     rp, col, val = O.random_csr(300, 50, 20.0, seed=3, distinct=False)  # many duplicate columns
     D = O.normal((50, 256), 6, 1)
