@@ -1145,6 +1145,74 @@ hipError_t launch_f32_ring(GemmParams p, long batch, hipStream_t s) {
 // (MN-contiguous) past the tile base.
 bool ring_offsets_fit(const GemmParams &p) { return p.lda < (1L << 21) && p.ldb < (1L << 21); }
 
+// The fp16 ring kernel's tile from a time model. A round is 256 tiles (one per CU) for the
+// one-workgroup-per-CU tiles (256x256 and 128x192, 8 waves; 128x128 with 8 waves when one
+// round holds every tile) and 512 for the two-per-CU ones (128x128 and 128x96, 4 waves).
+// Each tile type takes a measured time per round, relative to a round of 256x256 tiles at
+// the same K: 128x192 0.509, 128x128 8-wave 0.508; two co-resident 128x128 0.638 (0.52 for
+// one alone), 128x96 0.542 (0.43 alone, estimated). A last, partial round costs its fill
+// fraction but at least 0.75 of a full one: with fewer CUs busy the power-limited clock
+// rises (3072^3: 144 tiles of 256x256 on 256 CUs take 0.75 of a full round's time), so a
+// 256x256 round that is half full still beats twice the 128x128 tiles. The model picks the
+// measured best of these tiles at n^3 from 1536 to 6144 and at M x 11008 x 4096 for M =
+// 512..2048, NT and TT (3072^3: 63 us against 82 us for the earlier 128x128 choice; 1536 x
+// 11008 x 4096 NT: 147 us against 179 us for 256x256; the 512 x 11008 x 4096 linear layer:
+// 128x192).
+enum class F16Tile { k256, k128w8, k128w4, k192, k96 };
+struct F16Choice {
+  double cost;
+  F16Tile tile;
+};
+
+inline double f16_rounds1(long t, double r) {
+  const long u = t % 256;
+  return (double)(t / 256) * r + (u ? r * fmax(0.75, u / 256.0) : 0.0);
+}
+inline double f16_rounds2(long t, double r2, double r1) {
+  const long u = t % 512;
+  return (double)(t / 512) * r2 + (u == 0 ? 0.0 : u <= 256 ? r1 * fmax(0.75, u / 256.0) : r2 * fmax(0.75, u / 512.0));
+}
+
+template <bool TB>
+F16Choice f16_best(long M, long N, long batch) {
+  const long tiles256 = ((M + 255) / 256) * ((N + 255) / 256) * batch;
+  const long tiles128 = ((M + 127) / 128) * ((N + 127) / 128) * batch;
+  F16Choice b{f16_rounds1(tiles256, 1.0), F16Tile::k256};
+  const double c128 = tiles128 <= 256 ? f16_rounds1(tiles128, 0.508) : f16_rounds2(tiles128, 0.638, 0.52);
+  if (c128 < b.cost) b = {c128, tiles128 <= 256 ? F16Tile::k128w8 : F16Tile::k128w4};
+  if constexpr (TB) {
+    // 128 x 192 and 128 x 96 only for a K-contiguous B: 384- and 192-byte MN-contiguous rows
+    // would not take the 32-byte block swizzle of the transposing reads.
+    const long tiles192 = ((M + 127) / 128) * ((N + 191) / 192) * batch;
+    const long tiles96 = ((M + 127) / 128) * ((N + 95) / 96) * batch;
+    const double c192 = f16_rounds1(tiles192, 0.509), c96 = f16_rounds2(tiles96, 0.542, 0.43);
+    if (c192 < b.cost) b = {c192, F16Tile::k192};
+    if (c96 < b.cost) b = {c96, F16Tile::k96};
+  }
+  return b;
+}
+
+template <bool TA, bool TB>
+hipError_t launch_f16_tile(const GemmParams &p, long batch, hipStream_t s, F16Tile t) {
+  switch (t) {
+    case F16Tile::k256:
+      return launch_f16_ring<256, 256, 2, 4, TA, TB>(p, batch, s);
+    case F16Tile::k128w8:
+      return launch_f16_ring<128, 128, 2, 4, TA, TB>(p, batch, s);
+    case F16Tile::k128w4:
+      return launch_f16_ring<128, 128, 2, 2, TA, TB>(p, batch, s);
+    default:
+      if constexpr (TB) {
+        // 128 x 192: 8 waves, one workgroup per CU and a ring of three K-tile pairs (120 KiB),
+        // two pairs in flight (the 512 x 11008 x 4096 linear layer: 49.0 -> 46.9 us ReLU
+        // against two-slot 128 x 96 tiles)
+        if (t == F16Tile::k192) return launch_f16_ring<128, 192, 2, 4, TA, TB, 2, 3>(p, batch, s);
+        return launch_f16_ring<128, 96, 2, 2, TA, TB>(p, batch, s);
+      }
+      return hipErrorInvalidValue;  // f16_best offers these tiles only for a K-contiguous B
+  }
+}
+
 template <bool TA, bool TB, bool VEC>
 hipError_t pick_f16(const GemmParams &p, long batch, hipStream_t s) {
   if constexpr (!VEC) {
@@ -1154,53 +1222,35 @@ hipError_t pick_f16(const GemmParams &p, long batch, hipStream_t s) {
     const long tiles256 = ((p.M + 255) / 256) * ((p.N + 255) / 256) * batch;
     const long tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
     if (tiles128 >= 128 && ring_offsets_fit(p)) {
-      // The ring kernel's tile from a time model. A round is 256 tiles (one per CU) for the
-      // one-workgroup-per-CU tiles (256x256 and 128x192, 8 waves; 128x128 with 8 waves when
-      // one round holds every tile) and 512 for the two-per-CU ones (128x128 and 128x96, 4
-      // waves). Each tile type takes a measured time per round, relative to a round of
-      // 256x256 tiles at the same K: 128x192 0.509, 128x128 8-wave 0.508; two co-resident
-      // 128x128 0.638 (0.52 for one alone), 128x96 0.542 (0.43 alone, estimated). A last,
-      // partial round costs its fill fraction but at least 0.75 of a full one: with fewer
-      // CUs busy the power-limited clock rises (3072^3: 144 tiles of 256x256 on 256 CUs take
-      // 0.75 of a full round's time), so a 256x256 round that is half full still beats twice
-      // the 128x128 tiles. The model picks the measured best of these tiles at n^3 from 1536
-      // to 6144 and at M x 11008 x 4096 for M = 512..2048, NT and TT (3072^3: 63 us against
-      // 82 us for the earlier 128x128 choice; 1536 x 11008 x 4096 NT: 147 us against 179 us
-      // for 256x256; the 512 x 11008 x 4096 linear layer: 128x192).
-      auto one = [](long t, double r) {
-        const long u = t % 256;
-        return (double)(t / 256) * r + (u ? r * fmax(0.75, u / 256.0) : 0.0);
-      };
-      auto two = [](long t, double r2, double r1) {
-        const long u = t % 512;
-        return (double)(t / 512) * r2 +
-               (u == 0 ? 0.0 : u <= 256 ? r1 * fmax(0.75, u / 256.0) : r2 * fmax(0.75, u / 512.0));
-      };
-      double best = one(tiles256, 1.0);
-      int pick = 0;
-      const double c128 = tiles128 <= 256 ? one(tiles128, 0.508) : two(tiles128, 0.638, 0.52);
-      if (c128 < best) best = c128, pick = 1;
-      if constexpr (TB) {
-        // 128 x 192 and 128 x 96 only for a K-contiguous B: 384- and 192-byte MN-contiguous
-        // rows would not take the 32-byte block swizzle of the transposing reads.
-        const long tiles192 = ((p.M + 127) / 128) * ((p.N + 191) / 192) * batch;
-        const long tiles96 = ((p.M + 127) / 128) * ((p.N + 95) / 96) * batch;
-        const double c192 = one(tiles192, 0.509), c96 = two(tiles96, 0.542, 0.43);
-        if (c192 < best) best = c192, pick = 2;
-        if (c96 < best) best = c96, pick = 3;
+      const F16Choice whole = f16_best<TB>(p.M, p.N, batch);
+      if (batch == 1) {
+        // Two launches over row blocks, rows 0..256k-1 on 256x256 tiles and the rest on the
+        // remainder's own best tile, when the model puts that at least 10% under one launch:
+        // a partial round of 256x256 tiles becomes a fuller one plus a round of smaller
+        // tiles. Each output element still comes from one tile in the same K order, so the
+        // result is bit-identical. fp16 4608^3: 224.5 -> 188.7 us (rows split at 3328); 6144^3:
+        // 415 -> 375 us (5120); at 5120^3, 3072^3 and 2560^3 every split measured slower, and
+        // the model keeps those in one launch.
+        const long tm = (p.M + 255) / 256, tn = (p.N + 255) / 256;
+        double best = 0.9 * whole.cost;
+        long k_best = 0;
+        F16Tile bottom = F16Tile::k256;
+        for (long k = 1; k < tm; ++k) {
+          const F16Choice b = f16_best<TB>(p.M - 256 * k, p.N, 1);
+          const double c = f16_rounds1(k * tn, 1.0) + b.cost;
+          if (c < best) best = c, k_best = k, bottom = b.tile;
+        }
+        if (k_best > 0) {
+          GemmParams top = p, bot = p;
+          top.M = 256 * k_best;
+          bot.M = p.M - top.M;
+          bot.A = static_cast<const _Float16 *>(p.A) + (TA ? top.M : top.M * p.lda);
+          bot.C = p.C + top.M * p.ldc;
+          if (hipError_t e = launch_f16_ring<256, 256, 2, 4, TA, TB>(top, 1, s)) return e;
+          return launch_f16_tile<TA, TB>(bot, 1, s, bottom);
+        }
       }
-      if (pick == 0) return launch_f16_ring<256, 256, 2, 4, TA, TB>(p, batch, s);
-      if (pick == 1) {
-        if (tiles128 <= 256) return launch_f16_ring<128, 128, 2, 4, TA, TB>(p, batch, s);
-        return launch_f16_ring<128, 128, 2, 2, TA, TB>(p, batch, s);
-      }
-      if constexpr (TB) {
-        // 128 x 192: 8 waves, one workgroup per CU and a ring of three K-tile pairs (120 KiB),
-        // two pairs in flight (the 512 x 11008 x 4096 linear layer: 49.0 -> 46.9 us ReLU
-        // against two-slot 128 x 96 tiles)
-        if (pick == 2) return launch_f16_ring<128, 192, 2, 4, TA, TB, 2, 3>(p, batch, s);
-        return launch_f16_ring<128, 96, 2, 2, TA, TB>(p, batch, s);
-      }
+      return launch_f16_tile<TA, TB>(p, batch, s, whole.tile);
     }
     if (tiles256 >= 512) return launch_f16<256, 256, 64, 2, 4, TA, TB, VEC>(p, batch, s);
     if (tiles128 >= 128) return launch_f16<128, 128, 64, 2, 2, TA, TB, VEC>(p, batch, s);

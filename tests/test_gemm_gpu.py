@@ -542,6 +542,38 @@ def test_f16_ring_transpose_variants_bit_identical(dev):
         np.testing.assert_array_equal(o, outs[0])
 
 
+def test_f16_row_split_all_transposes_bit_identical(dev):
+    """A shape whose last round of 256x256 tiles would be mostly empty (4600 x 4608: 18 x 18
+    tiles) runs as two launches over row blocks: rows below 3072 (NN, TN) or 3584 (NT, TT) on
+    256x256 tiles, the rest on 128-row tiles. M and K are ragged. NaN start and whole-output
+    row and column sums for every layout, sampled rows (both sides of each split) against
+    float64 of the fp16-rounded inputs, and the four layouts bit for bit."""
+    import torch
+
+    rng = np.random.default_rng(4600)
+    M, N, K = 4600, 4608, 96
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
+    outs = []
+    for tA, tB in VARIANTS:
+        _say("f16 row split", tA, tB)
+        ad = torch.from_numpy(_stored(A, tA)).to(dev).half()
+        bd = torch.from_numpy(_stored(B, tB)).to(dev).half()
+        cd = _nan_like(dev, M, N)
+        G.gemm(ad, bd, cd, transA=tA, transB=tB)
+        row_err, col_err = _sum_invariants(ad, bd, cd, tA, tB)
+        assert row_err <= 1e-5 and col_err <= 1e-5, (tA, tB, row_err, col_err)
+        outs.append(cd.cpu().numpy())
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])
+    rows = np.concatenate([np.arange(3064, 3080), np.arange(3576, 3592), rng.choice(M, 16, replace=False),
+                           np.arange(M - 8, M)])
+    ref_r = O.gemm_f64_rows(O.round_f16(A[rows], False), O.round_f16(B, False), np.arange(rows.size))
+    err = O.rel_frob(outs[0][rows], ref_r)
+    _say("f16 row split relFrob", err)
+    assert err <= 1e-5
+
+
 @pytest.mark.parametrize("K", [8, 40, 968])
 def test_f16_ring_odd_k_tiles_all_layouts(dev, K):
     """The ring takes K-tiles two at a time. One 32-deep K-tile (K = 8), two with a tail
