@@ -28,21 +28,25 @@ def test_graph_replays_match_eager(dev):
     x32 = torch.randn(700, 300, device=dev)              # fp32 register-staged kernel
     w32 = torch.randn(300, 500, device=dev)
     bias = torch.randn(500, device=dev)
-    rp, col, val = O.random_csr(2000, 3000, 20.0, seed=3)
+    a2 = torch.randn(4600, 64, device=dev).half()        # fp16 row split: two launches
+    b2 = torch.randn(64, 4608, device=dev).half()
+    rp, col, val = O.random_csr(4000, 3000, 20.0, seed=3)  # > 65536 entries: SpMM in two launches
     d_rp, d_col, d_val = (torch.from_numpy(v).to(dev) for v in (rp, col, val))
     D = torch.randn(3000, 64, device=dev)
     xv = torch.randn(3000, device=dev)
 
     c16 = torch.empty(4096, 4096, device=dev)
+    c2 = torch.empty(4600, 4608, device=dev)
     y32 = torch.empty(700, 500, device=dev)
-    S = torch.empty(2000, 64, device=dev)
-    yv = torch.empty(2000, device=dev)
+    S = torch.empty(4000, 64, device=dev)
+    yv = torch.empty(4000, device=dev)
 
     def work():
         G.gemm(a16, b16, c16)
+        G.gemm(a2, b2, c2)
         G.gemm(x32, w32, y32, bias=bias, act=G.ACT_GELU)
-        G.spmm_csr(2000, 64, 3000, val.size, d_rp, d_col, d_val, D, S)
-        G.spmv_csr(2000, 3000, val.size, d_rp, d_col, d_val, xv, yv)
+        G.spmm_csr(4000, 64, 3000, val.size, d_rp, d_col, d_val, D, S)
+        G.spmv_csr(4000, 3000, val.size, d_rp, d_col, d_val, xv, yv)
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -55,11 +59,13 @@ def test_graph_replays_match_eager(dev):
         work()
     torch.cuda.synchronize()
 
-    outs = (c16, y32, S, yv)
+    assert val.size >= 1 << 16
+    outs = (c16, c2, y32, S, yv)
     for rep in range(3):
         # new inputs, eager work and a synchronisation between replays
         with torch.no_grad():
             a16.copy_(torch.randn_like(a16, dtype=torch.float32).half())
+            b2.copy_(torch.randn_like(b2, dtype=torch.float32).half())
             w32.mul_(0.5).add_(0.1)
             D.copy_(torch.randn_like(D))
             xv.mul_(-1.5)
@@ -69,7 +75,7 @@ def test_graph_replays_match_eager(dev):
         got = [t.clone() for t in outs]
         work()  # eager, on the current stream
         torch.cuda.synchronize()
-        for name, gt, ref in zip(("gemm f16", "gemm f32", "spmm", "spmv"), got, outs):
+        for name, gt, ref in zip(("gemm f16", "gemm f16 row split", "gemm f32", "spmm", "spmv"), got, outs):
             same = torch.equal(gt, ref)
             _say("replay", rep, name, "bit-identical" if same else "DIFFERS")
             assert same, (rep, name)
