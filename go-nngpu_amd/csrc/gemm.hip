@@ -1258,49 +1258,72 @@ hipError_t pick_f16(const GemmParams &p, long batch, hipStream_t s) {
   }
 }
 
+// The fp32 ring's tile (K a multiple of 32): each candidate's time is modelled as its rounds
+// (ceil(tiles / 256), the CU count) times the tile's area over the tile's per-CU efficiency
+// with the CU kept busy. The efficiencies are fits to n^3 problems from 2048 to 6144 in all
+// four layouts (256: 0.95; 128: 0.93, 0.89 for a single round of 8-wave tiles; 64: 0.88),
+// and the model picks the measured best at every size tried: 64 x 64 at 2560..5120 (5120^3:
+// 1920 us against 2040 for 128 x 128 and 2302 for 256 x 256), 128 x 128 at 2048 and 6144
+// (3145 us against 3269 and 4155), 256 x 256 at 4096 and 8192.
+//  * 256 x 256, 8 waves, one workgroup per CU: NN with 2 x 4 waves of 128 x 64; NT, TN and TT
+//    with 4 x 2 waves of 64 x 128 (an MN-contiguous A takes the shorter wave side; TN streams
+//    its fragments a component at a time);
+//  * 128 x 128: 8 waves (2 x 4, or 4 x 2 for a K-contiguous B) when one round holds every
+//    tile, else 4 waves with two workgroups per CU;
+//  * 64 x 64, 4 waves, up to five workgroups per CU.
+template <bool TA, bool TB>
+hipError_t launch_f32_ring_best(const GemmParams &p, long batch, hipStream_t s) {
+  const long tiles256 = ((p.M + 255) / 256) * ((p.N + 255) / 256) * batch;
+  const long tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
+  const long tiles64 = ((p.M + 63) / 64) * ((p.N + 63) / 64) * batch;
+  auto cost = [](long tiles, double area, double eff) { return (double)((tiles + 255) / 256) * area / eff; };
+  const double c256 = cost(tiles256, 256.0 * 256.0, 0.95);
+  const double c128 = cost(tiles128, 128.0 * 128.0, tiles128 <= 256 ? 0.89 : 0.93);
+  const double c64 = cost(tiles64, 64.0 * 64.0, 0.88);
+  if (c256 <= c128 && c256 <= c64) {
+    if constexpr (!TA && !TB) return launch_f32_ring<256, 256, 2, 4, TA, TB>(p, batch, s);
+    else return launch_f32_ring<256, 256, 4, 2, TA, TB>(p, batch, s);
+  }
+  if (c128 <= c64) {
+    if (tiles128 > 256) return launch_f32_ring<128, 128, 2, 2, TA, TB>(p, batch, s);
+    if constexpr (TB) return launch_f32_ring<128, 128, 4, 2, TA, TB>(p, batch, s);
+    else return launch_f32_ring<128, 128, 2, 4, TA, TB>(p, batch, s);
+  }
+  return launch_f32_ring<64, 64, 2, 2, TA, TB>(p, batch, s);
+}
+
 template <bool TA, bool TB, bool VEC>
 hipError_t pick_f32(const GemmParams &p, long batch, hipStream_t s) {
   if constexpr (!VEC) {
     return launch_f32<64, 64, 16, 2, 2, TA, TB, VEC>(p, batch, s);
   } else {
-    // The DMA ring whenever K is a multiple of 32 (whole K-tile pairs); the vector path's
-    // alignment (every contiguous extent a multiple of 4 floats) keeps its 16-byte copies
-    // inside the operands. Tiles:
-    //  * 256 x 256, 8 waves, one workgroup per CU: NN with 2 x 4 waves of 128 x 64; NT, TN and
-    //    TT with 4 x 2 waves of 64 x 128 (an MN-contiguous A takes the shorter wave side; TN
-    //    streams its fragments a component at a time);
-    //  * 128 x 128: 8 waves (2 x 4, or 4 x 2 for a K-contiguous B) when one round holds every
-    //    tile, else 4 waves with two workgroups per CU;
-    //  * 64 x 64, 4 waves, up to five workgroups per CU.
-    // Each candidate's time is modelled as its rounds (ceil(tiles / 256), the CU count) times
-    // the tile's area over the tile's per-CU efficiency with the CU kept busy. The efficiencies
-    // are fits to n^3 problems from 2048 to 6144 in all four layouts (256: 0.95; 128: 0.93,
-    // 0.89 for a single round of 8-wave tiles; 64: 0.88), and the model picks the measured
-    // best at every size tried: 64 x 64 at 2560..5120 (5120^3: 1920 us against 2040 for 128 x
-    // 128 and 2302 for 256 x 256), 128 x 128 at 2048 and 6144 (3145 us against 3269 and
-    // 4155), 256 x 256 at 4096 and 8192.
-    // Other K take the register-staged kernel with the largest tile that still gives 256 tiles
-    // (256 x 256 with 16 waves of 64 x 64: 4096^3 132-135 TFLOP/s against 125 / 120 for 128 x
-    // 128 tiles).
-    const bool ring = p.K % 32 == 0 && ring_offsets_fit(p);
+    // The DMA ring for the vector path, whose alignment (every contiguous extent a multiple
+    // of 4 floats) keeps its 16-byte copies inside the operands. The ring takes whole K-tile
+    // pairs (it carries no K-tail masking, which would cost it registers), so a K that is not
+    // a multiple of 32 runs in two launches: the ring over the first K - K % 32 (alpha, beta,
+    // no bias or activation), then the register-staged kernel over the last K % 32 with
+    // beta = 1 on that partial result, bias and activation. The tail pointers stay 16-byte
+    // aligned: K is a multiple of 4 for a K-contiguous operand, and leading dimensions are.
+    // The result differs from one launch only in where the two partial sums are rounded
+    // together. Against the register-staged kernel: 1000^3 35.3 -> 28.7 us, 3000^3 616 ->
+    // 424 us, 4096 x 4096 x 4100 1026 -> 950 us (torch.matmul 24.0, 431, 907 us). Leading dimensions too large for the ring's 32-bit offsets, and K < 32, take
+    // the register-staged kernel with the largest tile that still gives 256 tiles (256 x 256
+    // with 16 waves of 64 x 64: 4096^3 132-135 TFLOP/s against 125 / 120 for 128 x 128).
     const long tiles256 = ((p.M + 255) / 256) * ((p.N + 255) / 256) * batch;
     const long tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
-    if (ring) {
-      const long tiles64 = ((p.M + 63) / 64) * ((p.N + 63) / 64) * batch;
-      auto cost = [](long tiles, double area, double eff) { return (double)((tiles + 255) / 256) * area / eff; };
-      const double c256 = cost(tiles256, 256.0 * 256.0, 0.95);
-      const double c128 = cost(tiles128, 128.0 * 128.0, tiles128 <= 256 ? 0.89 : 0.93);
-      const double c64 = cost(tiles64, 64.0 * 64.0, 0.88);
-      if (c256 <= c128 && c256 <= c64) {
-        if constexpr (!TA && !TB) return launch_f32_ring<256, 256, 2, 4, TA, TB>(p, batch, s);
-        else return launch_f32_ring<256, 256, 4, 2, TA, TB>(p, batch, s);
-      }
-      if (c128 <= c64) {
-        if (tiles128 > 256) return launch_f32_ring<128, 128, 2, 2, TA, TB>(p, batch, s);
-        if constexpr (TB) return launch_f32_ring<128, 128, 4, 2, TA, TB>(p, batch, s);
-        else return launch_f32_ring<128, 128, 2, 4, TA, TB>(p, batch, s);
-      }
-      return launch_f32_ring<64, 64, 2, 2, TA, TB>(p, batch, s);
+    if (ring_offsets_fit(p) && p.K >= 32) {
+      const long kt = p.K % 32;
+      if (kt == 0) return launch_f32_ring_best<TA, TB>(p, batch, s);
+      GemmParams head = p, tail = p;
+      head.K = p.K - kt;
+      head.bias = nullptr;
+      head.act = -1;
+      tail.K = kt;
+      tail.beta = 1.0f;
+      tail.A = static_cast<const float *>(p.A) + (TA ? head.K * p.lda : head.K);
+      tail.B = static_cast<const float *>(p.B) + (TB ? head.K : head.K * p.ldb);
+      if (hipError_t e = launch_f32_ring_best<TA, TB>(head, batch, s)) return e;
+      return launch_f32<64, 64, 16, 2, 2, TA, TB, VEC>(tail, batch, s);
     }
     if (tiles256 >= 256) return launch_f32<256, 256, 16, 4, 4, TA, TB, VEC>(p, batch, s);
     if (tiles128 >= 256) return launch_f32<128, 128, 32, 2, 2, TA, TB, VEC>(p, batch, s);

@@ -267,6 +267,41 @@ def test_f32_ring_batched_alpha_beta_bias_act(dev, tA, tB):
         assert O.rel_frob(Cn[z][rows], O.act_f64(G.ACT_GELU, pre)) <= 1e-5, z
 
 
+@pytest.mark.parametrize("M,N,K,tA,tB", [(1000, 1000, 1000, False, False), (1000, 1000, 1000, False, True),
+                                           (1000, 1000, 1000, True, True), (300, 500, 100, False, False),
+                                           (2000, 2012, 1001, True, False), (4000, 4000, 40, True, False),
+                                           (2048, 2048, 36, False, True)])
+def test_f32_k_tail_split_alpha_beta_bias_act(dev, M, N, K, tA, tB):
+    """A K that is not a multiple of 32 runs as the ring over the first K - K % 32 and the
+    register-staged kernel over the rest, the partial result passing through C: alpha, beta,
+    bias and GELU must apply once. K = 1000, 100, 40 and 36 leave 8, 4, 8 and 4; TN takes any
+    K (1001: a tail of 9). Every tile: NaN-free output and row sums against float64; sampled
+    rows in full."""
+    import torch
+
+    rng = np.random.default_rng(K + M)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    ad = torch.from_numpy(_stored(A, tA)).to(dev)
+    bd = torch.from_numpy(_stored(B, tB)).to(dev)
+    C = torch.from_numpy(C0).to(dev)
+    _say("f32 K tail", M, N, K, tA, tB)
+    G.gemm(ad, bd, C, transA=tA, transB=tB, alpha=0.5, beta=0.25, bias=torch.from_numpy(bias).to(dev),
+           act=G.ACT_GELU)
+    Cn = C.cpu().numpy()
+    assert np.isfinite(Cn).all()
+    rows = np.concatenate([np.arange(0, 4), rng.choice(M, 12, replace=False), np.arange(M - 4, M)])
+    pre = 0.5 * O.gemm_f64_rows(A, B, rows) + 0.25 * C0[rows].astype(np.float64) + bias
+    assert O.rel_frob(Cn[rows], O.act_f64(G.ACT_GELU, pre)) <= 1e-5
+    # the same product with no epilogue: whole-output row and column sums
+    C2 = _nan_like(dev, M, N)
+    G.gemm(ad, bd, C2, transA=tA, transB=tB)
+    row_err, col_err = _sum_invariants(ad, bd, C2, tA, tB)
+    assert row_err <= 1e-5 and col_err <= 1e-5, (row_err, col_err)
+
+
 def test_f32_transpose_variants_bit_identical(dev):
     """All four load paths feed MFMA the same operands in the same order."""
     rng = np.random.default_rng(5)
