@@ -1350,6 +1350,48 @@ hipError_t dispatch(const GemmDesc &d, const GemmParams &p, long batch, hipStrea
   }
 }
 
+// Packs an operand for the aligned path: dst[z] (rows x Kp, row pitch Kp, 16-byte aligned)
+// = op(src[z]) zero-padded from K to Kp, where op(src) is src (rows x K, pitch ld) or, for
+// TRANS, the transpose of src (K x rows, pitch ld). 64 x 64 tiles; the transposing form goes
+// through LDS so that both its reads and its writes are coalesced. Loads are element-wise,
+// so src needs no alignment.
+template <typename T, bool TRANS>
+__global__ void __launch_bounds__(256) pack_kcontig_kernel(const T *__restrict__ src, long rows, long K, long ld,
+                                                           long sstride, T *__restrict__ dst, long Kp, long dstride) {
+  __shared__ T tile[64][65];
+  const long r0 = (long)blockIdx.y * 64, k0 = (long)blockIdx.x * 64;
+  src += (long)blockIdx.z * sstride;
+  dst += (long)blockIdx.z * dstride;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  if constexpr (TRANS) {
+    for (int i = ty; i < 64; i += 4) {
+      const long k = k0 + i, r = r0 + tx;
+      tile[i][tx] = (k < K && r < rows) ? src[k * ld + r] : T(0);
+    }
+    __syncthreads();
+    for (int i = ty; i < 64; i += 4) {
+      const long r = r0 + i, k = k0 + tx;
+      if (r < rows && k < Kp) dst[r * Kp + k] = tile[tx][i];
+    }
+  } else {
+    for (int i = ty; i < 64; i += 4) {
+      const long r = r0 + i, k = k0 + tx;
+      if (r < rows && k < Kp) dst[r * Kp + k] = k < K ? src[r * ld + k] : T(0);
+    }
+  }
+}
+
+template <typename T>
+hipError_t launch_pack(const void *src, long rows, long K, long ld, long sstride, bool trans, void *dst, long Kp,
+                       long batch, hipStream_t s) {
+  const dim3 g((unsigned)((Kp + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)batch);
+  const T *sp = static_cast<const T *>(src);
+  T *dp = static_cast<T *>(dst);
+  if (trans) hipLaunchKernelGGL((pack_kcontig_kernel<T, true>), g, dim3(256), 0, s, sp, rows, K, ld, sstride, dp, Kp, rows * Kp);
+  else hipLaunchKernelGGL((pack_kcontig_kernel<T, false>), g, dim3(256), 0, s, sp, rows, K, ld, sstride, dp, Kp, rows * Kp);
+  return hipGetLastError();
+}
+
 // Zero-K / empty-product epilogue: C = act(beta*C + bias) (alpha*0 contributes nothing).
 __global__ void gemm_k0_kernel(GemmParams p, long batch) {
   const long total = p.M * p.N * batch;
@@ -1406,6 +1448,30 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
     // The batch index is blockIdx.z (at most 65535 per launch): larger batches run as
     // consecutive launches over chunks of the batch, each with offset operands.
     constexpr long kMaxZ = 65535;
+    // Unaligned operands of a large enough product are first packed into zero-padded,
+    // K-contiguous copies (row pitch K rounded up to 64) in the stream's scratch, and the
+    // aligned path runs on them. Only the operands that fail the alignment test are packed;
+    // the product keeps its K, and a 16-byte block of a packed row that straddles K reads the
+    // padding's zeros, while the aligned kernels mask an unpacked operand's rows at or past K
+    // (per copy in the fp16 ring, by the K-tail split of the fp32 path). The result is the
+    // aligned path's on the same values. The element-wise-load kernel stays for small
+    // products, for scratch beyond 4 GiB, and under HIP graph capture (the scratch may need an
+    // allocation).
+    const long Kp = (d.K + 63) / 64 * 64;
+    const bool a_ok = aligned(d.A, d.lda, d.strideA) && a_contig % epv == 0;
+    const bool b_ok = aligned(d.B, d.ldb, d.strideB) && b_contig % epv == 0;
+    const size_t pack_bytes =
+        (size_t)((a_ok ? 0 : d.M) + (b_ok ? 0 : d.N)) * (size_t)Kp * esz * (size_t)std::min(kMaxZ, d.batch);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    const bool pack = !vec && (double)d.M * d.N * d.K >= (double)(1L << 24) && pack_bytes <= ((size_t)4 << 30) &&
+                      (std::max(d.M, d.N) + 63) / 64 <= 65535 &&  // the pack grid's y extent
+                      hipStreamIsCapturing(s, &cap) == hipSuccess && cap == hipStreamCaptureStatusNone;
+    std::unique_lock<std::mutex> lk;
+    char *ws = nullptr;
+    if (pack) {
+      ws = static_cast<char *>(stream_scratch(s, pack_bytes, lk, err));
+      if (!ws) return -3;
+    }
     e = hipSuccess;
     for (long z0 = 0; z0 < d.batch && e == hipSuccess; z0 += kMaxZ) {
       GemmParams q = p;
@@ -1413,7 +1479,31 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
       q.B = static_cast<const char *>(d.B) + z0 * d.strideB * (long)esz;
       q.C = d.C + z0 * d.strideC;
       const long nb = std::min(kMaxZ, d.batch - z0);
-      e = vec ? dispatch<true>(d, q, nb, s) : dispatch<false>(d, q, nb, s);
+      if (!pack) {
+        e = vec ? dispatch<true>(d, q, nb, s) : dispatch<false>(d, q, nb, s);
+        continue;
+      }
+      GemmDesc dp = d;
+      char *next = ws;
+      if (!a_ok) {
+        e = esz == 2 ? launch_pack<_Float16>(q.A, d.M, d.K, d.lda, d.strideA, d.ta, next, Kp, nb, s)
+                     : launch_pack<float>(q.A, d.M, d.K, d.lda, d.strideA, d.ta, next, Kp, nb, s);
+        q.A = next;
+        q.lda = Kp;
+        q.strideA = d.M * Kp;
+        dp.ta = false;
+        next += (size_t)nb * d.M * Kp * esz;
+      }
+      if (!b_ok && e == hipSuccess) {
+        e = esz == 2 ? launch_pack<_Float16>(q.B, d.N, d.K, d.ldb, d.strideB, !d.tb, next, Kp, nb, s)
+                     : launch_pack<float>(q.B, d.N, d.K, d.ldb, d.strideB, !d.tb, next, Kp, nb, s);
+        q.B = next;
+        q.ldb = Kp;
+        q.strideB = d.N * Kp;
+        dp.tb = true;
+      }
+      if (!a_ok && !b_ok) q.K = Kp;  // both padded with zeros: whole K-tile pairs, no K tail
+      if (e == hipSuccess) e = dispatch<true>(dp, q, nb, s);
     }
   }
   if (e != hipSuccess) return hip_error(err, -6, "gemm launch", e);

@@ -302,6 +302,105 @@ def test_f32_k_tail_split_alpha_beta_bias_act(dev, M, N, K, tA, tB):
     assert row_err <= 1e-5 and col_err <= 1e-5, (row_err, col_err)
 
 
+@pytest.mark.parametrize("dtype,M,N,K,tA,tB", [(G.GN_F16, 777, 1234, 4099, False, False), (G.GN_F16, 777, 1234, 4099, False, True),
+                                                 (G.GN_F16, 777, 1234, 4099, True, False), (G.GN_F16, 777, 1234, 4099, True, True),
+                                                 (G.GN_F32, 513, 1027, 999, False, False), (G.GN_F32, 513, 1027, 999, True, True),
+                                                 (G.GN_F32, 1023, 1023, 1023, False, True), (G.GN_F32, 1023, 1023, 1023, True, False)])
+def test_unaligned_packed_alpha_beta_bias_act(dev, dtype, M, N, K, tA, tB):
+    """Operands whose rows are not 16-byte multiples are packed into zero-padded K-contiguous
+    copies and multiplied on the aligned path: alpha, beta, bias and GELU against float64 of
+    the rounded inputs on sampled rows, and whole-output row and column sums (no epilogue)."""
+    import torch
+
+    rng = np.random.default_rng(M + N + K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    half = dtype == G.GN_F16
+    ad = torch.from_numpy(_stored(A, tA)).to(dev)
+    bd = torch.from_numpy(_stored(B, tB)).to(dev)
+    if half:
+        ad, bd = ad.half(), bd.half()
+    Ar, Br = (O.round_f16(A, False), O.round_f16(B, False)) if half else (A, B)
+    C = torch.from_numpy(C0).to(dev)
+    _say("unaligned packed", dtype, M, N, K, tA, tB)
+    G.gemm(ad, bd, C, transA=tA, transB=tB, alpha=0.5, beta=0.25, bias=torch.from_numpy(bias).to(dev), act=G.ACT_GELU)
+    Cn = C.cpu().numpy()
+    assert np.isfinite(Cn).all()
+    rows = np.concatenate([np.arange(0, 4), rng.choice(M, 12, replace=False), np.arange(M - 4, M)])
+    pre = 0.5 * O.gemm_f64_rows(Ar, Br, rows) + 0.25 * C0[rows].astype(np.float64) + bias
+    assert O.rel_frob(Cn[rows], O.act_f64(G.ACT_GELU, pre)) <= 1e-5
+    C2 = _nan_like(dev, M, N)
+    G.gemm(ad, bd, C2, transA=tA, transB=tB)
+    row_err, col_err = _sum_invariants(ad, bd, C2, tA, tB)
+    assert row_err <= 1e-5 and col_err <= 1e-5, (row_err, col_err)
+
+
+def test_unaligned_packed_batched_and_offset_pointer(dev):
+    """The packed path with a batch (strides of unaligned rows) and an aligned shape whose A
+    starts one element into its buffer (so no 16-byte loads), fp32 and fp16."""
+    import torch
+
+    rng = np.random.default_rng(17)
+    bs, M, N, K = 3, 300, 500, 257
+    A = rng.standard_normal((bs, M, K)).astype(np.float32)
+    B = rng.standard_normal((bs, K, N)).astype(np.float32)
+    C = _nan_like(dev, bs * M, N).reshape(bs, M, N)
+    G.gemm(torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev), C, batch=bs, strideA=M * K, strideB=K * N,
+           strideC=M * N)
+    Cn = C.cpu().numpy()
+    for z in range(bs):
+        assert O.rel_frob(Cn[z], A[z].astype(np.float64) @ B[z]) <= 1e-5, z
+    for half in (False, True):
+        M, N, K = 1024, 1024, 512
+        A = rng.standard_normal((M, K)).astype(np.float32)
+        B = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
+        buf = torch.zeros(M * K + 1, dtype=torch.float32, device=dev)
+        buf[1:] = torch.from_numpy(A.reshape(-1)).to(dev)
+        if half:
+            buf = buf.half()
+        ad = buf[1:].view(M, K)
+        bd = torch.from_numpy(B).to(dev)
+        bd = bd.half() if half else bd
+        C = _nan_like(dev, M, N)
+        G.gemm(ad, bd, C)
+        Ar, Br = (O.round_f16(A, False), O.round_f16(B, False)) if half else (A, B)
+        rows = rng.choice(M, 16, replace=False)
+        assert O.rel_frob(C.cpu().numpy()[rows], O.gemm_f64_rows(Ar, Br, rows)) <= 1e-5, half
+
+
+def test_unaligned_gemm_under_graph_capture(dev):
+    """Under HIP graph capture an unaligned GEMM takes the element-wise-load kernel (the
+    packed path's scratch could need an allocation): the captured graph replays correctly."""
+    import torch
+
+    rng = np.random.default_rng(23)
+    M, N, K = 777, 1234, 1027
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
+    ad = torch.from_numpy(A).to(dev).half()
+    bd = torch.from_numpy(B).to(dev).half()
+    C = _nan_like(dev, M, N)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        G.gemm(ad, bd, C)
+    torch.cuda.synchronize()
+    rows = rng.choice(M, 16, replace=False)
+    for rep in range(2):
+        C.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        Cn = C.cpu().numpy()
+        assert np.isfinite(Cn).all(), rep
+        err = O.rel_frob(Cn[rows], O.gemm_f64_rows(O.round_f16(A, False), O.round_f16(B, False), rows))
+        assert err <= 1e-5, (rep, err)
+
+
 def test_f32_transpose_variants_bit_identical(dev):
     """All four load paths feed MFMA the same operands in the same order."""
     rng = np.random.default_rng(5)
