@@ -1271,15 +1271,24 @@ hipError_t pick_f16(const GemmParams &p, long batch, hipStream_t s) {
 //  * 128 x 128: 8 waves (2 x 4, or 4 x 2 for a K-contiguous B) when one round holds every
 //    tile, else 4 waves with two workgroups per CU;
 //  * 64 x 64, 4 waves, up to five workgroups per CU.
+struct F32Costs {
+  double c256, c128, c64;
+  double best() const { return fmin(c256, fmin(c128, c64)); }
+};
+inline F32Costs f32_ring_costs(long M, long N, long batch) {
+  const long tiles256 = ((M + 255) / 256) * ((N + 255) / 256) * batch;
+  const long tiles128 = ((M + 127) / 128) * ((N + 127) / 128) * batch;
+  const long tiles64 = ((M + 63) / 64) * ((N + 63) / 64) * batch;
+  auto cost = [](long tiles, double area, double eff) { return (double)((tiles + 255) / 256) * area / eff; };
+  return {cost(tiles256, 256.0 * 256.0, 0.95), cost(tiles128, 128.0 * 128.0, tiles128 <= 256 ? 0.89 : 0.93),
+          cost(tiles64, 64.0 * 64.0, 0.88)};
+}
+
 template <bool TA, bool TB>
 hipError_t launch_f32_ring_best(const GemmParams &p, long batch, hipStream_t s) {
-  const long tiles256 = ((p.M + 255) / 256) * ((p.N + 255) / 256) * batch;
   const long tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
-  const long tiles64 = ((p.M + 63) / 64) * ((p.N + 63) / 64) * batch;
-  auto cost = [](long tiles, double area, double eff) { return (double)((tiles + 255) / 256) * area / eff; };
-  const double c256 = cost(tiles256, 256.0 * 256.0, 0.95);
-  const double c128 = cost(tiles128, 128.0 * 128.0, tiles128 <= 256 ? 0.89 : 0.93);
-  const double c64 = cost(tiles64, 64.0 * 64.0, 0.88);
+  const F32Costs k = f32_ring_costs(p.M, p.N, batch);
+  const double c256 = k.c256, c128 = k.c128, c64 = k.c64;
   if (c256 <= c128 && c256 <= c64) {
     if constexpr (!TA && !TB) return launch_f32_ring<256, 256, 2, 4, TA, TB>(p, batch, s);
     else return launch_f32_ring<256, 256, 4, 2, TA, TB>(p, batch, s);
@@ -1417,6 +1426,121 @@ __global__ void gemm_k0_kernel(GemmParams p, long batch) {
   }
 }
 
+// ------------------------------------------------------------------ split-K
+// A product with few output tiles and a long K leaves most CUs idle (512 x 4096 x 11008
+// fp16: 128 tiles of 128 x 128 for 256 CUs). It runs instead as S slices of K: one launch of
+// the aligned kernels computes every slice's partial product P_s = op(A)[:, slice s] op(B)[slice
+// s, :] into its own fp32 M x N buffer (slice s is batch index s, through the batch strides),
+// then splitk_reduce_kernel writes C = act(alpha (P_0 + P_1 + ... + P_{S-1}) + beta C + bias),
+// summing the partials in slice order, so the result does not depend on timing. It differs
+// from the one-launch product only in where the K sum is rounded.
+template <bool VEC, int ACT>
+__global__ void __launch_bounds__(256)
+    splitk_reduce_kernel(const float *__restrict__ P, int S, long M, long N, float *C, long ldc, float alpha,
+                         float beta, const float *__restrict__ bias, int act_rt, float act_alpha) {
+  const long MN = M * N;
+  const int act = ACT == kActRuntime ? act_rt : ACT;
+  const long step = (long)gridDim.x * blockDim.x;
+  if constexpr (VEC) {  // N, ldc and C allow 16-byte rows
+    for (long v = blockIdx.x * (long)blockDim.x + threadIdx.x; v < MN / 4; v += step) {
+      const long i = 4 * v, r = i / N, c = i - r * N;
+      // the loads of up to eight partials are issued before their adds, which then run
+      // in slice order
+      float4_t acc = *reinterpret_cast<const float4_t *>(P + i);
+      int k = 1;
+      for (; k + 8 <= S; k += 8) {
+        float4_t x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = *reinterpret_cast<const float4_t *>(P + (k + j) * MN + i);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc += x[j];
+      }
+      for (; k < S; ++k) acc += *reinterpret_cast<const float4_t *>(P + k * MN + i);
+      float *dst = C + r * ldc + c;
+      const float4_t old = beta != 0.0f ? *reinterpret_cast<const float4_t *>(dst) : float4_t{0.f, 0.f, 0.f, 0.f};
+      float4_t o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = apply_act(act, alpha * acc[e] + beta * old[e] + (bias ? bias[c + e] : 0.0f), act_alpha);
+      *reinterpret_cast<float4_t *>(dst) = o;
+    }
+  } else {
+    for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < MN; i += step) {
+      const long r = i / N, c = i - r * N;
+      float acc = P[i];
+      int k = 1;
+      for (; k + 8 <= S; k += 8) {
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = P[(k + j) * MN + i];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc += x[j];
+      }
+      for (; k < S; ++k) acc += P[k * MN + i];
+      float *dst = C + r * ldc + c;
+      float x = alpha * acc;
+      if (beta != 0.0f) x += beta * *dst;
+      *dst = apply_act(act, x + (bias ? bias[c] : 0.0f), act_alpha);
+    }
+  }
+}
+
+hipError_t launch_splitk_reduce(const float *P, int S, const GemmParams &p, hipStream_t s) {
+  const bool vec = p.N % 4 == 0 && p.ldc % 4 == 0 && ((uintptr_t)p.C & 15) == 0;
+  const long work = vec ? p.M * p.N / 4 : p.M * p.N;
+  const dim3 grid((unsigned)std::min<long>((work + 255) / 256, 4096)), block(256);
+  auto go = [&](auto v, auto a) {
+    hipLaunchKernelGGL((splitk_reduce_kernel<decltype(v)::value, decltype(a)::value>), grid, block, 0, s, P, S, p.M,
+                       p.N, p.C, p.ldc, p.alpha, p.beta, p.bias, p.act, p.act_alpha);
+  };
+  auto pick = [&](auto v) {
+    switch (p.act) {
+      case -1: go(v, ActCode<-1>{}); break;
+      case 0: go(v, ActCode<0>{}); break;
+      case 7: go(v, ActCode<7>{}); break;
+      default: go(v, ActCode<kActRuntime>{}); break;
+    }
+  };
+  if (vec) pick(std::true_type{});
+  else pick(std::false_type{});
+  return hipGetLastError();
+}
+
+// The slice count S for a batch-1 product on the aligned path (1: no split). Candidates
+// divide K into slices of a whole number of 64-element steps, at least 512 long; each is
+// priced in microseconds as its partial launch plus the reduce, and the cheapest is taken
+// when it beats one launch by the margin. The partial launch's price is the tile model of
+// the aligned kernels (rounds of tiles times their per-round time) at batch S and the slice
+// length. fp16: cost x (Ks / 1024 x 24.9 + 13.8) us, with the cost of the 256 x 256 and
+// 128 x 128 tiles; the constants are a fit to the partial launches of nine shapes from
+// 64 x 4096 x 4096 to 2048 x 2048 x 8192 at S = 1..16. The 128 x 192 and 128 x 96 tiles
+// (K-contiguous B only) are left out so that all four transpose layouts choose the same S
+// and stay bit-identical. fp32: 219.6 us per 1024 of K per round of 256 x 256 tiles, scaled
+// by the fp32 ring's cost. The reduce: 2.5 us plus its HBM bytes at 5 TB/s. Only products
+// whose whole tile count leaves CUs idle are split (fewer than 256 tiles of 128 x 128 for
+// fp16; fp32 takes the model's word).
+int choose_split(int dtype, long M, long N, long K, bool beta) {
+  if (K < 1024 || K % 64) return 1;
+  const bool f16 = dtype == GN_F16;
+  const long tiles128 = ((M + 127) / 128) * ((N + 127) / 128);
+  if (f16 && tiles128 >= 256) return 1;
+  auto gemm_us = [&](long S) {
+    const double ks = (double)(K / S) / 1024.0;
+    if (f16) return f16_best<false>(M, N, S).cost * (ks * 24.9 + 13.8);
+    return 219.6 * f32_ring_costs(M, N, S).best() / 65536.0 * ks;
+  };
+  auto reduce_us = [&](long S) { return 2.5 + (double)(S + 1 + (beta ? 1 : 0)) * (double)(M * N) * 4.0 / 5.0e6; };
+  const double whole = gemm_us(1);
+  double best = whole * (f16 ? 0.9 : 0.95);
+  int pick = 1;
+  for (long S = 2; S <= 32; ++S) {
+    if (K % (64 * S) || K / S < 512) continue;
+    const double t = gemm_us(S) + reduce_us(S);
+    if (t < best) best = t, pick = (int)S;
+  }
+  return pick;
+}
+
 }  // namespace
 
 bool act_supported(int act) { return act == -1 || act == 0 || act == 1 || act == 2 || (act >= 4 && act <= 7); }
@@ -1473,14 +1597,27 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
     const bool b_ok = aligned(d.B, d.ldb, d.strideB) && b_contig % epv == 0;
     const size_t pack_bytes =
         (size_t)((a_ok ? 0 : d.M) + (b_ok ? 0 : d.N)) * (size_t)Kp * esz * (size_t)std::min(kMaxZ, d.batch);
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    const bool pack = !vec && (double)d.M * d.N * d.K >= (double)(1L << 24) && pack_bytes <= ((size_t)4 << 30) &&
-                      (std::max(d.M, d.N) + 63) / 64 <= 65535 &&  // the pack grid's y extent
-                      hipStreamIsCapturing(s, &cap) == hipSuccess && cap == hipStreamCaptureStatusNone;
+    const bool big = (double)d.M * d.N * d.K >= (double)(1L << 24);
+    bool pack = !vec && big && pack_bytes <= ((size_t)4 << 30) &&
+                (std::max(d.M, d.N) + 63) / 64 <= 65535;  // the pack grid's y extent
+    // Split-K (choose_split) for a batch-1 product on the aligned path, packed or not, whose
+    // operands suit the DMA ring; the partial products take S x M x N floats of the scratch,
+    // ahead of the packed copies.
+    const long k_aligned = (!a_ok && !b_ok) ? Kp : d.K;  // the K the aligned kernels see
+    int S = 1;
+    if (d.batch == 1 && big && (vec || pack) && (a_ok ? d.lda : Kp) < (1L << 21) && (b_ok ? d.ldb : Kp) < (1L << 21))
+      S = choose_split(d.dtype, d.M, d.N, k_aligned, d.beta != 0.0f);
+    const size_t part_bytes = S > 1 ? ((size_t)S * d.M * d.N * sizeof(float) + 255) / 256 * 256 : 0;
+    if (part_bytes > ((size_t)1 << 30)) S = 1;
+    if (pack || S > 1) {  // the scratch may need an allocation, which graph capture must not see
+      hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) pack = false, S = 1;
+    }
+    const size_t ws_bytes = (pack ? pack_bytes : 0) + (S > 1 ? part_bytes : 0);
     std::unique_lock<std::mutex> lk;
     char *ws = nullptr;
-    if (pack) {
-      ws = static_cast<char *>(stream_scratch(s, pack_bytes, lk, err));
+    if (ws_bytes) {
+      ws = static_cast<char *>(stream_scratch(s, ws_bytes, lk, err));
       if (!ws) return -3;
     }
     e = hipSuccess;
@@ -1490,12 +1627,12 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
       q.B = static_cast<const char *>(d.B) + z0 * d.strideB * (long)esz;
       q.C = d.C + z0 * d.strideC;
       const long nb = std::min(kMaxZ, d.batch - z0);
-      if (!pack) {
+      if (!pack && S == 1) {
         e = vec ? dispatch<true>(d, q, nb, s) : dispatch<false>(d, q, nb, s);
         continue;
       }
       GemmDesc dp = d;
-      char *next = ws;
+      char *next = ws + (S > 1 ? part_bytes : 0);
       if (!a_ok) {
         e = esz == 2 ? launch_pack<_Float16>(q.A, d.M, d.K, d.lda, d.strideA, d.ta, next, Kp, nb, s)
                      : launch_pack<float>(q.A, d.M, d.K, d.lda, d.strideA, d.ta, next, Kp, nb, s);
@@ -1514,7 +1651,28 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
         dp.tb = true;
       }
       if (!a_ok && !b_ok) q.K = Kp;  // both padded with zeros: whole K-tile pairs, no K tail
-      if (e == hipSuccess) e = dispatch<true>(dp, q, nb, s);
+      if (e != hipSuccess) break;
+      if (S == 1) {
+        e = dispatch<true>(dp, q, nb, s);
+        continue;
+      }
+      // slice s of K is batch index s: A and B advance by the slice along K, the partial
+      // products are S consecutive M x N buffers; alpha, beta, bias and the activation wait
+      // for the reduce
+      GemmParams r = q;
+      const long ks = q.K / S;
+      r.K = ks;
+      r.alpha = 1.0f;
+      r.beta = 0.0f;
+      r.bias = nullptr;
+      r.act = -1;
+      r.C = reinterpret_cast<float *>(ws);
+      r.ldc = d.N;
+      r.strideC = d.M * d.N;
+      r.strideA = dp.ta ? ks * q.lda : ks;
+      r.strideB = dp.tb ? ks : ks * q.ldb;
+      e = dispatch<true>(dp, r, S, s);
+      if (e == hipSuccess) e = launch_splitk_reduce(r.C, S, q, s);
     }
   }
   if (e != hipSuccess) return hip_error(err, -6, "gemm launch", e);

@@ -337,6 +337,125 @@ def test_unaligned_packed_alpha_beta_bias_act(dev, dtype, M, N, K, tA, tB):
     assert row_err <= 1e-5 and col_err <= 1e-5, (row_err, col_err)
 
 
+@pytest.mark.parametrize("dtype,M,N,K,tA,tB", [(G.GN_F16, 300, 1000, 8192, False, False), (G.GN_F16, 300, 1000, 8192, False, True),
+                                                 (G.GN_F16, 300, 1000, 8192, True, False), (G.GN_F16, 300, 1000, 8192, True, True),
+                                                 (G.GN_F32, 300, 1000, 8192, False, False), (G.GN_F32, 300, 1000, 8192, True, True),
+                                                 (G.GN_F16, 512, 512, 16384, False, True), (G.GN_F32, 64, 4096, 4096, True, False)])
+def test_splitk_alpha_beta_bias_act(dev, dtype, M, N, K, tA, tB):
+    """Few output tiles and a long K: the product runs as slices of K into fp32 partial
+    buffers and a reduce applies alpha, beta*C, bias and GELU. Every row against float64 of
+    the rounded inputs, and whole-output row and column sums without the epilogue."""
+    import torch
+
+    rng = np.random.default_rng(M * 7 + N + K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    half = dtype == G.GN_F16
+    ad = torch.from_numpy(_stored(A, tA)).to(dev)
+    bd = torch.from_numpy(_stored(B, tB)).to(dev)
+    if half:
+        ad, bd = ad.half(), bd.half()
+    Ar, Br = (O.round_f16(A, False), O.round_f16(B, False)) if half else (A, B)
+    C = torch.from_numpy(C0).to(dev)
+    _say("split-K", dtype, M, N, K, tA, tB)
+    G.gemm(ad, bd, C, transA=tA, transB=tB, alpha=0.5, beta=0.25, bias=torch.from_numpy(bias).to(dev), act=G.ACT_GELU)
+    Cn = C.cpu().numpy()
+    assert np.isfinite(Cn).all()
+    rows = np.arange(M) if M * N * K <= (1 << 32) else rng.choice(M, 48, replace=False)
+    pre = 0.5 * O.gemm_f64_rows(Ar, Br, rows) + 0.25 * C0[rows].astype(np.float64) + bias
+    assert O.rel_frob(Cn[rows], O.act_f64(G.ACT_GELU, pre)) <= 1e-5
+    C2 = _nan_like(dev, M, N)
+    G.gemm(ad, bd, C2, transA=tA, transB=tB)
+    row_err, col_err = _sum_invariants(ad, bd, C2, tA, tB)
+    assert row_err <= 1e-5 and col_err <= 1e-5, (row_err, col_err)
+
+
+@pytest.mark.parametrize("dtype", [G.GN_F16, G.GN_F32])
+def test_splitk_layouts_bit_identical_and_repeatable(dev, dtype):
+    """The slice count does not depend on the layout, and the partials are summed in slice
+    order: all four transpose layouts of a split product, each called twice, give one result."""
+    import torch
+
+    rng = np.random.default_rng(91)
+    M, N, K = 300, 1000, 8192
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    outs = []
+    for tA, tB in VARIANTS:
+        ad = torch.from_numpy(_stored(A, tA)).to(dev)
+        bd = torch.from_numpy(_stored(B, tB)).to(dev)
+        if dtype == G.GN_F16:
+            ad, bd = ad.half(), bd.half()
+        for _ in range(2):
+            C = _nan_like(dev, M, N)
+            G.gemm(ad, bd, C, transA=tA, transB=tB)
+            outs.append(C.cpu().numpy())
+    _say("split-K layouts", dtype, [bool(np.array_equal(o, outs[0])) for o in outs])
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])
+
+
+def test_splitk_linear_backward_shape_relu(dev):
+    """grad_input = G W^T of the 512 x 11008 -> 4096 linear layer (fp16, K = 11008 split in
+    four), ReLU epilogue: sampled rows against float64 and whole-output sums."""
+    import torch
+
+    rng = np.random.default_rng(23)
+    M, N, K = 512, 4096, 11008
+    Gd = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(dev).half()
+    W = torch.from_numpy((0.02 * rng.standard_normal((N, K))).astype(np.float32)).to(dev).half()
+    C = _nan_like(dev, M, N)
+    G.gemm(Gd, W, C, transB=True, act=G.ACT_RELU)
+    Cn = C.cpu().numpy()
+    rows = np.concatenate([np.arange(0, 4), rng.choice(M, 12, replace=False), np.arange(M - 4, M)])
+    Ar = Gd.float().cpu().numpy()
+    Br = W.float().cpu().numpy().T.copy()
+    assert O.rel_frob(Cn[rows], np.maximum(O.gemm_f64_rows(Ar, Br, rows), 0.0)) <= 1e-5
+    C2 = _nan_like(dev, M, N)
+    G.gemm(Gd, W, C2, transB=True)
+    row_err, col_err = _sum_invariants(Gd, W, C2, False, True)
+    assert row_err <= 1e-5 and col_err <= 1e-5, (row_err, col_err)
+
+
+def test_splitk_shape_under_graph_capture(dev):
+    """Under HIP graph capture the split (whose scratch may need an allocation) is not taken:
+    the captured product replays within tolerance of float64, the same on every replay."""
+    import torch
+
+    rng = np.random.default_rng(29)
+    M, N, K = 300, 1000, 8192
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    ad = torch.from_numpy(A).to(dev).half()
+    bd = torch.from_numpy(B).to(dev).half()
+    C = torch.empty(M, N, device=dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        G.gemm(ad, bd, C)  # eager, split
+    torch.cuda.synchronize()
+    eager = C.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        G.gemm(ad, bd, C)
+    torch.cuda.synchronize()
+    ref = O.gemm_f64_rows(O.round_f16(A, False), O.round_f16(B, False), np.arange(M))
+    reps = []
+    for rep in range(3):
+        C.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        reps.append(C.cpu().numpy())
+        _say("captured split-K shape, replay", rep)
+        assert O.rel_frob(reps[-1], ref) <= 1e-5
+    for r in reps[1:]:
+        np.testing.assert_array_equal(r, reps[0])
+    assert O.rel_frob(eager.cpu().numpy(), ref) <= 1e-5
+
+
 def test_unaligned_packed_batched_and_offset_pointer(dev):
     """The packed path with a batch (strides of unaligned rows) and an aligned shape whose A
     starts one element into its buffer (so no 16-byte loads), fp32 and fp16."""
