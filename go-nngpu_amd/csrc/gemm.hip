@@ -1378,26 +1378,38 @@ __global__ void __launch_bounds__(256) pack_kcontig_kernel(const T *__restrict__
   src += (long)blockIdx.z * sstride;
   dst += (long)blockIdx.z * dstride;
   if constexpr (TRANS) {
+    // all 16 loads of a thread are issued before the first LDS store
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-    for (int i = ty; i < 64; i += 4) {
-      const long k = k0 + i, r = r0 + tx;
-      tile[i][tx] = (k < K && r < rows) ? src[k * ld + r] : T(0);
+    const long r = r0 + tx;
+    T x[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const long k = k0 + ty + 4 * u;
+      x[u] = (k < K && r < rows) ? src[k * ld + r] : T(0);
     }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) tile[ty + 4 * u][tx] = x[u];
     __syncthreads();
   }
   const int vr = threadIdx.x / VPR, vc = (threadIdx.x % VPR) * VL;
   const long k = k0 + vc;
   if (k >= Kp) return;  // Kp is a multiple of 64 here, so a vector never straddles it
-  for (int i = vr; i < 64; i += RPP) {
+  constexpr int NP = 64 / RPP;  // passes over the tile's rows
+  vec_t v[NP];
+#pragma unroll
+  for (int u = 0; u < NP; ++u) {
+    const int i = vr + u * RPP;
     const long r = r0 + i;
-    if (r >= rows) break;
-    vec_t v;
 #pragma unroll
     for (int j = 0; j < VL; ++j) {
-      if constexpr (TRANS) v[j] = tile[vc + j][i];
-      else v[j] = k + j < K ? src[r * ld + k + j] : T(0);
+      if constexpr (TRANS) v[u][j] = tile[vc + j][i];
+      else v[u][j] = (r < rows && k + j < K) ? src[r * ld + k + j] : T(0);
     }
-    *reinterpret_cast<vec_t *>(dst + r * Kp + k) = v;
+  }
+#pragma unroll
+  for (int u = 0; u < NP; ++u) {
+    const long r = r0 + vr + u * RPP;
+    if (r < rows) *reinterpret_cast<vec_t *>(dst + r * Kp + k) = v[u];
   }
 }
 
