@@ -25,8 +25,15 @@ semantics) on a bounded row sample of the headline problem, on the host cores.
 C ABI, PCIe included: upload fp32 A and B (create_gpu_buffer), cast both to fp16 on
 the device, GEMM, download C (retrieve_gpu_buffer_data), wall-clock per step.
 
-`--only a,b,...` runs a subset of {c3, c2, c1, c4, spmm, spmv, e2e, copy} (used by the
-rocprofv3 passes that produce profiles/); `copy` is a 1 GiB device copy used to
+`ceiling` (in `secondary`, and `roofline.measured_ceiling_tflops`): the sustained rate of
+the GEMM's matrix instruction with register operands and no memory traffic
+(go-nngpu_amd/lib/mfma_ceiling, run as a child process right after the headline), on
+operands with the headline's distributions and on all-zero operands. Under the board's
+power limit the clock, and so this rate, depends on the operand values; the first figure
+is the most any GEMM on such data can reach on the box.
+
+`--only a,b,...` runs a subset of {c3, ceiling, c2, c1, c4, spmm, spmv, e2e, copy} (used by
+the rocprofv3 passes that produce profiles/); `copy` is a 1 GiB device copy used to
 calibrate the HBM byte counters.
 """
 import argparse
@@ -45,7 +52,7 @@ PEAK_F16_TFLOPS = 2516.6  # dense MFMA fp16, 256 CU x 4096 flop/clk x 2.4 GHz
 PEAK_F32_TFLOPS = 157.3   # fp32 MFMA
 MIN_WARM_MS = 50.0        # least untimed GPU time before each timed leg (see timed())
 PEAK_HBM_GBS = 8000.0
-ALL = ("c3", "c2", "c1", "c4", "spmm", "spmv", "e2e", "copy")
+ALL = ("c3", "ceiling", "c2", "c1", "c4", "spmm", "spmv", "e2e", "copy")
 
 
 def log(*a):
@@ -478,6 +485,24 @@ def run_e2e(c, steps, warmup):
             "steps": f"upload A, B fp32 (256 MiB each), device fp16 cast, GEMM, download C fp32 (256 MiB)"}
 
 
+def run_ceiling(seconds=3.0):
+    """The register-operand MFMA rate (see the module docstring), from the probe executable."""
+    import subprocess
+
+    exe = os.path.join(ROOT, "go-nngpu_amd", "lib", "mfma_ceiling")
+    if not os.path.exists(exe):
+        raise RuntimeError(f"{exe} is missing: build it first (__graft_entry__.build() or make in go-nngpu_amd)")
+    r = subprocess.run([exe, str(seconds)], capture_output=True, text=True, timeout=120)
+    if r.returncode != 0:
+        raise RuntimeError(f"mfma_ceiling exited with {r.returncode}: {r.stderr.strip()}")
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    for k in ("gemm_data", "zero_data"):
+        res[k]["frac_of_peak"] = round(res[k]["tflops"] / PEAK_F16_TFLOPS, 4)
+    log(f"mfma ceiling: {res['gemm_data']['tflops']:.0f} TFLOP/s on the headline's data "
+        f"({res['gemm_data']['frac_of_peak']:.3f} of peak), {res['zero_data']['tflops']:.0f} on zeros")
+    return res
+
+
 def run_copy(c, steps, warmup):
     """1 GiB device-to-device copy (torch's copy kernel): calibration for the PMC byte counters."""
     n = 1 << 28
@@ -515,6 +540,8 @@ def main():
         head = run_c3(c, steps, warmup)
         secondary["c3_torch_matmul_reference"] = c.vendor_c3
         c.torch.cuda.empty_cache()
+    if "ceiling" in only:
+        secondary["mfma_power_ceiling"] = run_ceiling()
     if "c2" in only:
         secondary.update(run_c2(c, steps2, 3))
         c.torch.cuda.empty_cache()
@@ -565,6 +592,10 @@ def main():
                     "unit": "TFLOP/s", "frac": round(head["tflops"] / PEAK_F16_TFLOPS, 4),
                     "traffic": load_traffic("gemm_f16_8192_nn"),
                     "kernel": "gemm_f16_ring_kernel<256,256,2,4,NN>", "flop_per_launch": head["flop"]}
+        if "mfma_power_ceiling" in secondary:
+            ceil = secondary["mfma_power_ceiling"]["gemm_data"]["tflops"]
+            roofline["measured_ceiling_tflops"] = ceil
+            roofline["frac_of_measured_ceiling"] = round(head["tflops"] / ceil, 4)
     out = {
         "metric": METRIC,
         "value": round(head["tflops"], 2) if head else None,
