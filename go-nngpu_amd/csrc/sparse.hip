@@ -212,20 +212,24 @@ __global__ void __launch_bounds__(kBlock) spmm_band_kernel(long M, long N, long 
   *reinterpret_cast<float4_t *>(C + row * ldc + c0) = acc;
 }
 
-// The band kernel in two launches, each row's entries split at their midpoint: launch 0 sums
-// entries s .. m-1 into C, launch 1 loads that partial and adds entries m .. e-1, so each
-// output still takes one fma per entry in CSR order (the partial is stored exactly). With
-// sorted columns the first half of a row's entries gathers from the low rows of D, so the
-// D lines either launch reaches at a time are about half a band. Batches of 16 entries may
-// read indices and values past the row's end (never past nnz) and mask them, so no row ends
-// in a one-entry-at-a-time tail; only the last entries of the arrays take it.
-template <bool SECOND>
+// The band kernel in two launches over each row's entries: launch 0 sums entries s .. p-1
+// into C, launch 1 loads that partial and adds entries p .. e-1, so each output still takes
+// one fma per entry in CSR order (the partial is stored exactly) and the result is
+// bit-identical to one launch for any split point p. CUT: p is the row's first entry whose
+// column reaches kcut (K / 2), found by launch 0 and passed to launch 1 through split[row]
+// (written by the row's band-0 lanes); otherwise p is the midpoint of the row's entries. With
+// sorted columns either split keeps each launch's gathers in about half of D's rows; the
+// column cut does so exactly. Batches of 16 entries may read indices and values past the
+// row's end (never past nnz) and mask them, so no row ends in a one-entry-at-a-time tail;
+// only the last entries of the arrays take it.
+template <bool SECOND, bool CUT>
 __global__ void __launch_bounds__(kBlock) spmm_band_half_kernel(long M, long N, long K, long nnz, long row_blocks,
                                                                 const int32_t *__restrict__ rowptr,
                                                                 const int32_t *__restrict__ col,
                                                                 const float *__restrict__ val,
                                                                 const float *__restrict__ D, long ldd,
-                                                                float *__restrict__ C, long ldc, int *flags) {
+                                                                float *__restrict__ C, long ldc, int *flags, int kcut,
+                                                                int *__restrict__ split) {
   const int lane = threadIdx.x & 63;
   const int li = lane % kBandLanes;
   const long band = blockIdx.x / row_blocks;
@@ -235,13 +239,21 @@ __global__ void __launch_bounds__(kBlock) spmm_band_half_kernel(long M, long N, 
   if (row >= M || c0 >= N) return;
   int s, e;
   row_bounds(rowptr, row, nnz, s, e, flags, li == 0 && !SECOND);
-  const int m = s + ((e - s) >> 1);
-  const int lo = SECOND ? m : s, hi = SECOND ? e : m;
+  int lo, hi;
+  if constexpr (CUT) {
+    lo = SECOND ? split[row] : s;  // launch 0 wrote a position in [s, e]
+    hi = e;
+  } else {
+    const int m = s + ((e - s) >> 1);
+    lo = SECOND ? m : s;
+    hi = SECOND ? e : m;
+  }
+  constexpr bool STOP = CUT && !SECOND;  // launch 0 of the column cut ends at the first column >= kcut
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
   if (SECOND) acc = *reinterpret_cast<const float4_t *>(C + row * ldc + c0);
-  bool bad_col = false;
+  bool bad_col = false, cut = false;
   int k = lo;
-  for (; k < hi && k + kBandUnroll <= nnz; k += kBandUnroll) {
+  while (k < hi && k + kBandUnroll <= nnz) {
     int cc[kBandUnroll];
     float vv[kBandUnroll];
     float4_t dd[kBandUnroll];
@@ -250,7 +262,14 @@ __global__ void __launch_bounds__(kBlock) spmm_band_half_kernel(long M, long N, 
       cc[u] = col[k + u];
       vv[u] = val[k + u];
     }
-    const int f = hi - k < kBandUnroll ? hi - k : kBandUnroll;  // entries of this range in the batch
+    int f = hi - k < kBandUnroll ? hi - k : kBandUnroll;  // entries of this range in the batch
+    if constexpr (STOP) {
+      int g = kBandUnroll;
+#pragma unroll
+      for (int u = kBandUnroll - 1; u >= 0; --u)
+        if (cc[u] >= kcut) g = u;
+      if (g < f) f = g, cut = true;
+    }
     unsigned ok = 0;
 #pragma unroll
     for (int u = 0; u < kBandUnroll; ++u) {
@@ -269,9 +288,12 @@ __global__ void __launch_bounds__(kBlock) spmm_band_half_kernel(long M, long N, 
         acc[3] = __builtin_fmaf(vv[u], dd[u][3], acc[3]);
       }
     }
+    k += f;
+    if (cut) break;
   }
-  for (; k < hi; ++k) {  // within 16 entries of the end of the arrays
+  for (; !cut && k < hi; ++k) {  // within 16 entries of the end of the arrays
     const int c = col[k];
+    if (STOP && c >= kcut) break;
     if ((unsigned)c < (unsigned long)K) {
       const float v = val[k];
       const float4_t d = *reinterpret_cast<const float4_t *>(D + (long)c * ldd + c0);
@@ -283,6 +305,7 @@ __global__ void __launch_bounds__(kBlock) spmm_band_half_kernel(long M, long N, 
       bad_col = true;
     }
   }
+  if (STOP && band == 0 && li == 0) split[row] = k;
   if (bad_col && flags) flags[1] = 1;
   *reinterpret_cast<float4_t *>(C + row * ldc + c0) = acc;
 }
@@ -332,13 +355,31 @@ int launch_spmm(long M, long N, long K, long nnz, const int32_t *rowptr, const i
     if (row_blocks > 0x7FFFFFFFL / bands) return set_error(err, -1, "spmm: too many rows");
     const dim3 g((unsigned)(row_blocks * bands)), b(kBlock);
     if (nnz >= kSplitMinNnz) {
-      // Two launches (rows split at their entries' midpoint). C5 (65536^2, 4.3 M entries, N =
-      // 256): 463 -> 383 us; 16 entries per row 218 -> 144 us; N = 32 65 -> 54 us; K = 16384
-      // 313 -> 280 us; K = 131072 580 -> 563 us; bit-identical to one launch in every case.
-      hipLaunchKernelGGL(spmm_band_half_kernel<false>, g, b, 0, s, M, N, K, nnz, row_blocks, rowptr, col, val, D, ldd,
-                         C, ldc, flags);
-      hipLaunchKernelGGL(spmm_band_half_kernel<true>, g, b, 0, s, M, N, K, nnz, row_blocks, rowptr, col, val, D, ldd,
-                         C, ldc, flags);
+      // Two launches. With the rows split at their entries' midpoint, C5 (65536^2, 4.3 M
+      // entries, N = 256): 463 -> 383 us against one launch; 16 entries per row 218 -> 144 us;
+      // N = 32 65 -> 54 us; K = 16384 313 -> 280 us; K = 131072 580 -> 563 us; bit-identical to
+      // one launch in every case. The column cut needs the M split positions between the
+      // launches, in the stream's scratch, so graph capture (where that may allocate) keeps
+      // the midpoint.
+      hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+      std::unique_lock<std::mutex> lk;
+      int *split = nullptr;
+      if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap == hipStreamCaptureStatusNone) {
+        split = static_cast<int *>(stream_scratch(s, (size_t)M * sizeof(int), lk, err));
+        if (!split) return -3;
+      }
+      const int kcut = (int)std::min<long>(K / 2, 0x7FFFFFFFL);  // columns are int32
+      if (split) {
+        hipLaunchKernelGGL((spmm_band_half_kernel<false, true>), g, b, 0, s, M, N, K, nnz, row_blocks, rowptr, col, val,
+                           D, ldd, C, ldc, flags, kcut, split);
+        hipLaunchKernelGGL((spmm_band_half_kernel<true, true>), g, b, 0, s, M, N, K, nnz, row_blocks, rowptr, col, val,
+                           D, ldd, C, ldc, flags, kcut, split);
+      } else {
+        hipLaunchKernelGGL((spmm_band_half_kernel<false, false>), g, b, 0, s, M, N, K, nnz, row_blocks, rowptr, col,
+                           val, D, ldd, C, ldc, flags, kcut, split);
+        hipLaunchKernelGGL((spmm_band_half_kernel<true, false>), g, b, 0, s, M, N, K, nnz, row_blocks, rowptr, col, val,
+                           D, ldd, C, ldc, flags, kcut, split);
+      }
     } else {
       hipLaunchKernelGGL(spmm_band_kernel, g, b, 0, s, M, N, K, nnz, row_blocks, rowptr, col, val, D, ldd, C, ldc,
                          flags);

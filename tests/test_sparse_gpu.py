@@ -170,6 +170,49 @@ def test_spmm_two_launch_split_bit_exact(dev, N, ldd, ldc, order):
     assert np.all(C[[0, 4], :N] == 0)
 
 
+def test_spmm_column_cut_edges_bit_exact(dev):
+    """The two-launch SpMM outside graph capture cuts each row at its first column >= K / 2:
+    rows wholly below or above the cut, cuts at and around the 16-entry batch boundary, a row
+    whose first column is already past the cut (unsorted), a cut inside the arrays' last
+    16 entries, and a decreasing row-pointer pair (that row empty, flags[0]); every row bit for
+    bit against the fmaf restatement of the reference loop."""
+    import torch
+
+    rng = np.random.default_rng(77)
+    M, K, N = 2000, 3001, 64
+    cut = K // 2
+    lo = lambda n: np.sort(rng.choice(cut, n, replace=False))
+    hi = lambda n: np.sort(cut + rng.choice(K - cut, n, replace=False))
+    rows = [lo(40), hi(40), np.concatenate([lo(16), hi(20)]), np.concatenate([lo(17), hi(5)]),
+            np.concatenate([lo(15), hi(1)]), np.concatenate([hi(3), lo(30)]), np.array([cut]), np.array([cut - 1])]
+    while len(rows) < M - 1:
+        rows.append(np.sort(rng.choice(K, 40, replace=False)))
+    rows.append(np.concatenate([lo(5), hi(5)]))  # ends inside the arrays' last 16 entries
+    rp = np.concatenate([[0], np.cumsum([r.size for r in rows])]).astype(np.int32)
+    col = np.concatenate(rows).astype(np.int32)
+    val = rng.uniform(-1, 1, col.size).astype(np.float32)
+    assert col.size >= 1 << 16
+    rp[101] = rp[100] - 3  # row 100: s > e, invalid; row 101 starts 3 entries into row 99
+    s_e = []
+    for r in range(M):
+        s, e = int(rp[r]), int(rp[r + 1])
+        s_e.append((s, e) if 0 <= s <= e <= col.size else (0, 0))
+    rp_eff = np.concatenate([[0], np.cumsum([e - s for s, e in s_e])]).astype(np.int32)
+    col_eff = np.concatenate([col[s:e] for s, e in s_e]).astype(np.int32)
+    val_eff = np.concatenate([val[s:e] for s, e in s_e]).astype(np.float32)
+    D = O.normal((K, N), 4, N)
+    ref = O.spmm_f32(rp_eff, col_eff, val_eff, D, use_fma=True)
+    d = [torch.from_numpy(a).to(dev) for a in (rp, col, val, D)]
+    Cd = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+    flags = torch.zeros(2, dtype=torch.int32, device=dev)
+    _say("spmm column cut edges", col.size)
+    G.spmm_csr(M, N, K, val.size, d[0], d[1], d[2], d[3], Cd, flags)
+    assert flags.cpu().tolist() == [1, 0]
+    C = Cd.cpu().numpy()
+    np.testing.assert_array_equal(C, ref)
+    assert np.all(C[100] == 0)
+
+
 def test_spmm_with_duplicates_unsorted_columns(dev):
     rp, col, val = O.random_csr(300, 50, 20.0, seed=3, distinct=False)  # many duplicate columns
     D = O.normal((50, 256), 6, 1)
