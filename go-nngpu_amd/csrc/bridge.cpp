@@ -2,6 +2,7 @@
 // Part 1 keeps the reference bridge's names, signatures and return codes
 // (internal/cgo/metal_bridge*.m); Part 2 is the device-pointer API.
 #include <atomic>
+#include <chrono>
 #include <cstdlib>
 #include <cstring>
 #include <memory>
@@ -20,8 +21,20 @@ struct Scratch {  // device scratch released on scope exit (after the stream is 
   ~Scratch() { gn::dev_free(p); }
 };
 
+// Waits for the work enqueued on s, as the reference's waitUntilCompleted does. The stream is
+// polled for up to 5 ms before the blocking wait, whose wake-up is slower: the C5 SpMM through
+// perform_sparse_dense_matmul took 0.400 ms per synchronous call with the blocking wait alone
+// and 0.385 ms with the polling, against 0.366 ms of kernels. Longer work pays the blocking
+// wait's latency once, against milliseconds of kernel time.
 int sync(hipStream_t s, CError *err, int code) {
-  hipError_t e = hipStreamSynchronize(s);
+  const auto t0 = std::chrono::steady_clock::now();
+  hipError_t e;
+  while ((e = hipStreamQuery(s)) == hipErrorNotReady) {
+    if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(5)) {
+      e = hipStreamSynchronize(s);
+      break;
+    }
+  }
   if (e != hipSuccess) return gn::hip_error(err, code, "device execution", e);
   return 0;
 }
