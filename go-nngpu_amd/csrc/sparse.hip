@@ -8,9 +8,9 @@
 // the D lines gathered at any time fit the L2 far better than whole 1 KiB D rows do: the
 // kernel is bound by L2 refills from the Infinity Cache, and banding cuts them by a
 // quarter at N = 256. From 65536 entries up, spmm_band_half_kernel does the same in two
-// launches over the first and second half of each row's entries (the partial sum goes
-// through C), which halves the D rows each launch gathers from when columns are sorted and
-// cuts the refills by another quarter. Narrower or unaligned products use a group of LPR lanes per CSR
+// launches, each row's entries split at its first column >= K/2 (at the midpoint of its
+// entries under graph capture); the partial sum goes through C. That halves the D rows each
+// launch gathers from when columns are sorted and cuts the refills by another quarter. Narrower or unaligned products use a group of LPR lanes per CSR
 // row, lane l accumulating columns 4l..4l+3 (or column l). Each output is accumulated in
 // CSR order with one fma per entry, which reproduces the reference loop's summation
 // order exactly (bit-identical to an fmaf restatement of it, in every kernel).
