@@ -541,7 +541,11 @@ def main():
         secondary["c3_torch_matmul_reference"] = c.vendor_c3
         c.torch.cuda.empty_cache()
     if "ceiling" in only:
-        secondary["mfma_power_ceiling"] = run_ceiling()
+        try:
+            secondary["mfma_power_ceiling"] = run_ceiling()
+        except Exception as exc:  # a side measurement: the headline stands without it
+            log(f"mfma ceiling probe failed: {exc}")
+            secondary["mfma_power_ceiling_error"] = str(exc)
     if "c2" in only:
         secondary.update(run_c2(c, steps2, 3))
         c.torch.cuda.empty_cache()
