@@ -1367,16 +1367,13 @@ hipError_t dispatch(const GemmDesc &d, const GemmParams &p, long batch, hipStrea
 // run along src's rows (staging the other form too measured slower: 7.1 -> 9.7 us for a
 // 2047 x 2047 fp16 operand).
 template <typename T, bool TRANS>
-__global__ void __launch_bounds__(256) pack_kcontig_kernel(const T *__restrict__ src, long rows, long K, long ld,
-                                                           long sstride, T *__restrict__ dst, long Kp, long dstride) {
+__device__ __forceinline__ void pack_tile(const T *__restrict__ src, long rows, long K, long ld, T *__restrict__ dst,
+                                          long Kp, long tile_row, T (*tile)[65]) {
   constexpr int VL = 16 / sizeof(T);   // elements per 16-byte store
   constexpr int VPR = 64 / VL;         // vectors per tile row
   constexpr int RPP = 256 / VPR;       // tile rows per pass
   typedef T vec_t __attribute__((ext_vector_type(VL)));
-  __shared__ T tile[64][65];
-  const long r0 = (long)blockIdx.y * 64, k0 = (long)blockIdx.x * 64;
-  src += (long)blockIdx.z * sstride;
-  dst += (long)blockIdx.z * dstride;
+  const long r0 = tile_row * 64, k0 = (long)blockIdx.x * 64;
   if constexpr (TRANS) {
     // all 16 loads of a thread are issued before the first LDS store
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
@@ -1413,6 +1410,34 @@ __global__ void __launch_bounds__(256) pack_kcontig_kernel(const T *__restrict__
   }
 }
 
+// One operand: grid (Kp / 64, tile rows, batch).
+template <typename T, bool TRANS>
+__global__ void __launch_bounds__(256) pack_kcontig_kernel(const T *__restrict__ src, long rows, long K, long ld,
+                                                           long sstride, T *__restrict__ dst, long Kp, long dstride) {
+  __shared__ T tile[64][65];
+  pack_tile<T, TRANS>(src + (long)blockIdx.z * sstride, rows, K, ld, dst + (long)blockIdx.z * dstride, Kp, blockIdx.y,
+                      tile);
+}
+
+template <typename T>
+struct PackOp {
+  const T *src;
+  T *dst;
+  long rows, ld, sstride;
+};
+
+// Both operands in one launch: grid rows below ya pack A's tile rows, the rest B's (the branch
+// is uniform within a workgroup), so the two copies run side by side.
+template <typename T, bool TA, bool TB>
+__global__ void __launch_bounds__(256) pack2_kcontig_kernel(PackOp<T> a, PackOp<T> b, long K, long Kp, long ya) {
+  __shared__ T tile[64][65];
+  const long z = blockIdx.z;
+  if ((long)blockIdx.y < ya)
+    pack_tile<T, TA>(a.src + z * a.sstride, a.rows, K, a.ld, a.dst + z * a.rows * Kp, Kp, blockIdx.y, tile);
+  else
+    pack_tile<T, TB>(b.src + z * b.sstride, b.rows, K, b.ld, b.dst + z * b.rows * Kp, Kp, blockIdx.y - ya, tile);
+}
+
 template <typename T>
 hipError_t launch_pack(const void *src, long rows, long K, long ld, long sstride, bool trans, void *dst, long Kp,
                        long batch, hipStream_t s) {
@@ -1421,6 +1446,19 @@ hipError_t launch_pack(const void *src, long rows, long K, long ld, long sstride
   T *dp = static_cast<T *>(dst);
   if (trans) hipLaunchKernelGGL((pack_kcontig_kernel<T, true>), g, dim3(256), 0, s, sp, rows, K, ld, sstride, dp, Kp, rows * Kp);
   else hipLaunchKernelGGL((pack_kcontig_kernel<T, false>), g, dim3(256), 0, s, sp, rows, K, ld, sstride, dp, Kp, rows * Kp);
+  return hipGetLastError();
+}
+
+// A (M x K after op) and B (N x K after op) packed by one launch; ta / tb: the stored operand
+// is the transpose of the K-contiguous layout.
+template <typename T>
+hipError_t launch_pack2(PackOp<T> a, bool ta, PackOp<T> b, bool tb, long K, long Kp, long batch, hipStream_t s) {
+  const long ya = (a.rows + 63) / 64, yb = (b.rows + 63) / 64;
+  const dim3 g((unsigned)((Kp + 63) / 64), (unsigned)(ya + yb), (unsigned)batch), blk(256);
+  if (ta && tb) hipLaunchKernelGGL((pack2_kcontig_kernel<T, true, true>), g, blk, 0, s, a, b, K, Kp, ya);
+  else if (ta) hipLaunchKernelGGL((pack2_kcontig_kernel<T, true, false>), g, blk, 0, s, a, b, K, Kp, ya);
+  else if (tb) hipLaunchKernelGGL((pack2_kcontig_kernel<T, false, true>), g, blk, 0, s, a, b, K, Kp, ya);
+  else hipLaunchKernelGGL((pack2_kcontig_kernel<T, false, false>), g, blk, 0, s, a, b, K, Kp, ya);
   return hipGetLastError();
 }
 
@@ -1610,8 +1648,8 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
     const size_t pack_bytes =
         (size_t)((a_ok ? 0 : d.M) + (b_ok ? 0 : d.N)) * (size_t)Kp * esz * (size_t)std::min(kMaxZ, d.batch);
     const bool big = (double)d.M * d.N * d.K >= (double)(1L << 24);
-    bool pack = !vec && big && pack_bytes <= ((size_t)4 << 30) &&
-                (std::max(d.M, d.N) + 63) / 64 <= 65535;  // the pack grid's y extent
+    const long pack_grid_y = (a_ok ? 0 : (d.M + 63) / 64) + (b_ok ? 0 : (d.N + 63) / 64);
+    bool pack = !vec && big && pack_bytes <= ((size_t)4 << 30) && pack_grid_y <= 65535;
     // Split-K (choose_split) for a batch-1 product on the aligned path, packed or not, whose
     // operands suit the DMA ring; the partial products take S x M x N floats of the scratch,
     // ahead of the packed copies.
@@ -1645,19 +1683,31 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
       }
       GemmDesc dp = d;
       char *next = ws + (S > 1 ? part_bytes : 0);
+      char *a_dst = next, *b_dst = next + (a_ok ? 0 : (size_t)nb * d.M * Kp * esz);
+      if (!a_ok && !b_ok) {  // one launch for both
+        e = esz == 2 ? launch_pack2<_Float16>({static_cast<const _Float16 *>(q.A), reinterpret_cast<_Float16 *>(a_dst),
+                                               d.M, d.lda, d.strideA}, d.ta,
+                                              {static_cast<const _Float16 *>(q.B), reinterpret_cast<_Float16 *>(b_dst),
+                                               d.N, d.ldb, d.strideB}, !d.tb, d.K, Kp, nb, s)
+                     : launch_pack2<float>({static_cast<const float *>(q.A), reinterpret_cast<float *>(a_dst), d.M, d.lda,
+                                            d.strideA}, d.ta,
+                                           {static_cast<const float *>(q.B), reinterpret_cast<float *>(b_dst), d.N, d.ldb,
+                                            d.strideB}, !d.tb, d.K, Kp, nb, s);
+      } else if (!a_ok) {
+        e = esz == 2 ? launch_pack<_Float16>(q.A, d.M, d.K, d.lda, d.strideA, d.ta, a_dst, Kp, nb, s)
+                     : launch_pack<float>(q.A, d.M, d.K, d.lda, d.strideA, d.ta, a_dst, Kp, nb, s);
+      } else if (!b_ok) {
+        e = esz == 2 ? launch_pack<_Float16>(q.B, d.N, d.K, d.ldb, d.strideB, !d.tb, b_dst, Kp, nb, s)
+                     : launch_pack<float>(q.B, d.N, d.K, d.ldb, d.strideB, !d.tb, b_dst, Kp, nb, s);
+      }
       if (!a_ok) {
-        e = esz == 2 ? launch_pack<_Float16>(q.A, d.M, d.K, d.lda, d.strideA, d.ta, next, Kp, nb, s)
-                     : launch_pack<float>(q.A, d.M, d.K, d.lda, d.strideA, d.ta, next, Kp, nb, s);
-        q.A = next;
+        q.A = a_dst;
         q.lda = Kp;
         q.strideA = d.M * Kp;
         dp.ta = false;
-        next += (size_t)nb * d.M * Kp * esz;
       }
-      if (!b_ok && e == hipSuccess) {
-        e = esz == 2 ? launch_pack<_Float16>(q.B, d.N, d.K, d.ldb, d.strideB, !d.tb, next, Kp, nb, s)
-                     : launch_pack<float>(q.B, d.N, d.K, d.ldb, d.strideB, !d.tb, next, Kp, nb, s);
-        q.B = next;
+      if (!b_ok) {
+        q.B = b_dst;
         q.ldb = Kp;
         q.strideB = d.N * Kp;
         dp.tb = true;
