@@ -290,7 +290,13 @@ int gn_synchronize(void *stream, CError *err);
  * dtype GN_F16: A, B fp16, fp32 accumulate (v_mfma_f32_16x16x32_f16).
  * C and bias are fp32; bias may be NULL; beta == 0 never reads C.
  * batch >= 1 with element strides strideA/B/C between consecutive problems.
- * Codes: -1 invalid argument, -6 launch error. */
+ * Outside HIP graph capture two paths use a scratch block that the library keeps per stream
+ * (grown on demand from its pool): operands whose pointer, leading dimension or row length
+ * is not a multiple of 16 bytes, in products of at least 2^24 multiply-adds, are first
+ * copied into padded K-contiguous buffers, and batch-1 products with few output tiles and a
+ * long K are summed over slices of K (partial products, then a reduce in slice order).
+ * Under capture neither is taken, and nothing is allocated.
+ * Codes: -1 invalid argument, -3 scratch allocation failed, -6 launch error. */
 int gn_gemm(int dtype, int transA, int transB, long M, long N, long K, float alpha, const void *A, long lda,
             long strideA, const void *B, long ldb, long strideB, float beta, float *C, long ldc, long strideC,
             long batch, const float *bias, int act, float act_alpha, void *stream, CError *err);
@@ -367,7 +373,12 @@ int gn_transpose_f32(const float *in, long rows, long cols, float *out, void *st
  * Accumulates each output in CSR order with one fused multiply-add per stored entry.
  * error_flags (2 ints, may be NULL) receive nonzero values if a row pointer pair is
  * invalid ([0]) or a column index is outside [0,K) ([1]); offending rows / entries
- * contribute nothing and never cause an out-of-bounds access. */
+ * contribute nothing and never cause an out-of-bounds access. From 65536 stored entries
+ * (N >= 32, 16-byte aligned rows) it runs as two launches, each row split at its first
+ * column >= K/2; outside HIP graph capture the split positions (M ints) go through the
+ * library's per-stream scratch, under capture the rows split at the midpoint of their
+ * entries instead (no scratch). Either way the result is the same, bit for bit.
+ * Codes: -1 invalid argument, -3 scratch allocation failed, -6 launch error. */
 int gn_spmm_csr(long M, long N, long K, long nnz, const int32_t *rowptr, const int32_t *col, const float *val,
                 const float *D, long ldd, float *C, long ldc, int *error_flags, void *stream, CError *err);
 /* CSR SpMV on device arrays: y[M] = S[M,K] * x[K]; error_flags as gn_spmm_csr. */
