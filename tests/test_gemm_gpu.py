@@ -397,6 +397,35 @@ def test_splitk_layouts_bit_identical_and_repeatable(dev, dtype):
         np.testing.assert_array_equal(o, outs[0])
 
 
+@pytest.mark.parametrize("dtype", [G.GN_F16, G.GN_F32])
+def test_splitk_scalar_reduce_strided_c(dev, dtype):
+    """Split-K into an output whose row length (N = 999) and pitch (ldc = 1004) rule out
+    16-byte rows: the reduce takes its element-wise form, beta reads C through the pitch, and
+    the columns between N and ldc keep their NaN sentinel."""
+    import torch
+
+    rng = np.random.default_rng(41)
+    M, N, K, ldc = 200, 999, 8192, 1004
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    half = dtype == G.GN_F16
+    ad, bd = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
+    if half:
+        ad, bd = ad.half(), bd.half()
+    Ar, Br = (O.round_f16(A, False), O.round_f16(B, False)) if half else (A, B)
+    Cbig = torch.full((M, ldc), float("nan"), dtype=torch.float32, device=dev)
+    Cbig[:, :N] = torch.from_numpy(C0).to(dev)
+    C = Cbig[:, :N]
+    assert C.stride(0) == ldc
+    _say("split-K scalar reduce", dtype, M, N, K, ldc)
+    G.gemm(ad, bd, C, alpha=2.0, beta=-0.5, act=G.ACT_RELU)
+    out = Cbig.cpu().numpy()
+    assert np.isnan(out[:, N:]).all()
+    ref = np.maximum(2.0 * O.gemm_f64_rows(Ar, Br, np.arange(M)) - 0.5 * C0.astype(np.float64), 0.0)
+    assert O.rel_frob(out[:, :N], ref) <= 1e-5
+
+
 def test_splitk_linear_backward_shape_relu(dev):
     """grad_input = G W^T of the 512 x 11008 -> 4096 linear layer (fp16, K = 11008 split in
     four), ReLU epilogue: sampled rows against float64 and whole-output sums."""
