@@ -1566,7 +1566,8 @@ hipError_t launch_splitk_reduce(const float *P, int S, const GemmParams &p, hipS
 // 64 x 4096 x 4096 to 2048 x 2048 x 8192 at S = 1..16. The 128 x 192 and 128 x 96 tiles
 // (K-contiguous B only) are left out so that all four transpose layouts choose the same S
 // and stay bit-identical. fp32: 219.6 us per 1024 of K per round of 256 x 256 tiles, scaled
-// by the fp32 ring's cost. The reduce: 2.5 us plus its HBM bytes at 5 TB/s. Only products
+// by the fp32 ring's cost (1.1x for one 64 x 64 workgroup per CU). The reduce: 2.5 us plus
+// its HBM bytes at 5 TB/s. Only products
 // whose whole tile count leaves CUs idle are split (fewer than 256 tiles of 128 x 128 for
 // fp16; fp32 takes the model's word).
 int choose_split(int dtype, long M, long N, long K, bool beta) {
@@ -1577,7 +1578,11 @@ int choose_split(int dtype, long M, long N, long K, bool beta) {
   auto gemm_us = [&](long S) {
     const double ks = (double)(K / S) / 1024.0;
     if (f16) return f16_best<false>(M, N, S).cost * (ks * 24.9 + 13.8);
-    return 219.6 * f32_ring_costs(M, N, S).best() / 65536.0 * ks;
+    // one 64 x 64 workgroup per CU (4 waves, one per SIMD) runs about 10% below two or more
+    // co-resident ones (128 x 8192 x 8192: 142.6 us in one launch, 127.9 us for the partial
+    // launch at S = 2)
+    const long tiles64 = ((M + 63) / 64) * ((N + 63) / 64) * S;
+    return 219.6 * f32_ring_costs(M, N, S).best() / 65536.0 * ks * (tiles64 <= 256 ? 1.1 : 1.0);
   };
   auto reduce_us = [&](long S) { return 2.5 + (double)(S + 1 + (beta ? 1 : 0)) * (double)(M * N) * 4.0 / 5.0e6; };
   const double whole = gemm_us(1);
