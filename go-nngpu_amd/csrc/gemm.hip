@@ -1567,14 +1567,15 @@ hipError_t launch_splitk_reduce(const float *P, int S, const GemmParams &p, hipS
 // (K-contiguous B only) are left out so that all four transpose layouts choose the same S
 // and stay bit-identical. fp32: 219.6 us per 1024 of K per round of 256 x 256 tiles, scaled
 // by the fp32 ring's cost (1.1x for one 64 x 64 workgroup per CU). The reduce: 2.5 us plus
-// its HBM bytes at 5 TB/s. Only products
-// whose whole tile count leaves CUs idle are split (fewer than 256 tiles of 128 x 128 for
-// fp16; fp32 takes the model's word).
+// its HBM bytes at 5 TB/s. fp16 splits only products of fewer than 512 tiles of 128 x 128
+// (one round of the two-per-CU tiles), the range its model was checked on: there the split
+// won or tied on every shape measured (2048 x 2048 x 16384: 167 -> 129 us; 2048 x 2048 x 8192:
+// 90 -> 81 us); fp32 takes the model's word.
 int choose_split(int dtype, long M, long N, long K, bool beta) {
   if (K < 1024 || K % 64) return 1;
   const bool f16 = dtype == GN_F16;
   const long tiles128 = ((M + 127) / 128) * ((N + 127) / 128);
-  if (f16 && tiles128 >= 256) return 1;
+  if (f16 && tiles128 >= 512) return 1;
   auto gemm_us = [&](long S) {
     const double ks = (double)(K / S) / 1024.0;
     if (f16) return f16_best<false>(M, N, S).cost * (ks * 24.9 + 13.8);
