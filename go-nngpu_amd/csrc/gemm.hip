@@ -1484,28 +1484,40 @@ __global__ void gemm_k0_kernel(GemmParams p, long batch) {
 // then splitk_reduce_kernel writes C = act(alpha (P_0 + P_1 + ... + P_{S-1}) + beta C + bias),
 // summing the partials in slice order, so the result does not depend on timing. It differs
 // from the one-launch product only in where the K sum is rounded.
-template <bool VEC, int ACT>
+// Each thread sums one 16-byte group of four consecutive elements of the M x N partials
+// (flat index i .. i+3; the partials' stride PS is a multiple of 4, so every group is aligned,
+// and a group past M*N reads only the stride's padding). VST: N, ldc and C allow 16-byte rows,
+// so a group lies in one row of C and is stored as a vector; otherwise element by element.
+template <bool VST, int ACT>
 __global__ void __launch_bounds__(256)
-    splitk_reduce_kernel(const float *__restrict__ P, int S, long M, long N, float *C, long ldc, float alpha,
-                         float beta, const float *__restrict__ bias, int act_rt, float act_alpha) {
+    splitk_reduce_kernel(const float *__restrict__ P, int S, long PS, long M, long N, float *C, long ldc,
+                         float alpha, float beta, const float *__restrict__ bias, int act_rt, float act_alpha) {
   const long MN = M * N;
   const int act = ACT == kActRuntime ? act_rt : ACT;
   const long step = (long)gridDim.x * blockDim.x;
-  if constexpr (VEC) {  // N, ldc and C allow 16-byte rows
-    for (long v = blockIdx.x * (long)blockDim.x + threadIdx.x; v < MN / 4; v += step) {
-      const long i = 4 * v, r = i / N, c = i - r * N;
-      // the loads of up to eight partials are issued before their adds, which then run
-      // in slice order
-      float4_t acc = *reinterpret_cast<const float4_t *>(P + i);
-      int k = 1;
-      for (; k + 8 <= S; k += 8) {
-        float4_t x[8];
+  for (long v = blockIdx.x * (long)blockDim.x + threadIdx.x; 4 * v < MN; v += step) {
+    const long i = 4 * v;
+    // the loads of up to eight partials are issued before their adds, which then run in
+    // slice order
+    float4_t acc = *reinterpret_cast<const float4_t *>(P + i);
+    int k = 1;
+    for (; k + 8 <= S; k += 8) {
+      float4_t x[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = *reinterpret_cast<const float4_t *>(P + (k + j) * MN + i);
+      for (int j = 0; j < 8; ++j) x[j] = *reinterpret_cast<const float4_t *>(P + (k + j) * PS + i);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc += x[j];
-      }
-      for (; k < S; ++k) acc += *reinterpret_cast<const float4_t *>(P + k * MN + i);
+      for (int j = 0; j < 8; ++j) acc += x[j];
+    }
+    for (; k + 4 <= S; k += 4) {
+      float4_t x[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[j] = *reinterpret_cast<const float4_t *>(P + (k + j) * PS + i);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc += x[j];
+    }
+    for (; k < S; ++k) acc += *reinterpret_cast<const float4_t *>(P + k * PS + i);
+    if constexpr (VST) {
+      const long r = i / N, c = i - r * N;
       float *dst = C + r * ldc + c;
       const float4_t old = beta != 0.0f ? *reinterpret_cast<const float4_t *>(dst) : float4_t{0.f, 0.f, 0.f, 0.f};
       float4_t o;
@@ -1513,35 +1525,31 @@ __global__ void __launch_bounds__(256)
       for (int e = 0; e < 4; ++e)
         o[e] = apply_act(act, alpha * acc[e] + beta * old[e] + (bias ? bias[c + e] : 0.0f), act_alpha);
       *reinterpret_cast<float4_t *>(dst) = o;
-    }
-  } else {
-    for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < MN; i += step) {
-      const long r = i / N, c = i - r * N;
-      float acc = P[i];
-      int k = 1;
-      for (; k + 8 <= S; k += 8) {
-        float x[8];
+    } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = P[(k + j) * MN + i];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc += x[j];
+      for (int e = 0; e < 4; ++e) {
+        if (i + e >= MN) break;
+        const long r = (i + e) / N, c = (i + e) - r * N;
+        float *dst = C + r * ldc + c;
+        float x = alpha * acc[e];
+        if (beta != 0.0f) x += beta * *dst;
+        *dst = apply_act(act, x + (bias ? bias[c] : 0.0f), act_alpha);
       }
-      for (; k < S; ++k) acc += P[k * MN + i];
-      float *dst = C + r * ldc + c;
-      float x = alpha * acc;
-      if (beta != 0.0f) x += beta * *dst;
-      *dst = apply_act(act, x + (bias ? bias[c] : 0.0f), act_alpha);
     }
   }
 }
 
+// The partials' stride: M x N rounded up to a multiple of 4 floats.
+inline long splitk_stride(long M, long N) { return (M * N + 3) / 4 * 4; }
+
 hipError_t launch_splitk_reduce(const float *P, int S, const GemmParams &p, hipStream_t s) {
-  const bool vec = p.N % 4 == 0 && p.ldc % 4 == 0 && ((uintptr_t)p.C & 15) == 0;
-  const long work = vec ? p.M * p.N / 4 : p.M * p.N;
-  const dim3 grid((unsigned)std::min<long>((work + 255) / 256, 4096)), block(256);
+  const bool vst = p.N % 4 == 0 && p.ldc % 4 == 0 && ((uintptr_t)p.C & 15) == 0;
+  const long groups = (p.M * p.N + 3) / 4;
+  const dim3 grid((unsigned)std::min<long>((groups + 255) / 256, 4096)), block(256);
+  const long PS = splitk_stride(p.M, p.N);
   auto go = [&](auto v, auto a) {
-    hipLaunchKernelGGL((splitk_reduce_kernel<decltype(v)::value, decltype(a)::value>), grid, block, 0, s, P, S, p.M,
-                       p.N, p.C, p.ldc, p.alpha, p.beta, p.bias, p.act, p.act_alpha);
+    hipLaunchKernelGGL((splitk_reduce_kernel<decltype(v)::value, decltype(a)::value>), grid, block, 0, s, P, S, PS,
+                       p.M, p.N, p.C, p.ldc, p.alpha, p.beta, p.bias, p.act, p.act_alpha);
   };
   auto pick = [&](auto v) {
     switch (p.act) {
@@ -1551,7 +1559,7 @@ hipError_t launch_splitk_reduce(const float *P, int S, const GemmParams &p, hipS
       default: go(v, ActCode<kActRuntime>{}); break;
     }
   };
-  if (vec) pick(std::true_type{});
+  if (vst) pick(std::true_type{});
   else pick(std::false_type{});
   return hipGetLastError();
 }
@@ -1657,13 +1665,13 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
     const long pack_grid_y = (a_ok ? 0 : (d.M + 63) / 64) + (b_ok ? 0 : (d.N + 63) / 64);
     bool pack = !vec && big && pack_bytes <= ((size_t)4 << 30) && pack_grid_y <= 65535;
     // Split-K (choose_split) for a batch-1 product on the aligned path, packed or not, whose
-    // operands suit the DMA ring; the partial products take S x M x N floats of the scratch,
-    // ahead of the packed copies.
+    // operands suit the DMA ring; the partial products take S x M x N floats of the scratch
+    // (each M x N rounded up to a multiple of 4), ahead of the packed copies.
     const long k_aligned = (!a_ok && !b_ok) ? Kp : d.K;  // the K the aligned kernels see
     int S = 1;
     if (d.batch == 1 && big && (vec || pack) && (a_ok ? d.lda : Kp) < (1L << 21) && (b_ok ? d.ldb : Kp) < (1L << 21))
       S = choose_split(d.dtype, d.M, d.N, k_aligned, d.beta != 0.0f);
-    const size_t part_bytes = S > 1 ? ((size_t)S * d.M * d.N * sizeof(float) + 255) / 256 * 256 : 0;
+    const size_t part_bytes = S > 1 ? ((size_t)S * splitk_stride(d.M, d.N) * sizeof(float) + 255) / 256 * 256 : 0;
     if (part_bytes > ((size_t)1 << 30)) S = 1;
     if (pack || S > 1) {  // the scratch may need an allocation, which graph capture must not see
       hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
@@ -1736,7 +1744,7 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
       r.act = -1;
       r.C = reinterpret_cast<float *>(ws);
       r.ldc = d.N;
-      r.strideC = d.M * d.N;
+      r.strideC = splitk_stride(d.M, d.N);
       r.strideA = dp.ta ? ks * q.lda : ks;
       r.strideB = dp.tb ? ks : ks * q.ldb;
       e = dispatch<true>(dp, r, S, s);
