@@ -100,6 +100,48 @@ def test_injected_allocation_failure_is_clean(dev):
     assert out.returncode == 0 and "OK" in out.stdout, out.stderr[-2000:]
 
 
+def test_scratch_allocation_failure_is_clean(dev):
+    """The GEMM's split-K partials and the SpMM's split positions live in a per-stream scratch
+    block; when that allocation fails (injected) the call returns -3 with a message before
+    anything is launched, and calls that need no scratch keep working."""
+    code = textwrap.dedent(f"""
+        import sys
+        sys.path.insert(0, {os.path.join(ROOT, 'go-nngpu_amd')!r})
+        import numpy as np, torch, gonngpu as G
+        G.init()
+        a = torch.randn(300, 8192, device="cuda").half()
+        b = torch.randn(8192, 1000, device="cuda").half()
+        c = torch.zeros(300, 1000, device="cuda")
+        try:
+            G.gemm(a, b, c)  # few tiles, long K: split-K, partials in the scratch
+            raise SystemExit("split-K GEMM did not fail")
+        except G.GonngpuError as e:
+            assert e.code == -3 and "injected" in e.message, e
+        M, K, N = 2000, 3000, 64
+        rp = np.arange(0, 40 * (M + 1), 40, dtype=np.int32)
+        col = np.tile(np.arange(0, 3000, 75, dtype=np.int32), M)
+        val = np.ones(col.size, np.float32)
+        d = [torch.from_numpy(x).cuda() for x in (rp, col, val)]
+        D = torch.ones(K, N, device="cuda")
+        C = torch.zeros(M, N, device="cuda")
+        try:
+            G.spmm_csr(M, N, K, val.size, d[0], d[1], d[2], D, C)  # 80000 entries: split positions in the scratch
+            raise SystemExit("two-launch SpMM did not fail")
+        except G.GonngpuError as e:
+            assert e.code == -3 and "injected" in e.message, e
+        x = torch.randn(64, 64, device="cuda")
+        y = torch.empty(64, 64, device="cuda")
+        G.gemm(x, x, y)  # no scratch needed
+        torch.cuda.synchronize()
+        assert torch.allclose(y, x @ x, rtol=1e-4, atol=1e-4)
+        assert torch.count_nonzero(c).item() == 0 and torch.count_nonzero(C).item() == 0
+        print("OK")
+    """)
+    env = dict(os.environ, GONNGPU_FAIL_ALLOC_AFTER="0")
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=180)
+    assert out.returncode == 0 and "OK" in out.stdout, (out.stdout[-1000:], out.stderr[-2000:])
+
+
 def test_release_is_stream_ordered(dev):
     """gn_free / release_gpu_buffer do not wait: a block freed while kernels on the library
     stream still read it goes to a new owner only after they have finished. Here A is freed
