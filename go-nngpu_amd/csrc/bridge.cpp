@@ -6,6 +6,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <memory>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
@@ -34,6 +35,7 @@ int sync(hipStream_t s, CError *err, int code) {
       e = hipStreamSynchronize(s);
       break;
     }
+    std::this_thread::yield();  // threads waiting side by side leave the CPU (and the stream) to each other
   }
   if (e != hipSuccess) return gn::hip_error(err, code, "device execution", e);
   return 0;
