@@ -1164,13 +1164,13 @@ struct F16Choice {
   F16Tile tile;
 };
 
-inline double f16_rounds1(long t, double r) {
+inline double f16_rounds1(long t, double r, double fl = 0.75) {
   const long u = t % 256;
-  return (double)(t / 256) * r + (u ? r * fmax(0.75, u / 256.0) : 0.0);
+  return (double)(t / 256) * r + (u ? r * fmax(fl, u / 256.0) : 0.0);
 }
-inline double f16_rounds2(long t, double r2, double r1) {
+inline double f16_rounds2(long t, double r2, double r1, double fl = 0.75) {
   const long u = t % 512;
-  return (double)(t / 512) * r2 + (u == 0 ? 0.0 : u <= 256 ? r1 * fmax(0.75, u / 256.0) : r2 * fmax(0.75, u / 512.0));
+  return (double)(t / 512) * r2 + (u == 0 ? 0.0 : u <= 256 ? r1 * fmax(fl, u / 256.0) : r2 * fmax(fl, u / 512.0));
 }
 
 template <bool TB>
@@ -1178,14 +1178,20 @@ F16Choice f16_best(long M, long N, long batch) {
   const long tiles256 = ((M + 255) / 256) * ((N + 255) / 256) * batch;
   const long tiles128 = ((M + 127) / 128) * ((N + 127) / 128) * batch;
   F16Choice b{f16_rounds1(tiles256, 1.0), F16Tile::k256};
-  const double c128 = tiles128 <= 256 ? f16_rounds1(tiles128, 0.508) : f16_rounds2(tiles128, 0.638, 0.52);
+  // When one round of 128 x 128 tiles holds the product, the smaller tiles' partial rounds
+  // are priced as full ones: the 0.75 floor models the clock a power-limited round of
+  // 256 x 256 tiles gains with fewer CUs busy, and the lighter tiles did not show it (NT,
+  // forced choices, us: 2048^2 x 4096 128x128 45.0 against 128x192 on 176 CUs 47.2;
+  // 2048^3 25.7 against 27.7; 1536^2 x 4096 128x96 41.6 against 128x128 42.6).
+  const double fl = tiles128 <= 256 ? 1.0 : 0.75;
+  const double c128 = tiles128 <= 256 ? f16_rounds1(tiles128, 0.508, fl) : f16_rounds2(tiles128, 0.638, 0.52);
   if (c128 < b.cost) b = {c128, tiles128 <= 256 ? F16Tile::k128w8 : F16Tile::k128w4};
   if constexpr (TB) {
     // 128 x 192 and 128 x 96 only for a K-contiguous B: 384- and 192-byte MN-contiguous rows
     // would not take the 32-byte block swizzle of the transposing reads.
     const long tiles192 = ((M + 127) / 128) * ((N + 191) / 192) * batch;
     const long tiles96 = ((M + 127) / 128) * ((N + 95) / 96) * batch;
-    const double c192 = f16_rounds1(tiles192, 0.509), c96 = f16_rounds2(tiles96, 0.542, 0.43);
+    const double c192 = f16_rounds1(tiles192, 0.509, fl), c96 = f16_rounds2(tiles96, 0.542, 0.43, fl);
     if (c192 < b.cost) b = {c192, F16Tile::k192};
     if (c96 < b.cost) b = {c96, F16Tile::k96};
   }
