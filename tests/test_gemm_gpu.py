@@ -824,6 +824,34 @@ def test_f16_ring_transpose_variants_bit_identical(dev):
         np.testing.assert_array_equal(o, outs[0])
 
 
+@pytest.mark.parametrize("M,N,K", [(2048, 2048, 1024), (1536, 1536, 512)])
+def test_f16_one_round_tiles_all_layouts(dev, M, N, K):
+    """Products that one round of 128x128 tiles holds: 2048^2 runs on 128x128 tiles with 8
+    waves in every layout; 1536^2 on 128x96 tiles when B is K-contiguous and 128x128
+    otherwise. The four layouts must agree bit for bit, start from NaN, and match float64 of
+    the fp16-rounded inputs in whole-output row and column sums and on sampled rows."""
+    import torch
+
+    rng = np.random.default_rng(M + K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
+    outs = []
+    for tA, tB in VARIANTS:
+        ad = torch.from_numpy(_stored(A, tA)).to(dev).half()
+        bd = torch.from_numpy(_stored(B, tB)).to(dev).half()
+        C = _nan_like(dev, M, N)
+        _say("one-round tiles", M, N, K, tA, tB)
+        G.gemm(ad, bd, C, transA=tA, transB=tB)
+        row_err, col_err = _sum_invariants(ad, bd, C, tA, tB)
+        assert row_err <= 1e-5 and col_err <= 1e-5, (tA, tB, row_err, col_err)
+        outs.append(C.cpu().numpy())
+    rows = np.concatenate([np.arange(0, 3), rng.choice(M, 8, replace=False), np.arange(M - 3, M)])
+    ref = O.gemm_f64_rows(O.round_f16(A, False), O.round_f16(B, False), rows)
+    assert O.rel_frob(outs[0][rows], ref) <= 1e-5
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])
+
+
 def test_f16_row_split_all_transposes_bit_identical(dev):
     """A shape whose last round of 256x256 tiles would be mostly empty (4600 x 4608: 18 x 18
     tiles) runs as two launches over row blocks: rows below 3072 (NN, TN) or 3584 (NT, TT) on
