@@ -56,13 +56,16 @@ bool fits(const Buffer *b, long rows, long cols, size_t esz) {
 // entry), or when gn_csr_indices_changed is called for it. Row pointers are compared
 // on every call (4(rows+1) bytes); column indices changed in place under an unchanged
 // values buffer need gn_csr_indices_changed, just as changed values need a new upload.
+// The validation checks the indices against the call's column count (K), so an entry
+// counts as validated only for the K it was checked against: a call with another K
+// validates again.
 // GONNGPU_CSR_CACHE=0 turns the cache off (upload and validate on every call).
 struct CsrEntry {
   const int *host_rp = nullptr, *host_col = nullptr;
   long rows = 0, nnz = 0;
   std::vector<int> rp_copy;
   void *d_rp = nullptr, *d_col = nullptr;
-  std::atomic<bool> validated{false};
+  std::atomic<long> validated_bound{-1};  // the K the indices were checked against (-1: none)
   ~CsrEntry() {  // stream-ordered: after every call already enqueued with this entry
     gn::dev_free(d_rp);
     gn::dev_free(d_col);
@@ -135,8 +138,8 @@ void csr_cache_forget(const Buffer *key, const CsrEntry *only) {
 // reference's error convention. fn must only write its outputs, so enqueuing it a second
 // time gives the same result.
 template <typename Fn>
-int with_csr(const Buffer *values, const int *rowptr, long rows, const int *cols, long nnz, hipStream_t s,
-             CError *err, Fn fn) {
+int with_csr(const Buffer *values, const int *rowptr, long rows, const int *cols, long nnz, long bound,
+             hipStream_t s, CError *err, Fn fn) {
   const auto bad = [&](int f0, int f1) {
     if (f0) return set_error(err, -3, "malformed CSR: row pointers are not monotone within [0, nnz]");
     if (f1) return set_error(err, -3, "malformed CSR: column index outside [0, cols)");
@@ -150,8 +153,8 @@ int with_csr(const Buffer *values, const int *rowptr, long rows, const int *cols
     // stays in bounds: the stale indices were validated for the same rows and nnz, and
     // the kernels check every column against this call's K.
     std::shared_ptr<CsrEntry> cur = csr_lookup(values);
-    if (cur && cur->validated.load(std::memory_order_acquire) && cur->host_rp == rowptr && cur->host_col == cols &&
-        cur->rows == rows && cur->nnz == nnz) {
+    if (cur && cur->validated_bound.load(std::memory_order_acquire) == bound && cur->host_rp == rowptr &&
+        cur->host_col == cols && cur->rows == rows && cur->nnz == nnz) {
       if (int rc = fn(static_cast<const int32_t *>(cur->d_rp), static_cast<const int32_t *>(cur->d_col), nullptr))
         return rc;
       if (memcmp(cur->rp_copy.data(), rowptr, sizeof(int) * (size_t)(rows + 1)) == 0) return sync(s, err, -6);
@@ -160,7 +163,7 @@ int with_csr(const Buffer *values, const int *rowptr, long rows, const int *cols
     std::shared_ptr<CsrEntry> e = csr_entry(values, rowptr, rows, cols, nnz, s, err);
     if (!e) return -3;
     const int32_t *d_rp = static_cast<const int32_t *>(e->d_rp), *d_col = static_cast<const int32_t *>(e->d_col);
-    if (e->validated.load(std::memory_order_acquire)) {
+    if (e->validated_bound.load(std::memory_order_acquire) == bound) {
       if (int rc = fn(d_rp, d_col, nullptr)) return rc;
       return sync(s, err, -6);
     }
@@ -176,7 +179,7 @@ int with_csr(const Buffer *values, const int *rowptr, long rows, const int *cols
       csr_cache_forget(values, e.get());
       return rc;
     }
-    e->validated.store(true, std::memory_order_release);
+    e->validated_bound.store(bound, std::memory_order_release);
     return 0;
   }
   Scratch d_rp, d_col, d_flags;
@@ -248,6 +251,8 @@ int download_coo(const Scratch &ri, const Scratch &ci, const Scratch &vv, long n
 }  // namespace
 
 void gn::csr_cache_drop(const Buffer *b) { csr_cache_forget(b, nullptr); }
+int gn::sync_stream(hipStream_t s, CError *err, int code) { return sync(s, err, code); }
+bool gn::buffer_fits(const Buffer *b, long rows, long cols, size_t esz) { return fits(b, rows, cols, esz); }
 
 extern "C" {
 
@@ -409,7 +414,7 @@ int perform_sparse_dense_matmul(GPUPtr aValuesPtr, int *aRowPtr, long aRowPtrLen
   if (!fits(b, bRows, bCols, 4) || !fits(c, resultRows, resultCols, 4) || (v && !fits(v, 1, aNNZ, 4)))
     return set_error(err, -2, "Buffer smaller than the matrix it describes.");
   const float *vals = v ? static_cast<const float *>(v->dptr) : nullptr;
-  return with_csr(v, aRowPtr, aRows, aColIndices, aNNZ, ctx->stream, err,
+  return with_csr(v, aRowPtr, aRows, aColIndices, aNNZ, aCols, ctx->stream, err,
                   [&](const int32_t *rp, const int32_t *col, int *flags) -> int {
                     int rc = gn::launch_spmm(aRows, bCols, aCols, aNNZ, rp, col, vals,
                                              static_cast<const float *>(b->dptr), bCols,
@@ -436,7 +441,7 @@ int perform_sparse_matvec(GPUPtr aValuesPtr, int *aRowPtr, long aRowPtrLen, int 
   if (!fits(x, 1, xSize, 4) || !fits(y, 1, resultSize, 4) || (v && !fits(v, 1, aNNZ, 4)))
     return set_error(err, -1, "Buffer smaller than the vector it describes.");
   const float *vals = v ? static_cast<const float *>(v->dptr) : nullptr;
-  return with_csr(v, aRowPtr, aRows, aColIndices, aNNZ, ctx->stream, err,
+  return with_csr(v, aRowPtr, aRows, aColIndices, aNNZ, aCols, ctx->stream, err,
                   [&](const int32_t *rp, const int32_t *col, int *flags) -> int {
                     int rc = gn::launch_spmv(aRows, aCols, aNNZ, rp, col, vals,
                                              static_cast<const float *>(x->dptr), static_cast<float *>(y->dptr),
@@ -570,7 +575,7 @@ int perform_dense_sparse_matmul(GPUPtr aMatrixPtr, long aRows, long aCols, GPUPt
                                   err);
   if (rc) return rc;
   const float *vals = bv ? static_cast<const float *>(bv->dptr) : nullptr;
-  rc = with_csr(bv, bColPtr, bCols, bRowIndices, bNNZ, s, err,
+  rc = with_csr(bv, bColPtr, bCols, bRowIndices, bNNZ, aCols, s, err,
                 [&](const int32_t *cp, const int32_t *rows, int *flags) -> int {
                   int r = gn::launch_spmm(bCols, aRows, aCols, bNNZ, cp, rows, vals, static_cast<const float *>(at.p),
                                           aRows, static_cast<float *>(ct.p), aRows, flags, s, err);
@@ -688,7 +693,7 @@ int perform_sparse_to_dense(GPUPtr valuesPtr, int *rowPtr, long rowPtrLen, int *
     return set_error(err, -1, "Buffer smaller than the matrix it describes.");
   if (rows == 0 || cols == 0) return 0;
   const float *vals = v ? static_cast<const float *>(v->dptr) : nullptr;
-  return with_csr(v, rowPtr, rows, colIndices, nnz, ctx->stream, err,
+  return with_csr(v, rowPtr, rows, colIndices, nnz, cols, ctx->stream, err,
                   [&](const int32_t *rp, const int32_t *col, int *flags) -> int {
                     return gn::launch_csr_to_dense(rows, cols, nnz, rp, col, vals, static_cast<float *>(d->dptr), flags,
                                                    ctx->stream, err);
@@ -771,6 +776,11 @@ int gn_malloc(void **ptr, size_t bytes, CError *err) {
 
 int gn_free(void *ptr) {
   if (!ptr) return 0;
+  // Device-wide: the block may have been used on any stream (the caller's own included).
+  if (hipDeviceSynchronize() != hipSuccess) {
+    (void)hipGetLastError();  // e.g. a stream capture in progress: keep the block, report it
+    return -1;
+  }
   gn::dev_free(ptr);
   return 0;
 }
@@ -783,7 +793,14 @@ int gn_csr_indices_changed(GPUPtr valuesPtr) {
 
 int gn_free_async(void *ptr, void *stream) {
   if (!ptr) return 0;
-  gn::dev_free_on(ptr, gn::resolve_stream(stream));
+  const hipStream_t s = gn::resolve_stream(stream);
+  // The release records an event that is queried later, which a capturing stream cannot do.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return -1;
+  }
+  gn::dev_free_on(ptr, s);
   return 0;
 }
 

@@ -55,6 +55,10 @@ void memory_stats(long *cur, long *peak, long *n);
 // kernel that uses the scratch is enqueued, so that another host thread cannot enqueue
 // work that reuses it in between (kernels on one stream run in order).
 void *stream_scratch(hipStream_t s, size_t bytes, std::unique_lock<std::mutex> &lk, CError *err);
+// Called with lk still held, after the kernels that use the scratch are enqueued: a block
+// above 256 MiB is released (stream-ordered) instead of being kept for the stream's next
+// call, so one large call does not pin it for the life of the process.
+void stream_scratch_trim(hipStream_t s, std::unique_lock<std::mutex> &lk);
 
 // ---------------------------------------------------------------- host <-> device
 // Synchronous copies of pageable host memory through a pinned staging ring.
@@ -133,6 +137,31 @@ int launch_dense_to_coo(bool write, long M, long N, const float *D, float thr, l
                         int32_t *ri, int32_t *ci, float *vv, hipStream_t s, CError *err);
 
 bool act_supported(int act);
+
+// compat_ops.hip: the element-wise matrix operations and activation backwards of the
+// reference bridge. op: 0 add, 1 subtract, 2 multiply, 3 divide; for division
+// *first_zero receives the lowest index with b == 0 (-1 when none), which waits for the
+// kernel.
+int launch_binary_f32(int op, const float *a, const float *b, float *c, long n, long *first_zero, hipStream_t s,
+                      CError *err);
+// c[i, j] = a[i * sa_r + j * sa_c] + b[i * sb_r + j * sb_c] over an M x N result.
+int launch_add_broadcast_f32(const float *a, long sa_r, long sa_c, const float *b, long sb_r, long sb_c, float *c,
+                             long M, long N, hipStream_t s, CError *err);
+// out = in * scalar (mul) or in + scalar.
+int launch_scalar_f32(bool mul, const float *in, float scalar, float *out, long n, hipStream_t s, CError *err);
+// gin = gradient through an activation, computed from its OUTPUT y (reference formulas).
+int launch_act_backward_from_output(const float *gout, const float *y, float *gin, long n, int act, float alpha,
+                                    hipStream_t s, CError *err);
+// gin = y * (g - dot(g, y)) per row of a [rows, cols] matrix.
+int launch_softmax_backward(const float *g, const float *y, float *gin, long rows, long cols, hipStream_t s,
+                            CError *err);
+
+// bridge.cpp helpers shared with bridge_compat.cpp.
+// Waits for the work enqueued on s, as the reference's waitUntilCompleted does; returns
+// code (with the HIP error in err) on a device error.
+int sync_stream(hipStream_t s, CError *err, int code);
+// True when buffer b holds a rows x cols matrix of esz-byte elements.
+bool buffer_fits(const Buffer *b, long rows, long cols, size_t esz);
 
 }  // namespace gn
 

@@ -1756,6 +1756,7 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
       e = dispatch<true>(dp, r, S, s);
       if (e == hipSuccess) e = launch_splitk_reduce(r.C, S, q, s);
     }
+    stream_scratch_trim(s, lk);
   }
   if (e != hipSuccess) return hip_error(err, -6, "gemm launch", e);
   return 0;

@@ -432,6 +432,10 @@ struct StreamScratch {
   size_t bytes = 0;
 };
 static std::unordered_map<hipStream_t, StreamScratch> g_scratch;
+// Scratch blocks above this size go back to the pool after the call that needed them (see
+// stream_scratch_trim): the pool's cache can hand them out again or, when hipMalloc fails,
+// return them to the driver, which it cannot do with a block a stream keeps.
+constexpr size_t kScratchRetainBytes = (size_t)256 << 20;
 
 void *stream_scratch(hipStream_t s, size_t bytes, std::unique_lock<std::mutex> &lk, CError *err) {
   lk = std::unique_lock<std::mutex>(g_scratch_mu);
@@ -448,6 +452,14 @@ void *stream_scratch(hipStream_t s, size_t bytes, std::unique_lock<std::mutex> &
     w.bytes = nb;
   }
   return w.ptr;
+}
+
+void stream_scratch_trim(hipStream_t s, std::unique_lock<std::mutex> &lk) {
+  if (!lk.owns_lock()) return;
+  auto it = g_scratch.find(s);
+  if (it == g_scratch.end() || it->second.bytes <= kScratchRetainBytes) return;
+  dev_free_on(it->second.ptr, s);  // after the kernels just enqueued; then back in the pool's cache
+  g_scratch.erase(it);
 }
 
 }  // namespace gn

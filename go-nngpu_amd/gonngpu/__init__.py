@@ -110,6 +110,25 @@ SIGNATURES = {
     "gn_spmv_csr": (_I, [_L, _L, _L, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _ERR]),
     "gn_fill_uniform_f32": (_I, [_VP, _SZ, _U64, _U64, _F, _F, _VP, _ERR]),
     "gn_fill_normal_f32": (_I, [_VP, _SZ, _U64, _U64, _F, _F, _VP, _ERR]),
+    # Part 3: the other reference-bridge entries with a device implementation. The rest of
+    # Part 3 (entries that report "not provided") has no Python binding.
+    "perform_mps_matrix_add": (_I, [_VP, _L, _L, _VP, _L, _L, _VP, _L, _L, _VP, _ERR]),
+    "perform_mps_matrix_add_broadcast": (_I, [_VP, _L, _L, _VP, _L, _L, _VP, _L, _L, _VP, _ERR]),
+    "perform_mps_matrix_subtract": (_I, [_VP, _L, _L, _VP, _L, _L, _VP, _L, _L, _VP, _ERR]),
+    "perform_mps_matrix_element_multiply": (_I, [_VP, _L, _L, _VP, _L, _L, _VP, _L, _L, _VP, _ERR]),
+    "perform_mps_matrix_element_divide": (_I, [_VP, _L, _L, _VP, _L, _L, _VP, _L, _L, _VP, _ERR]),
+    "perform_mps_matrix_scalar_add": (_I, [_VP, _L, _L, _F, _VP, _VP, _ERR]),
+    "perform_mps_matrix_scalar_multiply": (_I, [_VP, _L, _L, _F, _VP, _VP, _ERR]),
+    "perform_activation_relu_backward": (_I, [_VP, _VP, _L, _VP, _VP, _ERR]),
+    "perform_activation_sigmoid_backward": (_I, [_VP, _VP, _L, _VP, _VP, _ERR]),
+    "perform_activation_tanh_backward": (_I, [_VP, _VP, _L, _VP, _VP, _ERR]),
+    "perform_activation_softmax_1d_backward": (_I, [_VP, _VP, _L, _VP, _VP, _ERR]),
+    "perform_activation_softmax_2d_backward": (_I, [_VP, _VP, _L, _L, _VP, _VP, _ERR]),
+    "perform_activation_leaky_relu_backward": (_I, [_VP, _VP, _L, _F, _VP, _VP, _ERR]),
+    "perform_activation_elu_backward": (_I, [_VP, _VP, _L, _F, _VP, _VP, _ERR]),
+    "perform_activation_swish_backward": (_I, [_VP, _VP, _L, _VP, _VP, _ERR]),
+    "perform_activation_gelu_backward": (_I, [_VP, _VP, _L, _VP, _VP, _ERR]),
+    "getGPUMemoryUsage": (None, [ctypes.POINTER(_L), ctypes.POINTER(_L)]),
 }
 
 _lib = None

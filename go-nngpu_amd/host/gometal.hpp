@@ -85,7 +85,10 @@ class Tensor {
 
   Error EnsureGPU();   // tensor.go:113-150
   Error RetrieveCPU();  // tensor.go:154-184
-  void ReleaseGPU();   // tensor.go:189-202
+  // tensor.go:189-202. The reference's buffer aliases Data, so after the release Data
+  // holds what the device computed; here a device copy newer than Data (a GPU result not
+  // yet retrieved) is copied back first, then the allocation is returned.
+  void ReleaseGPU();
   void *GPUPtr() const { return gpuPtr_; }        // tensor.go:206
   void *DevicePtr() const { return devicePtr_; }  // tensor.go:211
   bool IsOnGPU() const { return isOnGPU_; }
@@ -100,6 +103,7 @@ class Tensor {
   void *devicePtr_ = nullptr;
   bool isOnGPU_ = false;
   bool isOwner_ = true;
+  bool hostStale_ = false;  // the device copy is newer than Data (NewDeviceResult)
   long gpuBytes_ = 0;
   void dropDeviceCopy();
 };
@@ -435,7 +439,12 @@ class GPUDense : public mat::Matrix {
   explicit GPUDense(TensorPtr t, bool transposed = false) : tensor_(std::move(t)), trans_(transposed) {}
   void Dims(int &r, int &c) const override;
   double At(int i, int j) const override;         // panics on out-of-range indices
-  std::shared_ptr<mat::Matrix> T() const override;  // transposed view of the same tensor
+  // The transpose. As in the reference (gonum-compat.go:61-68, a materialised Transpose) it
+  // behaves as an independent matrix; it starts as a view of the same tensor (so that Mul
+  // and GPUMatMul read it in place, with a transposed GEMM operand) and the two share the
+  // tensor copy-on-write: Set on either first gives it a private copy, and Mul replaces
+  // only the receiver's tensor.
+  std::shared_ptr<mat::Matrix> T() const override;
   void Set(int i, int j, double v);
   void Mul(const mat::Matrix &a, const mat::Matrix &b);  // receiver := a*b (device-resident)
   std::shared_ptr<mat::Dense> ToGonum() const;
@@ -448,6 +457,7 @@ class GPUDense : public mat::Matrix {
  private:
   TensorPtr tensor_;
   bool trans_ = false;
+  void detach();  // gives this matrix a private copy of a tensor it shares
 };
 // C = op(A) * op(B) on the device, with op(X) = X^T when the flag is set: the GEMM reads
 // the stored operands in place (device-resident fp32 result).

@@ -100,7 +100,16 @@ double GPUDense::At(int i, int j) const {
 
 std::shared_ptr<mat::Matrix> GPUDense::T() const { return std::make_shared<GPUDense>(tensor_, !trans_); }
 
+void GPUDense::detach() {
+  if (tensor_.use_count() <= 1) return;
+  if (Error e = tensor_->RetrieveCPU()) panic(e);
+  auto [t, err] = tensor::NewTensor(tensor_->Shape, tensor_->Data);
+  if (err) panic(err);
+  tensor_ = t;
+}
+
 void GPUDense::Set(int i, int j, double v) {
+  detach();  // a T() view and its parent are separate matrices (copy-on-write)
   if (Error e = tensor_->RetrieveCPU()) panic(e);
   int rows, cols;
   Dims(rows, cols);
@@ -139,7 +148,7 @@ void GPUDense::Mul(const mat::Matrix &a, const mat::Matrix &b) {
   Tensor &B = operand(b, kb, tb);
   auto [result, err] = MatMulTransposed(A, ta, B, tb);
   if (err) panic(err);
-  if (!trans_) tensor_->ReleaseGPU();  // a view's tensor belongs to its parent
+  // The old tensor goes with its last owner: a T() view taken earlier keeps it, with its data.
   tensor_ = result;  // device-resident until read
   trans_ = false;
 }
@@ -155,9 +164,7 @@ std::shared_ptr<mat::Dense> GPUDense::ToGonum() const {
   return mat::NewDense(r, c, std::move(t));
 }
 
-void GPUDense::ReleaseGPU() {
-  if (!trans_) tensor_->ReleaseGPU();
-}
+void GPUDense::ReleaseGPU() { tensor_->ReleaseGPU(); }  // Data keeps the values (Tensor::ReleaseGPU)
 
 std::shared_ptr<mat::Dense> GPUMatMul(const mat::Matrix &a, const mat::Matrix &b) {
   // gonum-compat.go:342-367 converts both operands with FromGonum; GPUDense operands and

@@ -139,6 +139,7 @@ Result<TensorPtr> Tensor::NewDeviceResult(std::vector<int> shape) {
   t->devicePtr_ = dev;
   t->gpuBytes_ = bytes;
   t->isOnGPU_ = true;
+  t->hostStale_ = true;
   track(buf, bytes);
   return {t, {}};
 }
@@ -151,11 +152,15 @@ Error Tensor::RetrieveCPU() {
   int rc = retrieve_gpu_buffer_data(gpuPtr_, Data.empty() ? nullptr : Data.data(), bytes, &e);
   if (rc != 0) return abi_error("failed to retrieve GPU buffer data", rc, e);
   isOnGPU_ = false;  // tensor.go:182; the allocation is kept until replaced or freed
+  hostStale_ = false;
   return {};
 }
 
 void Tensor::ReleaseGPU() {
-  if (isOnGPU_ && gpuPtr_ && isOwner_) dropDeviceCopy();
+  if (!(isOnGPU_ && gpuPtr_ && isOwner_)) return;
+  // Data must hold the device's results afterwards, as the reference's aliased slice does.
+  if (hostStale_ && RetrieveCPU()) return;  // keep the only valid copy if the read-back fails
+  dropDeviceCopy();
 }
 
 // ------------------------------------------------------------------ Float16Tensor

@@ -4,14 +4,21 @@
  *
  * Part 1 re-exports, with identical names and signatures, the subset of the
  * reference bridge header internal/cgo/metal_bridge.h that the matmul path binds
- * (each declaration cites the prototype it replaces). The Go call sites
- * (tensor/tensor.go:130,171,198; gpu/matrix/matrix.go:87,387;
+ * (each declaration cites the prototype it replaces): the calls of
+ * tensor/tensor.go:130,171,198; gpu/matrix/matrix.go:87,387;
  * gpu/matrix/sparse-matrix.go:167,562; gpu/matrix/optimized-kernels.go:57,118;
- * gpu/matrix/fused-operations.go:441) compile unchanged against it.
+ * gpu/matrix/fused-operations.go:441.
  *
  * Part 2 adds gn_* entry points that take raw device pointers, explicit
  * transposes, dtypes, epilogues and a HIP stream; they have no reference
  * counterpart and are what a caller that keeps data resident in HBM uses.
+ *
+ * Part 3 declares, with the reference prototypes, every other metal_bridge.h function
+ * that the Go packages gpu/matrix, gpu/optimizer and tensor call, so that with their
+ * cgo preambles pointed at this header and library (and nothing else changed in their
+ * code) they compile and link. The element-wise matrix operations and the activation
+ * backwards run on the device; the entries of subsystems outside this backend
+ * (convolution, losses, optimizers, decompositions, ...) return -1 with a message.
  *
  * Conventions shared by every entry point:
  *  - return 0 on success, a negative code on failure; on failure, if err is
@@ -27,6 +34,9 @@
 
 #include <stddef.h>
 #include <stdint.h>
+#ifndef __cplusplus
+#include <stdbool.h>
+#endif
 
 #ifdef __cplusplus
 extern "C" {
@@ -59,9 +69,9 @@ int create_gpu_buffer(float *data, long length_bytes, GPUPtr *outGPUPtr, DeviceP
  * (metal_bridge_buffer.m:65-72), -4 copy failed. */
 int retrieve_gpu_buffer_data(GPUPtr gpuPtr, float *data, long length_bytes, CError *err);
 
-/* metal_bridge.h:25. Returns the allocation to the library's pool, stream-ordered (see
- * gn_free): it does not wait, and the memory is reused only after the library stream's
- * work enqueued so far. NULL is a no-op. */
+/* metal_bridge.h:25. Returns the allocation to the library's pool, stream-ordered on the
+ * library stream (see gn_free_async): it does not wait, and the memory is reused only after
+ * the library stream's work enqueued so far (every Part-1 call runs there). NULL is a no-op. */
 int release_gpu_buffer(GPUPtr gpuPtr);
 
 /* metal_bridge.h:28-34. C[resultRows,resultCols] = A[aRows,aCols] * B[bRows,bCols],
@@ -95,11 +105,16 @@ int perform_batch_matmul_optimized(GPUPtr aPtr, GPUPtr bPtr, GPUPtr cPtr, long b
  * ActivationType codes (gpu/matrix/activation.go:20-29): 0 ReLU, 1 Sigmoid, 2 Tanh,
  * 4 LeakyReLU(alpha), 5 ELU(alpha), 6 Swish, 7 GELU (tanh form); any other code
  * (including 3 Softmax, which is not element-wise) is rejected with -1.
- * Code 6 is always Swish. The reference's Go caller sends C.int(OpReLU) for a nil
- * config.Activation (fused-operations.go:433), and OpReLU is 6 in the OpType enum
- * (gradient.go:27-39), so that unchanged call would run Swish here. The call site
- * must send ActivationType ReLU (0) for its documented "Default to ReLU"; the
- * one-line Go change is part of the integration.
+ * The reference is not consistent about these codes. Its Go caller sends the
+ * ActivationType of a non-nil config (fused-operations.go:436-439) but C.int(OpReLU) = 6
+ * (the OpType enum, gradient.go:27-39) for a nil one, commented "Default to ReLU" (:433);
+ * its kernel reads 0 ReLU, 1 LeakyReLU, 2 Sigmoid, 3 Tanh, 4 GELU and any other code as
+ * no activation (default.metal:488-506), so a nil activation would give the plain linear
+ * output, had the kernel ever loaded (its library load fails in cgo builds and the call
+ * copies the input instead, metal_bridge_fused.m:154-161). This library reads every code
+ * as an ActivationType, so code 6 is Swish, and the unchanged Go call with a nil activation
+ * runs Swish. The integration changes that one Go line to send ReLU (0), the comment's
+ * intent: a deliberate deviation from the kernel's reading (identity).
  * Codes: -1 invalid argument / NULL buffer / execution error (as the reference). */
 int perform_fused_linear_activation(GPUPtr input, long batch_size, long input_size, GPUPtr weight, long output_size,
                                     GPUPtr bias, int activation_type, float alpha, GPUPtr output, DevicePtr device,
@@ -272,12 +287,17 @@ long gn_buffer_bytes(GPUPtr buf);
 /* Live/peak bytes and live allocations of the library's device pool
  * (the GlobalMemoryPool statistics of tensor/tensor.go:65-77). */
 void gn_memory_stats(long *current_bytes, long *peak_bytes, long *num_allocations);
-/* Device memory from the library pool (caching allocator). Release is stream-ordered:
- * gn_free(ptr) hands the block to a new owner only after the work enqueued on the library
- * stream before the call has finished; gn_free_async(ptr, stream) does the same for
- * `stream` (NULL = the library stream). Neither waits. Work on any other stream that still
- * uses the block must be complete, or ordered before the block's next user, when it is
- * freed (the rule of every stream-ordered allocator). release_gpu_buffer follows gn_free. */
+/* Device memory from the library pool (caching allocator).
+ * gn_free(ptr) waits for the whole device (every stream) and then returns the block to the
+ * pool: safe whatever stream used it. It returns -1 and keeps the block when the device
+ * cannot be synchronised (a stream capture in progress); free such blocks after the capture.
+ * gn_free_async(ptr, stream) does not wait: the block is handed to a new owner only after the
+ * work enqueued on `stream` (NULL = the library stream) before the call has finished. Work on
+ * other streams that still uses the block must be complete, or ordered before the block's
+ * next user (the rule of every stream-ordered allocator). It returns -1 and keeps the block
+ * when `stream` is capturing. release_gpu_buffer orders the release on the library stream,
+ * where every Part-1 call runs; a caller that uses a GPUPtr's memory on another stream
+ * (through gn_buffer_device_ptr) synchronises that stream before releasing the buffer. */
 int gn_malloc(void **ptr, size_t bytes, CError *err);
 int gn_free(void *ptr);
 int gn_free_async(void *ptr, void *stream);
@@ -392,6 +412,448 @@ int gn_fill_uniform_f32(float *out, size_t n, uint64_t seed, uint64_t stream_id,
                         CError *err);
 int gn_fill_normal_f32(float *out, size_t n, uint64_t seed, uint64_t stream_id, float mean, float stddev,
                        void *stream, CError *err);
+
+/* ========================================================================== */
+/* Part 3 — the rest of internal/cgo/metal_bridge.h that the Go packages bind  */
+/* ========================================================================== */
+/* Every function that a non-test file of gpu/matrix, gpu/optimizer or tensor calls through
+ * cgo is declared here with the reference prototype, so that those packages compile and
+ * link against this library (tests/golden/cgo_abi.json lists each one with its reference
+ * header line and Go call sites). The element-wise matrix operations and the activation
+ * backwards below are device implementations; the groups after them belong to subsystems
+ * this backend does not cover and return -1 with the message "<name>: not provided by the
+ * go-nngpu MI355X GEMM/SpMM backend" in *err. */
+
+/* metal_bridge.h:7-16 types that Go code names (C.GPUCounters, C.KernelCompileOptions). */
+typedef void *CommandQueuePtr; /* metal_bridge.h:11 */
+typedef struct {               /* metal_bridge.h:1701-1708 */
+  int optimization_level;
+  bool fast_math;
+  bool debug_info;
+  int num_constants;
+  int num_macros;
+} KernelCompileOptions;
+typedef struct { /* metal_bridge.h:1810-1814 */
+  float computeUtilization;
+  float memoryBandwidth;
+  float cacheHitRate;
+} GPUCounters;
+
+/* Element-wise matrix operations (gpu/matrix/matrix.go calls at :486 add, :530 add_broadcast,
+ * :581 subtract, :632 element_multiply, :683 element_divide, :727 scalar_add, :771
+ * scalar_multiply; reference loops metal_bridge_matrix.m:172-543).
+ * fp32, one rounding per operation as written: result = a + b, a - b, a * b, a / b
+ * (IEEE, correctly rounded), input + scalar, input * scalar. The result buffer may be one of
+ * the inputs. mtlDevicePtr may be NULL. Synchronous.
+ *  add / subtract / element_multiply / element_divide: -2 unless aRows == bRows == resultRows
+ *    and aCols == bCols == resultCols (:180-183), -3 NULL or too small buffer (:215-218).
+ *  element_divide: -4 "Division by zero encountered at element <i>." with the lowest such i
+ *    (:470-474); the reference stops at that element, here every element is written.
+ *  add_broadcast: [M,N] + [1,N], [1,N] + [M,N], [M,N] + [M,1], [M,1] + [M,N] -> [M,N],
+ *    tried in that order (:267-311); another shape combination -2, NULL or too small
+ *    buffer -3.
+ *  scalar_add / scalar_multiply: -1 NULL or too small buffer (:492-495).
+ *  All: -1 on a device execution error. */
+int perform_mps_matrix_add(GPUPtr aMatrixPtr, long aRows, long aCols, GPUPtr bMatrixPtr, long bRows, long bCols,
+                           GPUPtr resultMatrixPtr, long resultRows, long resultCols, DevicePtr mtlDevicePtr,
+                           CError *err);
+int perform_mps_matrix_add_broadcast(GPUPtr aMatrixPtr, long aRows, long aCols, GPUPtr bMatrixPtr, long bRows,
+                                     long bCols, GPUPtr resultMatrixPtr, long resultRows, long resultCols,
+                                     DevicePtr mtlDevicePtr, CError *err);
+int perform_mps_matrix_element_divide(GPUPtr aMatrixPtr, long aRows, long aCols, GPUPtr bMatrixPtr, long bRows,
+                                      long bCols, GPUPtr resultMatrixPtr, long resultRows, long resultCols,
+                                      DevicePtr mtlDevicePtr, CError *err);
+int perform_mps_matrix_element_multiply(GPUPtr aMatrixPtr, long aRows, long aCols, GPUPtr bMatrixPtr, long bRows,
+                                        long bCols, GPUPtr resultMatrixPtr, long resultRows, long resultCols,
+                                        DevicePtr mtlDevicePtr, CError *err);
+int perform_mps_matrix_scalar_add(GPUPtr inputMatrixPtr, long rows, long cols, float scalar, GPUPtr resultMatrixPtr,
+                                  DevicePtr mtlDevicePtr, CError *err);
+int perform_mps_matrix_scalar_multiply(GPUPtr inputMatrixPtr, long rows, long cols, float scalar,
+                                       GPUPtr resultMatrixPtr, DevicePtr mtlDevicePtr, CError *err);
+int perform_mps_matrix_subtract(GPUPtr aMatrixPtr, long aRows, long aCols, GPUPtr bMatrixPtr, long bRows,
+                                long bCols, GPUPtr resultMatrixPtr, long resultRows, long resultCols,
+                                DevicePtr mtlDevicePtr, CError *err);
+/* Activation backward (gpu/matrix/activation.go ActivationBackward :177-300, calls at
+ * :223-283, called by
+ * FusedLinearActivation.Backward, fused-operations.go:486-523). Each takes the gradient with
+ * respect to the activation's output and the activation OUTPUT y (not its input), over
+ * `size` floats, and computes the reference's formulas (metal_bridge_activation.m) in fp32
+ * with one rounding per operation as written:
+ *   ReLU       gradIn = y > 0 ? g : 0                                   (:54-82)
+ *   Sigmoid    gradIn = g * y * (1 - y)                                 (:114-143)
+ *   Tanh       gradIn = g * (1 - y * y)                                 (:175-204)
+ *   LeakyReLU  gradIn = g * (y > 0 ? 1 : alpha)                         (:401-433)
+ *   ELU        gradIn = g * (y > 0 ? 1 : y + alpha)                     (:471-512)
+ *   Swish      x from y by three Newton steps on x*sigmoid(x) = y from x = y (a step is
+ *              skipped where |f'| <= 1e-8); gradIn = g * (s + x s (1 - s)), s = sigmoid(x);
+ *              |y| < 1e-8 gives g * 0.5                                 (:546-604)
+ *   GELU       x from y by three Newton steps on GELU(x) = y from x = y (tanh form, inner
+ *              argument clamped to [-88, 88]); gradIn = g * GELU'(x)    (:642-702)
+ *   Softmax    gradIn = y * (g - dot(g, y)), over all `size` values (1-D, :247-281) or per
+ *              row of [batchSize, features] (2-D, :329-369); the dot products are summed in
+ *              a fixed tree order, not the reference's sequential one.
+ * Sigmoid, Swish and GELU use expf / tanhf (within a few ulp of the C library's). gradIn
+ * may alias either input. Codes: -1 NULL or too small buffer, negative size, or execution
+ * error (the reference's -1 for bad buffers). */
+int perform_activation_elu_backward(GPUPtr gradOutputPtr, GPUPtr activationOutputPtr, long size, float alpha,
+                                    GPUPtr gradInputPtr, DevicePtr mtlDevicePtr, CError *err);
+int perform_activation_gelu_backward(GPUPtr gradOutputPtr, GPUPtr activationOutputPtr, long size,
+                                     GPUPtr gradInputPtr, DevicePtr mtlDevicePtr, CError *err);
+int perform_activation_leaky_relu_backward(GPUPtr gradOutputPtr, GPUPtr activationOutputPtr, long size, float alpha,
+                                           GPUPtr gradInputPtr, DevicePtr mtlDevicePtr, CError *err);
+int perform_activation_relu_backward(GPUPtr gradOutputPtr, GPUPtr activationOutputPtr, long size,
+                                     GPUPtr gradInputPtr, DevicePtr mtlDevicePtr, CError *err);
+int perform_activation_sigmoid_backward(GPUPtr gradOutputPtr, GPUPtr activationOutputPtr, long size,
+                                        GPUPtr gradInputPtr, DevicePtr mtlDevicePtr, CError *err);
+int perform_activation_softmax_1d_backward(GPUPtr gradOutputPtr, GPUPtr activationOutputPtr, long size,
+                                           GPUPtr gradInputPtr, DevicePtr mtlDevicePtr, CError *err);
+int perform_activation_softmax_2d_backward(GPUPtr gradOutputPtr, GPUPtr activationOutputPtr, long batchSize,
+                                           long features, GPUPtr gradInputPtr, DevicePtr mtlDevicePtr, CError *err);
+int perform_activation_swish_backward(GPUPtr gradOutputPtr, GPUPtr activationOutputPtr, long size,
+                                      GPUPtr gradInputPtr, DevicePtr mtlDevicePtr, CError *err);
+int perform_activation_tanh_backward(GPUPtr gradOutputPtr, GPUPtr activationOutputPtr, long size,
+                                     GPUPtr gradInputPtr, DevicePtr mtlDevicePtr, CError *err);
+/* Dense decompositions (matrix.go: Inverse, Determinant, LU, QR, Cholesky, Eigen, SVD; the
+ * reference runs LAPACK on the CPU, metal_bridge_decomposition.m). Not provided: -1. */
+/* metal_bridge.h:137; gpu/matrix/matrix.go:137 */
+int perform_matrix_cholesky_decomposition(GPUPtr inputMatrixPtr, long rows, long cols, GPUPtr lMatrixPtr,
+                                          DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:110; gpu/matrix/matrix.go:859 */
+int perform_matrix_determinant(GPUPtr inputMatrixPtr, long rows, long cols, float *determinant,
+                               DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:145; gpu/matrix/matrix.go:218 */
+int perform_matrix_eigenvalue_decomposition(GPUPtr inputMatrixPtr, long rows, long cols, GPUPtr eigenvaluesPtr,
+                                            GPUPtr eigenvectorsPtr, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:102; gpu/matrix/matrix.go:822 */
+int perform_matrix_inverse(GPUPtr inputMatrixPtr, long rows, long cols, GPUPtr resultMatrixPtr,
+                           DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:118; gpu/matrix/matrix.go:949 */
+int perform_matrix_lu_decomposition(GPUPtr inputMatrixPtr, long rows, long cols, GPUPtr lMatrixPtr,
+                                    GPUPtr uMatrixPtr, int *pivotIndices, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:129; gpu/matrix/matrix.go:1037 */
+int perform_matrix_qr_decomposition(GPUPtr inputMatrixPtr, long rows, long cols, GPUPtr qMatrixPtr,
+                                    GPUPtr rMatrixPtr, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:154; gpu/matrix/matrix.go:328 */
+int perform_matrix_svd_decomposition(GPUPtr inputMatrixPtr, long rows, long cols, GPUPtr uMatrixPtr,
+                                     GPUPtr sVectorPtr, GPUPtr vtMatrixPtr, DevicePtr mtlDevicePtr, CError *err);
+
+/* Loss functions (loss.go; CPU loops in metal_bridge_loss.m). Not provided: -1. */
+/* metal_bridge.h:422; gpu/matrix/loss.go:259 */
+int perform_loss_binary_crossentropy_backward(GPUPtr predictionsPtr, GPUPtr targetsPtr, long size,
+                                              GPUPtr gradInputPtr, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:415; gpu/matrix/loss.go:117 */
+int perform_loss_binary_crossentropy_forward(GPUPtr predictionsPtr, GPUPtr targetsPtr, long size, float *loss,
+                                             DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:437; gpu/matrix/loss.go:272 */
+int perform_loss_categorical_crossentropy_backward(GPUPtr predictionsPtr, GPUPtr targetsPtr, long batchSize,
+                                                   long numClasses, GPUPtr gradInputPtr, DevicePtr mtlDevicePtr,
+                                                   CError *err);
+/* metal_bridge.h:430; gpu/matrix/loss.go:130 */
+int perform_loss_categorical_crossentropy_forward(GPUPtr predictionsPtr, GPUPtr targetsPtr, long batchSize,
+                                                  long numClasses, float *loss, DevicePtr mtlDevicePtr,
+                                                  CError *err);
+/* metal_bridge.h:499; gpu/matrix/loss.go:314 */
+int perform_loss_hinge_backward(GPUPtr predictionsPtr, GPUPtr targetsPtr, long size, GPUPtr gradInputPtr,
+                                DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:492; gpu/matrix/loss.go:172 */
+int perform_loss_hinge_forward(GPUPtr predictionsPtr, GPUPtr targetsPtr, long size, float *loss,
+                               DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:468; gpu/matrix/loss.go:289 */
+int perform_loss_huber_backward(GPUPtr predictionsPtr, GPUPtr targetsPtr, long size, float delta,
+                                GPUPtr gradInputPtr, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:460; gpu/matrix/loss.go:147 */
+int perform_loss_huber_forward(GPUPtr predictionsPtr, GPUPtr targetsPtr, long size, float delta, float *loss,
+                               DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:484; gpu/matrix/loss.go:302 */
+int perform_loss_mae_backward(GPUPtr predictionsPtr, GPUPtr targetsPtr, long size, GPUPtr gradInputPtr,
+                              DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:477; gpu/matrix/loss.go:160 */
+int perform_loss_mae_forward(GPUPtr predictionsPtr, GPUPtr targetsPtr, long size, float *loss,
+                             DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:407; gpu/matrix/loss.go:247 */
+int perform_loss_mse_backward(GPUPtr predictionsPtr, GPUPtr targetsPtr, long size, GPUPtr gradInputPtr,
+                              DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:400; gpu/matrix/loss.go:105 */
+int perform_loss_mse_forward(GPUPtr predictionsPtr, GPUPtr targetsPtr, long size, float *loss,
+                             DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:452; gpu/matrix/loss.go:451 */
+int perform_loss_sparse_categorical_crossentropy_backward(GPUPtr predictionsPtr, int *targetIndices, long batchSize,
+                                                          long numClasses, GPUPtr gradInputPtr,
+                                                          DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:445; gpu/matrix/loss.go:388 */
+int perform_loss_sparse_categorical_crossentropy_forward(GPUPtr predictionsPtr, int *targetIndices, long batchSize,
+                                                         long numClasses, float *loss, DevicePtr mtlDevicePtr,
+                                                         CError *err);
+
+/* Apple memory-pool and buffer-placement helpers (memory-pool.go, memory-optimization.go;
+ * metal_bridge_memory.m). Buffers come from create_gpu_buffer and the gn_malloc pool here.
+ * Not provided: -1. */
+/* metal_bridge.h:1495; gpu/matrix/memory-optimization.go:30 */
+int allocate_aligned_gpu_buffer(long size, long alignment, GPUPtr *bufferPtr, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:1383; gpu/matrix/memory-pool.go:157 */
+int allocate_gpu_memory(long size, GPUPtr *ptr, CError *error);
+/* metal_bridge.h:1385; gpu/matrix/memory-pool.go:354 */
+int cleanup_memory_pool(CError *error);
+/* metal_bridge.h:1510; gpu/matrix/memory-optimization.go:67 */
+int coalesced_memory_copy(GPUPtr srcPtr, GPUPtr dstPtr, long size, long srcStride, long dstStride,
+                          DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:1530; gpu/matrix/memory-optimization.go:104 */
+int flush_gpu_cache(DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:1384; gpu/matrix/memory-pool.go:244 (+1 more) */
+int free_gpu_memory(GPUPtr ptr, CError *error);
+/* metal_bridge.h:1382; gpu/matrix/memory-pool.go:100 */
+int initialize_memory_pool(long max_memory, CError *error);
+/* metal_bridge.h:1521; gpu/matrix/memory-optimization.go:86 */
+int prefetch_gpu_data(GPUPtr bufferPtr, long size, long offset, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:1504; gpu/matrix/memory-optimization.go:49 */
+int release_optimized_gpu_buffer(GPUPtr bufferPtr, CError *err);
+
+/* Convolution, pooling, padding, im2col (convolution.go; metal_bridge_convolution.m).
+ * Not provided: -1. */
+/* metal_bridge.h:571; gpu/matrix/convolution.go:533 */
+int perform_avgpool2d_backward(GPUPtr gradOutputPtr, long gradOutputBatch, long gradOutputHeight,
+                               long gradOutputWidth, long gradOutputChannels, GPUPtr gradInputPtr,
+                               long gradInputBatch, long gradInputHeight, long gradInputWidth,
+                               long gradInputChannels, long poolHeight, long poolWidth, long strideH, long strideW,
+                               long padH, long padW, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:562; gpu/matrix/convolution.go:477 */
+int perform_avgpool2d_forward(GPUPtr inputPtr, long inputBatch, long inputHeight, long inputWidth,
+                              long inputChannels, GPUPtr outputPtr, long outputBatch, long outputHeight,
+                              long outputWidth, long outputChannels, long poolHeight, long poolWidth, long strideH,
+                              long strideW, long padH, long padW, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:609; gpu/matrix/convolution.go:783 */
+int perform_col2im(GPUPtr inputPtr, GPUPtr outputPtr, long outputBatch, long outputHeight, long outputWidth,
+                   long outputChannels, long kernelHeight, long kernelWidth, long strideH, long strideW, long padH,
+                   long padW, long inputHeight, long inputWidth, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:522; gpu/matrix/convolution.go:210 */
+int perform_conv2d_backward_input(GPUPtr gradOutputPtr, long gradOutputBatch, long gradOutputHeight,
+                                  long gradOutputWidth, long gradOutputChannels, GPUPtr kernelPtr,
+                                  long kernelHeight, long kernelWidth, long kernelInputChannels,
+                                  long kernelOutputChannels, GPUPtr gradInputPtr, long gradInputBatch,
+                                  long gradInputHeight, long gradInputWidth, long gradInputChannels, long strideH,
+                                  long strideW, long padH, long padW, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:532; gpu/matrix/convolution.go:283 */
+int perform_conv2d_backward_kernel(GPUPtr inputPtr, long inputBatch, long inputHeight, long inputWidth,
+                                   long inputChannels, GPUPtr gradOutputPtr, long gradOutputBatch,
+                                   long gradOutputHeight, long gradOutputWidth, long gradOutputChannels,
+                                   GPUPtr gradKernelPtr, long kernelHeight, long kernelWidth,
+                                   long kernelInputChannels, long kernelOutputChannels, long strideH, long strideW,
+                                   long padH, long padW, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:512; gpu/matrix/convolution.go:137 */
+int perform_conv2d_forward(GPUPtr inputPtr, long inputBatch, long inputHeight, long inputWidth, long inputChannels,
+                           GPUPtr kernelPtr, long kernelHeight, long kernelWidth, long kernelInputChannels,
+                           long kernelOutputChannels, GPUPtr outputPtr, long outputBatch, long outputHeight,
+                           long outputWidth, long outputChannels, long strideH, long strideW, long padH, long padW,
+                           DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:599; gpu/matrix/convolution.go:722 */
+int perform_im2col(GPUPtr inputPtr, long inputBatch, long inputHeight, long inputWidth, long inputChannels,
+                   GPUPtr outputPtr, long kernelHeight, long kernelWidth, long strideH, long strideW, long padH,
+                   long padW, long outputHeight, long outputWidth, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:552; gpu/matrix/convolution.go:415 */
+int perform_maxpool2d_backward(GPUPtr gradOutputPtr, long gradOutputBatch, long gradOutputHeight,
+                               long gradOutputWidth, long gradOutputChannels, GPUPtr indicesPtr,
+                               GPUPtr gradInputPtr, long gradInputBatch, long gradInputHeight, long gradInputWidth,
+                               long gradInputChannels, long poolHeight, long poolWidth, long strideH, long strideW,
+                               long padH, long padW, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:542; gpu/matrix/convolution.go:355 */
+int perform_maxpool2d_forward(GPUPtr inputPtr, long inputBatch, long inputHeight, long inputWidth,
+                              long inputChannels, GPUPtr outputPtr, long outputBatch, long outputHeight,
+                              long outputWidth, long outputChannels, GPUPtr indicesPtr, long poolHeight,
+                              long poolWidth, long strideH, long strideW, long padH, long padW,
+                              DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:580; gpu/matrix/convolution.go:595 */
+int perform_pad2d(GPUPtr inputPtr, long inputBatch, long inputHeight, long inputWidth, long inputChannels,
+                  GPUPtr outputPtr, long outputBatch, long outputHeight, long outputWidth, long outputChannels,
+                  long padTop, long padBottom, long padLeft, long padRight, float padValue, DevicePtr mtlDevicePtr,
+                  CError *err);
+/* metal_bridge.h:590; gpu/matrix/convolution.go:658 */
+int perform_unpad2d(GPUPtr inputPtr, long inputBatch, long inputHeight, long inputWidth, long inputChannels,
+                    GPUPtr outputPtr, long outputBatch, long outputHeight, long outputWidth, long outputChannels,
+                    long padTop, long padBottom, long padLeft, long padRight, DevicePtr mtlDevicePtr, CError *err);
+
+/* Batch / layer / group / instance normalisation (batch-norm.go; metal_bridge_normalization.m).
+ * Not provided: -1. */
+/* metal_bridge.h:621; gpu/matrix/batch-norm.go:111 */
+int perform_batch_mean(GPUPtr inputPtr, long batchSize, long features, GPUPtr meanPtr, DevicePtr mtlDevicePtr,
+                       CError *err);
+/* metal_bridge.h:648; gpu/matrix/batch-norm.go:304 */
+int perform_batch_norm_backward_input(GPUPtr gradOutputPtr, long batchSize, long features, GPUPtr inputPtr,
+                                      GPUPtr meanPtr, GPUPtr variancePtr, GPUPtr gammaPtr, float epsilon,
+                                      GPUPtr gradInputPtr, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:658; gpu/matrix/batch-norm.go:323 */
+int perform_batch_norm_backward_params(GPUPtr gradOutputPtr, long batchSize, long features, GPUPtr inputPtr,
+                                       GPUPtr meanPtr, GPUPtr variancePtr, float epsilon, GPUPtr gradGammaPtr,
+                                       GPUPtr gradBetaPtr, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:637; gpu/matrix/batch-norm.go:239 */
+int perform_batch_norm_forward(GPUPtr inputPtr, long batchSize, long features, GPUPtr meanPtr, GPUPtr variancePtr,
+                               GPUPtr gammaPtr, GPUPtr betaPtr, float epsilon, GPUPtr outputPtr,
+                               DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:629; gpu/matrix/batch-norm.go:165 */
+int perform_batch_variance(GPUPtr inputPtr, GPUPtr meanPtr, long batchSize, long features, GPUPtr variancePtr,
+                           DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:716; gpu/matrix/batch-norm.go:608 */
+int perform_group_norm_forward(GPUPtr inputPtr, long batchSize, long channels, long height, long width,
+                               long numGroups, GPUPtr gammaPtr, GPUPtr betaPtr, float epsilon, GPUPtr outputPtr,
+                               DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:697; gpu/matrix/batch-norm.go:553 */
+int perform_instance_norm_forward(GPUPtr inputPtr, long batchSize, long channels, long height, long width,
+                                  GPUPtr gammaPtr, GPUPtr betaPtr, float epsilon, GPUPtr outputPtr,
+                                  DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:678; gpu/matrix/batch-norm.go:455 */
+int perform_layer_norm_backward(GPUPtr gradOutputPtr, long batchSize, long features, GPUPtr inputPtr,
+                                GPUPtr meanPtr, GPUPtr variancePtr, GPUPtr gammaPtr, float epsilon,
+                                GPUPtr gradInputPtr, GPUPtr gradGammaPtr, GPUPtr gradBetaPtr,
+                                DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:668; gpu/matrix/batch-norm.go:389 */
+int perform_layer_norm_forward(GPUPtr inputPtr, long batchSize, long features, GPUPtr gammaPtr, GPUPtr betaPtr,
+                               float epsilon, GPUPtr outputPtr, GPUPtr meanPtr, GPUPtr variancePtr,
+                               DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:688; gpu/matrix/batch-norm.go:503 */
+int perform_update_running_stats(GPUPtr runningMeanPtr, GPUPtr runningVarPtr, GPUPtr batchMeanPtr,
+                                 GPUPtr batchVarPtr, float momentum, long features, DevicePtr mtlDevicePtr,
+                                 CError *err);
+
+/* Fused operations other than the linear layer (fused-operations.go; metal_bridge_fused.m).
+ * Not provided: -1. */
+/* metal_bridge.h:1355; gpu/matrix/fused-operations.go:645 */
+int perform_fused_attention(GPUPtr query, GPUPtr key, GPUPtr value, long batch_size, long seq_len, long model_dim,
+                            int num_heads, float scale, float dropout_rate, bool causal, GPUPtr output,
+                            DevicePtr device, CError *error);
+/* metal_bridge.h:1338; gpu/matrix/fused-operations.go:241 */
+int perform_fused_conv_bn_relu(GPUPtr input, long batch_size, long input_h, long input_w, long input_channels,
+                               GPUPtr kernel, long kernel_h, long kernel_w, long output_channels, GPUPtr gamma,
+                               GPUPtr beta, GPUPtr bias, long stride_h, long stride_w, long pad_h, long pad_w,
+                               float epsilon, bool training, GPUPtr output, long output_h, long output_w,
+                               DevicePtr device, CError *error);
+/* metal_bridge.h:1362; gpu/matrix/fused-operations.go:873 */
+int perform_fused_gelu_dropout(GPUPtr input, long size, float dropout_rate, unsigned int seed, GPUPtr output,
+                               DevicePtr device, CError *error);
+/* metal_bridge.h:1367; gpu/matrix/fused-operations.go:1047 */
+int perform_fused_layer_norm_linear(GPUPtr input, long batch_size, long seq_len, long input_dim, GPUPtr gamma,
+                                    GPUPtr beta, float epsilon, GPUPtr weight, long output_dim, GPUPtr bias,
+                                    GPUPtr output, DevicePtr device, CError *error);
+/* metal_bridge.h:1374; gpu/matrix/fused-operations.go:1234 */
+int perform_fused_residual_block(GPUPtr input, long batch_size, long height, long width, long channels,
+                                 GPUPtr conv1_weight, GPUPtr bn1_gamma, GPUPtr bn1_beta, GPUPtr conv2_weight,
+                                 GPUPtr bn2_gamma, GPUPtr bn2_beta, float epsilon, GPUPtr output, DevicePtr device,
+                                 CError *error);
+
+/* Embedded-MSL kernels other than the GEMMs (optimized-kernels.go; metal_bridge_kernels.m).
+ * Not provided: -1. */
+/* metal_bridge.h:1440; gpu/matrix/optimized-kernels.go:178 */
+int perform_conv1x1_optimized(GPUPtr inputPtr, GPUPtr weightPtr, GPUPtr outputPtr, long batch, long height,
+                              long width, long inChannels, long outChannels, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:1449; gpu/matrix/optimized-kernels.go:244 */
+int perform_depthwise_conv_optimized(GPUPtr inputPtr, GPUPtr kernelPtr, GPUPtr outputPtr, long batch, long inHeight,
+                                     long inWidth, long channels, long kernelH, long kernelW, long strideH,
+                                     long strideW, long padH, long padW, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:1459; gpu/matrix/optimized-kernels.go:310 */
+int perform_elementwise_binary_op_optimized(GPUPtr aPtr, GPUPtr bPtr, GPUPtr outputPtr, int opType, long size,
+                                            long aStride, long bStride, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:1484; gpu/matrix/optimized-kernels.go:466 */
+int perform_layer_norm_optimized(GPUPtr inputPtr, GPUPtr gammaPtr, GPUPtr betaPtr, GPUPtr outputPtr,
+                                 GPUPtr meanOutPtr, GPUPtr varOutPtr, long batchSize, long featureSize,
+                                 float epsilon, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:1468; gpu/matrix/optimized-kernels.go:352 */
+int perform_reduce_optimized(GPUPtr inputPtr, GPUPtr outputPtr, long size, int opType, DevicePtr mtlDevicePtr,
+                             CError *err);
+/* metal_bridge.h:1476; gpu/matrix/optimized-kernels.go:399 */
+int perform_softmax_optimized(GPUPtr inputPtr, GPUPtr outputPtr, long batchSize, long numClasses,
+                              DevicePtr mtlDevicePtr, CError *err);
+
+/* Gradient utilities (gradient.go, grad-ops.go, training.go; metal_bridge_gradient.m).
+ * Not provided: -1. */
+/* metal_bridge.h:1415; gpu/matrix/grad-ops.go:234 */
+int perform_dropout_backward(GPUPtr grad_output, GPUPtr mask, long size, float probability, GPUPtr grad_input,
+                             DevicePtr device, CError *error);
+/* metal_bridge.h:1410; gpu/matrix/grad-ops.go:190 */
+int perform_dropout_forward(GPUPtr input, long size, float probability, unsigned int seed, GPUPtr output,
+                            GPUPtr mask, DevicePtr device, CError *error);
+/* metal_bridge.h:1388; gpu/matrix/gradient.go:283 */
+int perform_gradient_accumulate(GPUPtr existing_grad, GPUPtr new_grad, long size, DevicePtr device, CError *error);
+/* metal_bridge.h:1398; gpu/matrix/gradient.go:914 */
+int perform_sum_along_axis(GPUPtr input, int axis, long input_ndim, long *input_shape, GPUPtr output,
+                           long output_ndim, long *output_shape, DevicePtr device, CError *error);
+/* metal_bridge.h:1404; gpu/matrix/training.go:894 (+4 more) */
+int perform_tensor_fill(GPUPtr tensor, long size, float value, DevicePtr device, CError *error);
+/* metal_bridge.h:1393; gpu/matrix/gradient.go:374 */
+int perform_tensor_sum_squares(GPUPtr tensor, long size, float *result, DevicePtr device, CError *error);
+
+/* Optimizer steps, clipping and learning-rate schedules (package gpu/optimizer;
+ * metal_bridge_optimizer.m). Not provided: -1. */
+/* metal_bridge.h:990; gpu/optimizer/optimizer.go:256 */
+int perform_adam_step(GPUPtr paramsPtr, GPUPtr gradPtr, long size, float learningRate, float beta1, float beta2,
+                      float epsilon, float weightDecay, GPUPtr m_bufferPtr, GPUPtr v_bufferPtr, long stepNumber,
+                      DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:1050; gpu/optimizer/optimizer.go:606 */
+int perform_adamw_step(GPUPtr paramsPtr, GPUPtr gradPtr, long size, float learningRate, float beta1, float beta2,
+                       float epsilon, float weightDecay, GPUPtr m_bufferPtr, GPUPtr v_bufferPtr, long stepNumber,
+                       DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:1142; gpu/optimizer/optimizer.go:730 */
+int perform_global_gradient_clip(GPUPtr *gradPtrs, long *sizes, long numTensors, float maxNorm, float *actualNorm,
+                                 DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:1132; gpu/optimizer/optimizer.go:810 */
+int perform_global_gradient_norm(GPUPtr *gradPtrs, long *sizes, long numTensors, float *globalNorm,
+                                 DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:1122; gpu/optimizer/optimizer.go:761 */
+int perform_gradient_clip_by_value(GPUPtr gradPtr, long size, float minValue, float maxValue,
+                                   DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:1089; gpu/optimizer/scheduler.go:167 */
+int perform_lr_cosine_annealing(float *currentLR, float initialLR, float minLR, long stepNumber, long totalSteps,
+                                CError *err);
+/* metal_bridge.h:1069; gpu/optimizer/scheduler.go:47 */
+int perform_lr_exponential_decay(float *currentLR, float initialLR, float decayRate, long stepNumber,
+                                 long decaySteps, CError *err);
+/* metal_bridge.h:1099; gpu/optimizer/scheduler.go:229 */
+int perform_lr_polynomial_decay(float *currentLR, float initialLR, float finalLR, long stepNumber, long totalSteps,
+                                float power, CError *err);
+/* metal_bridge.h:1079; gpu/optimizer/scheduler.go:107 */
+int perform_lr_step_decay(float *currentLR, float initialLR, float gamma, long stepNumber, long stepSize,
+                          CError *err);
+/* metal_bridge.h:1201; gpu/optimizer/scheduler.go:296 */
+int perform_lr_warmup(float *currentLR, float targetLR, long stepNumber, long warmupSteps, int warmupType,
+                      CError *err);
+/* metal_bridge.h:1007; gpu/optimizer/optimizer.go:436 */
+int perform_rmsprop_step(GPUPtr paramsPtr, GPUPtr gradPtr, long size, float learningRate, float alpha,
+                         float epsilon, float momentum, float weightDecay, GPUPtr squaredGradBufferPtr,
+                         GPUPtr momentumBufferPtr, DevicePtr mtlDevicePtr, CError *err);
+/* metal_bridge.h:977; gpu/optimizer/optimizer.go:97 */
+int perform_sgd_step(GPUPtr paramsPtr, GPUPtr gradPtr, long size, float learningRate, float momentum,
+                     GPUPtr momentumBufferPtr, float weightDecay, DevicePtr mtlDevicePtr, CError *err);
+
+/* Command queues, events, shared / mapped memory, counters and the MPSGraph convolution
+ * node (multi-stream-execution.go, unified-memory-optimization.go, command-queue-pool.go,
+ * profiling-autotuning.go, mps-graph-integration.go; metal_bridge_phase9b.m, whose own
+ * versions are placeholders). Pointer results are NULL (memoryMapFile also sets *error),
+ * void calls do nothing, getGPUCounters stores zeros, getGPUPowerUsage and
+ * getGPUTemperature return 0. getGPUMemoryUsage reports the device's total and used HBM
+ * (hipMemGetInfo). */
+/* metal_bridge.h:1803; gpu/matrix/unified-memory-optimization.go:476 */
+void *allocateSharedMemory(long size);
+/* metal_bridge.h:1797; gpu/matrix/command-queue-pool.go:53 (+2 more) */
+void *createCommandQueue(void *device);
+/* metal_bridge.h:1823; gpu/matrix/mps-graph-integration.go:582 */
+void *createConv2DNode(void *graph, void *input, void *weights, long strideH, long strideW, long padH, long padW);
+/* metal_bridge.h:1804; gpu/matrix/unified-memory-optimization.go:486 */
+void *createGPUBufferFromSharedMemory(void *device, void *sharedMemory, long size);
+/* metal_bridge.h:1799; gpu/matrix/multi-stream-execution.go:351 */
+void *createMetalEvent(void *device);
+/* metal_bridge.h:1816; gpu/matrix/profiling-autotuning.go:782 (+1 more) */
+void getGPUCounters(GPUCounters *counters);
+/* metal_bridge.h:1817; gpu/matrix/profiling-autotuning.go:769 (+1 more) */
+void getGPUMemoryUsage(long *totalBytes, long *usedBytes);
+/* metal_bridge.h:1818; gpu/matrix/profiling-autotuning.go:794 */
+float getGPUPowerUsage(void);
+/* metal_bridge.h:1819; gpu/matrix/profiling-autotuning.go:803 */
+float getGPUTemperature(void);
+/* metal_bridge.h:1805; gpu/matrix/unified-memory-optimization.go:530 */
+void makeBufferGPUResident(void *buffer);
+/* metal_bridge.h:1806; gpu/matrix/unified-memory-optimization.go:496 */
+void *memoryMapFile(const char *path, long *size, CError *error);
+/* metal_bridge.h:1798; gpu/matrix/multi-stream-execution.go:347 */
+void synchronizeCommandQueue(void *queue);
+/* metal_bridge.h:1807; gpu/matrix/unified-memory-optimization.go:512 */
+void unmapMemory(void *memory, long size);
 
 #ifdef __cplusplus
 }

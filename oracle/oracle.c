@@ -556,6 +556,65 @@ void orc_softmax_rows_f64(long rows, long cols, const float *in, double *out) {
   }
 }
 
+/* activation backward from the output: metal_bridge_activation.m:54-702 */
+float orc_act_backward_out_f32(int code, float alpha, float g, float y) {
+  switch (code) {
+    case 0: return y > 0.0f ? g : 0.0f;
+    case 1: return g * y * (1.0f - y);
+    case 2: return g * (1.0f - y * y);
+    case 4: return g * (y > 0.0f ? 1.0f : alpha);
+    case 5: return g * (y > 0.0f ? 1.0f : y + alpha);
+    case 6: {
+      if (fabsf(y) < 1e-8f) return g * 0.5f;
+      float x = y;
+      for (int it = 0; it < 3; ++it) {
+        float s = 1.0f / (1.0f + expf(-x));
+        float f = x * s - y;
+        float df = s + x * s * (1.0f - s);
+        if (fabsf(df) > 1e-8f) x = x - f / df;
+      }
+      float s = 1.0f / (1.0f + expf(-x));
+      return g * (s + x * s * (1.0f - s));
+    }
+    case 7: {
+      const float k = 0.7978845608028654f, c = 0.044715f;
+      float x = y;
+      for (int it = 0; it < 3; ++it) {
+        float x3 = x * x * x;
+        float inner = k * (x + c * x3);
+        inner = fmaxf(-88.0f, fminf(88.0f, inner));
+        float t = tanhf(inner);
+        float f = 0.5f * x * (1.0f + t) - y;
+        float dt = 1.0f - t * t;
+        float di = k * (1.0f + 3.0f * c * x * x);
+        float df = 0.5f * (1.0f + t) + 0.5f * x * dt * di;
+        if (fabsf(df) > 1e-8f) x = x - f / df;
+      }
+      float x3 = x * x * x;
+      float inner = k * (x + c * x3);
+      inner = fmaxf(-88.0f, fminf(88.0f, inner));
+      float t = tanhf(inner);
+      float sech2 = 1.0f - t * t;
+      float di = k * (1.0f + 3.0f * c * x * x);
+      return g * (0.5f * (1.0f + t) + 0.5f * x * sech2 * di);
+    }
+    default: return g;
+  }
+}
+
+void orc_act_backward_out_array_f32(int code, float alpha, const float *g, const float *y, float *out, long n) {
+  for (long i = 0; i < n; ++i) out[i] = orc_act_backward_out_f32(code, alpha, g[i], y[i]);
+}
+
+void orc_softmax_backward_f32(long rows, long cols, const float *g, const float *y, float *out) {
+  for (long r = 0; r < rows; ++r) {
+    const float *gr = g + r * cols, *yr = y + r * cols;
+    float dot = 0.0f;
+    for (long i = 0; i < cols; ++i) dot += gr[i] * yr[i];
+    for (long i = 0; i < cols; ++i) out[r * cols + i] = yr[i] * (gr[i] - dot);
+  }
+}
+
 /* ------------------------------------------------------------------------- */
 void orc_transpose_f32(long rows, long cols, const float *in, float *out) {
   for (long i = 0; i < rows; ++i)

@@ -160,6 +160,28 @@ double orc_act_grad_f64(int code, double alpha, double x);
 void orc_act_backward_f64(int code, double alpha, double scale, const float *dy, const float *pre, long n,
                           double *g);
 
+/* ---- activation backward from the activation OUTPUT (reference bridge) ------ */
+/* Restates perform_activation_*_backward, internal/cgo/metal_bridge_activation.m, which take
+ * the gradient g and the activation's OUTPUT y (gpu/matrix/activation.go:177-300), in fp32
+ * with one rounding per operation as the C source is written (this file is built with
+ * -ffp-contract=off): ReLU y>0 ? g : 0 (:77-79); Sigmoid g*y*(1-y) (:137-140); Tanh
+ * g*(1-y*y) (:198-201); LeakyReLU g*(y>0 ? 1 : a) (:425-429); ELU g*(y>0 ? 1 : y+a)
+ * (:494-506); Swish: |y|<1e-8 -> g*0.5, else x from y by three Newton steps on
+ * x*sigmoid(x) = y starting at x = y (a step is skipped when |f'| <= 1e-8), then
+ * g*(s + x*s*(1-s)) (:569-599); GELU: three Newton steps on GELU(x) = y from x = y, inner
+ * argument clamped to +-88, then g*GELU'(x) (:665-697). Other codes return g.
+ * Pins (tests/test_oracle.py): for y = act(x) computed in float64, the result equals
+ * g*act'(x) from the finite-difference-pinned orc_act_grad_f64 (the reference's formulas
+ * are exact identities for Sigmoid, Tanh, ELU, LeakyReLU, ReLU; for Swish and GELU where the
+ * three Newton steps converge); the special cases Swish(|y|<1e-8) = g/2 and GELU(y=0) =
+ * g/2. */
+float orc_act_backward_out_f32(int code, float alpha, float g, float y);
+void orc_act_backward_out_array_f32(int code, float alpha, const float *g, const float *y, float *out, long n);
+/* Restates perform_activation_softmax_{1d,2d}_backward (:247-281, :329-369): per row,
+ * dot = sequential fp32 sum of g*y, then out = y*(g - dot). Pins: float64 central finite
+ * differences of x -> sum(g * softmax(x)) at y = softmax(x). */
+void orc_softmax_backward_f32(long rows, long cols, const float *g, const float *y, float *out);
+
 /* ---- transpose ----------------------------------------------------------- */
 /* out[j,i] = in[i,j]; restates metal_bridge_matrix.m:162-166. */
 void orc_transpose_f32(long rows, long cols, const float *in, float *out);

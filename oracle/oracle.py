@@ -72,6 +72,8 @@ def lib():
         "orc_linear_f64": (None, [_L, _L, _L, _f32p, _f32p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
                                   ctypes.c_double, _f64p, ctypes.c_int]),
         "orc_transpose_f32": (None, [_L, _L, _f32p, _f32p]),
+        "orc_act_backward_out_array_f32": (None, [ctypes.c_int, ctypes.c_float, _f32p, _f32p, _f32p, _L]),
+        "orc_softmax_backward_f32": (None, [_L, _L, _f32p, _f32p, _f32p]),
         "orc_rel_frob": (ctypes.c_double, [_f32p, _f64p, ctypes.c_size_t]),
     }
     for name, (res, args) in sig.items():
@@ -384,6 +386,27 @@ def linear_f64(X, W, bias, act, w_out_in, alpha=0.0, nthreads=None):
     lib().orc_linear_f64(batch, fin, out, X.reshape(-1), W.reshape(-1), int(w_out_in),
                          b.ctypes.data if b is not None else None, act, alpha, Y.reshape(-1), nthreads or threads())
     return Y
+
+
+def act_backward_out_f32(code, g, y, alpha=0.0):
+    """The reference bridge's activation backward from the activation OUTPUT y
+    (orc_act_backward_out_f32), element-wise, fp32."""
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    out = np.empty(y.shape, dtype=np.float32)
+    lib().orc_act_backward_out_array_f32(code, alpha, g.reshape(-1), y.reshape(-1), out.reshape(-1), y.size)
+    return out
+
+
+def softmax_backward_f32(g, y):
+    """y * (g - dot(g, y)) per row (a 1-D array is one row), sequential fp32 dot
+    (orc_softmax_backward_f32)."""
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    rows, cols = (1, y.size) if y.ndim == 1 else y.shape
+    out = np.empty(y.shape, dtype=np.float32)
+    lib().orc_softmax_backward_f32(rows, cols, g.reshape(-1), y.reshape(-1), out.reshape(-1))
+    return out
 
 
 def transpose_f32(X):

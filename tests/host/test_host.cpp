@@ -703,7 +703,7 @@ void TestGPUDenseAndGPUMatMul() {
   CHECK_PANICS(g->At(M, 0));
   g->Set(0, 0, 42.0);
   CHECK(g->At(0, 0) == 42.0);
-  // T() is a materialised GPU transpose
+  // T() is the transpose (a copy-on-write view of the same tensor)
   auto t = ga->T();
   int r, c;
   t->Dims(r, c);
@@ -782,6 +782,56 @@ void TestGPUDenseTransposeViews() {
     double num = 0, den = 0;
     for (int j = 0; j < n; ++j) num += (colgot[j] - colref[j]) * (colgot[j] - colref[j]), den += colref[j] * colref[j];
     CHECK(std::sqrt(num / den) <= 1e-5);
+  }
+}
+
+// The reference's T() is a separate, materialised matrix (gonum-compat.go:61-68). Here it
+// starts as a view of the same tensor, shared copy-on-write: a later Mul into the parent,
+// Set on either side, and ReleaseGPU of a device-resident parent leave the other unchanged.
+void TestGPUDenseTransposeIsIndependent() {
+  const int M = 33, K = 21, N = 17;
+  std::vector<float> af = uniform((size_t)M * K, 400), bf = uniform((size_t)K * N, 401);
+  std::vector<float> xf = uniform((size_t)M * K, 402), yf = uniform((size_t)K * N, 403);
+  auto ga = matrix::NewGPUDense(M, K, std::vector<double>(af.begin(), af.end()));
+  auto gb = matrix::NewGPUDense(K, N, std::vector<double>(bf.begin(), bf.end()));
+  auto gx = matrix::NewGPUDense(M, K, std::vector<double>(xf.begin(), xf.end()));
+  auto gy = matrix::NewGPUDense(K, N, std::vector<double>(yf.begin(), yf.end()));
+  std::vector<double> ab((size_t)M * N), xy((size_t)M * N);
+  orc_gemm_f64(0, 0, M, N, K, 1.0, af.data(), K, bf.data(), N, 0.0, ab.data(), N, 1);
+  orc_gemm_f64(0, 0, M, N, K, 1.0, xf.data(), K, yf.data(), N, 0.0, xy.data(), N, 1);
+  auto close = [](double a, double b) { return std::fabs(a - b) <= 1e-5 * (1.0 + std::fabs(b)); };
+  auto c = matrix::NewGPUDense(M, N, std::vector<double>((size_t)M * N, 0.0));
+  c->Mul(*ga, *gb);  // c holds a device-resident product
+  auto t = c->T();   // transpose of the first product
+  c->Mul(*gx, *gy);  // the parent gets a new product; t keeps the first one
+  bool ok = true;
+  for (int i = 0; i < M; ++i)
+    for (int j = 0; j < N; ++j) ok = ok && close(t->At(j, i), ab[(size_t)i * N + j]) && close(c->At(i, j), xy[(size_t)i * N + j]);
+  CHECK(ok);
+  // Set on the view changes only the view, Set on the parent only the parent.
+  auto tv = std::dynamic_pointer_cast<matrix::GPUDense>(t);
+  CHECK(tv != nullptr);
+  auto u = c->T();
+  std::dynamic_pointer_cast<matrix::GPUDense>(u)->Set(2, 3, 7.0);
+  CHECK(u->At(2, 3) == 7.0 && close(c->At(3, 2), xy[(size_t)3 * N + 2]));
+  auto w = c->T();
+  c->Set(4, 1, -9.0);
+  CHECK(c->At(4, 1) == -9.0 && close(w->At(1, 4), xy[(size_t)4 * N + 1]));
+  // ReleaseGPU of a device-resident result keeps its values (the reference's buffer
+  // aliases the tensor's data), for the matrix and for a view taken before.
+  auto d = matrix::NewGPUDense(M, N, std::vector<double>((size_t)M * N, 0.0));
+  d->Mul(*ga, *gb);
+  auto dv = d->T();
+  CHECK(d->GetTensor()->IsOnGPU());
+  d->ReleaseGPU();
+  CHECK(!d->GetTensor()->IsOnGPU());
+  CHECK(close(d->At(5, 6), ab[(size_t)5 * N + 6]) && close(dv->At(6, 5), ab[(size_t)5 * N + 6]));
+  // the same at the tensor level: a GPU result released without RetrieveCPU
+  auto [r, err] = matrix::MatMul(*ga->GetTensor(), *gb->GetTensor());
+  CHECK_NOERR(err);
+  if (r) {
+    r->ReleaseGPU();
+    CHECK(!r->IsOnGPU() && close(r->Data[(size_t)7 * N + 8], ab[(size_t)7 * N + 8]));
   }
 }
 
@@ -951,6 +1001,7 @@ int main(int argc, char **argv) {
       {"TestLinearLayer", TestLinearLayer, true},
       {"TestGPUDenseAndGPUMatMul", TestGPUDenseAndGPUMatMul, true},
       {"TestGPUDenseTransposeViews", TestGPUDenseTransposeViews, true},
+      {"TestGPUDenseTransposeIsIndependent", TestGPUDenseTransposeIsIndependent, true},
       {"TestGPUMatMulC1Golden", TestGPUMatMulC1Golden, true},
       {"TestGPUSparseMatMulAndMatVec", TestGPUSparseMatMulAndMatVec, true},
       {"TestSparseOps", TestSparseOps, true},

@@ -34,7 +34,7 @@ def test_header_declares_reference_subset_and_extensions():
 def test_library_exports_every_declared_symbol(lib):
     for name in G.header_symbols():
         assert hasattr(lib, name), f"{name} declared in include/gonngpu.h but not exported"
-    assert set(G.SIGNATURES) == set(G.header_symbols()), "ctypes table and header disagree"
+    assert set(G.SIGNATURES) <= set(G.header_symbols()), "ctypes table binds an undeclared name"
 
 
 def test_library_targets_gfx950_only(lib):

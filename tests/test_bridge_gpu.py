@@ -143,11 +143,13 @@ def test_scratch_allocation_failure_is_clean(dev):
 
 
 def test_release_is_stream_ordered(dev):
-    """gn_free / release_gpu_buffer do not wait: a block freed while kernels on the library
-    stream still read it goes to a new owner only after they have finished. Here A is freed
-    right behind eight queued 4096^3 GEMMs that read it, a block of the same size is taken
-    at once and overwritten from another stream; the GEMMs' output must still equal the
-    product computed before."""
+    """gn_free_async (and release_gpu_buffer, on the library stream) does not wait: a block
+    freed while kernels on the library stream still read it goes to a new owner only after
+    they have finished. Here A is freed right behind eight queued 4096^3 GEMMs that read it, a
+    block of the same size is taken at once and overwritten from another stream; the GEMMs'
+    output must still equal the product computed before. gn_free waits for the whole device
+    instead: after it returns the block may be reused at once, and the GEMMs queued before it
+    have finished."""
     import ctypes
 
     import torch
@@ -168,24 +170,34 @@ def test_release_is_stream_ordered(dev):
     ref = torch.empty((n, n), dtype=torch.float32, device=dev)
     out = torch.empty((n, n), dtype=torch.float32, device=dev)
 
-    def gemm(dst):  # on the library stream (NULL)
-        G.call("gn_gemm", G.GN_F32, 0, 0, n, n, n, 1.0, pa, n, 0, B.data_ptr(), n, 0, 0.0, dst.data_ptr(), n, 0, 1,
+    def gemm(src, dst):  # on the library stream (NULL)
+        G.call("gn_gemm", G.GN_F32, 0, 0, n, n, n, 1.0, src, n, 0, B.data_ptr(), n, 0, 0.0, dst.data_ptr(), n, 0, 1,
                None, G.ACT_NONE, 0.0, None)
 
-    gemm(ref)
+    gemm(pa, ref)
     G.call("gn_synchronize", None)
     for _ in range(8):
-        gemm(out)
-    G.call("gn_free", pa)  # A is still being read by the queued GEMMs
+        gemm(pa, out)
+    G.call("gn_free_async", pa, None)  # A is still being read by the queued GEMMs
     pz = malloc()
     G.call("gn_fill_uniform_f32", pz, n * n, 7, 7, 100.0, 200.0, torch.cuda.current_stream().cuda_stream)
     G.call("gn_synchronize", None)
     torch.cuda.synchronize()
     assert pz != pa, "a block still read by queued kernels was handed out again"
     assert torch.equal(out, ref)
-    # once the work is done, the freed blocks are reused (no growth of the pool)
+    # gn_free: device-wide wait, then the block is free at once
+    G.call("gn_fill_normal_f32", pz, n * n, 42, 901, 0.0, 1.0, None)
+    out.zero_()
+    torch.cuda.synchronize()
+    for _ in range(8):
+        gemm(pz, out)
     G.call("gn_free", pz)
-    G.call("gn_synchronize", None)
+    p3 = malloc()
+    G.call("gn_fill_uniform_f32", p3, n * n, 7, 7, 100.0, 200.0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), "gn_free returned before the GEMMs reading the block had finished"
+    # once the work is done, the freed blocks are reused (no growth of the pool)
+    G.call("gn_free", p3)
     p2 = malloc()
-    assert p2 in (pa, pz)
+    assert p2 in (pa, pz, p3)
     G.call("gn_free_async", p2, torch.cuda.current_stream().cuda_stream)

@@ -770,9 +770,11 @@ def test_fused_linear_reference_abi(dev):
 def test_fused_linear_nil_activation_call_sequence(dev):
     """The reference's FusedLinearActivation.Forward with config.Activation == nil sends
     C.int(OpReLU) and alpha 0 (fused-operations.go:433-434). OpReLU is 6 in the OpType enum
-    (gradient.go:27-39), and code 6 of the ActivationType enum this entry reads is Swish
-    (activation.go:20-29). The unchanged call therefore runs Swish; the required one-line Go
-    edit (ActivationType ReLU, 0) runs ReLU, the comment's "Default to ReLU"."""
+    (gradient.go:27-39). The reference kernel would read 6 as no activation
+    (default.metal:488-506, codes 0-4 only); this entry reads every code as an ActivationType
+    (activation.go:20-29), where 6 is Swish. The unchanged call therefore runs Swish here; the
+    one-line Go edit of the integration (ActivationType ReLU, 0) runs ReLU, the comment's
+    "Default to ReLU", a deliberate deviation from the kernel's identity."""
     rng = np.random.default_rng(31)
     X = rng.standard_normal((24, 64)).astype(np.float32)
     W = rng.standard_normal((64, 40)).astype(np.float32)

@@ -504,3 +504,63 @@ def test_parallel_sparse_loops_equal_the_serial_ones():
                                       O.spmm_f32(rp, col, val, D, use_fma=fma))
         np.testing.assert_array_equal(O.spmv_f32_par(rp, col, val, x, 8, use_fma=fma),
                                       O.spmv_f32(rp, col, val, x, use_fma=fma))
+
+
+# ---------------------------------------------------------------- backward from the output
+@pytest.mark.parametrize("code,alpha,lo,hi,atol", [
+    (0, 0.0, -4, 4, 0.0), (1, 0.0, -6, 6, 2e-7), (2, 0.0, -4, 4, 1e-6), (4, 0.1, -4, 4, 1e-7),
+    (5, 1.0, -6, 4, 5e-7), (6, 0.0, -0.3, 6, 3e-6), (7, 0.0, -0.3, 3, 5e-6)])
+def test_act_backward_out_equals_derivative_at_the_input(code, alpha, lo, hi, atol):
+    """The reference's backward formulas in terms of the OUTPUT y = act(x) are identities of
+    act'(x): y(1-y), 1-y^2, y+alpha (ELU, x<0), 1 or alpha; for Swish and GELU the three
+    Newton steps from x = y converge on [lo, hi] (two steps leave errors of 1e-4 to 1e-3
+    there, so a wrong step count fails). Checked against orc_act_grad_f64, itself pinned
+    by finite differences above."""
+    rng = np.random.default_rng(90 + code)
+    x = rng.uniform(lo, hi, 4000)
+    x = x[np.abs(x) > 1e-3]
+    g = rng.standard_normal(x.size).astype(np.float32)
+    y = O.act_f64(code, x, alpha).astype(np.float32)
+    got = O.act_backward_out_f32(code, g, y, alpha)
+    ref = g.astype(np.float64) * O.act_grad_f64(code, x, alpha)
+    np.testing.assert_allclose(got, ref, rtol=2e-6 if code != 2 else 0, atol=atol * 4)
+
+
+def test_act_backward_out_special_cases():
+    one = np.ones(1, np.float32)
+    # Swish: |y| < 1e-8 short-cuts to g/2 (metal_bridge_activation.m:573-577); GELU: y = 0 gives x = 0.
+    assert O.act_backward_out_f32(6, 3 * one, np.float32([5e-9]))[0] == 1.5
+    assert O.act_backward_out_f32(7, 3 * one, np.float32([0.0]))[0] == 1.5
+    # ReLU passes g where y > 0 only; LeakyReLU / ELU use the output's sign.
+    y = np.float32([-1.0, 0.0, 2.0])
+    g = np.float32([5.0, 6.0, 7.0])
+    assert list(O.act_backward_out_f32(0, g, y)) == [0.0, 0.0, 7.0]
+    assert list(O.act_backward_out_f32(4, g, y, 0.5)) == [2.5, 3.0, 7.0]
+    assert list(O.act_backward_out_f32(5, g, y, 2.0)) == [5.0, 12.0, 7.0]  # g * (y + alpha) for y <= 0
+    # Sigmoid at y = 1/2 is g/4, Tanh at y = 0 is g.
+    assert O.act_backward_out_f32(1, 4 * one, np.float32([0.5]))[0] == 1.0
+    assert O.act_backward_out_f32(2, 4 * one, np.float32([0.0]))[0] == 4.0
+
+
+def test_softmax_backward_matches_finite_differences():
+    """y * (g - <g, y>) is the gradient of x -> <g, softmax(x)> at y = softmax(x): checked by
+    float64 central differences (a dropped term or a wrong sign fails)."""
+    rng = np.random.default_rng(123)
+    for rows, cols in ((1, 7), (3, 33), (2, 300)):
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        g = rng.standard_normal((rows, cols)).astype(np.float32)
+        y = O.softmax_rows_f64(x)
+        got = O.softmax_backward_f32(g, y.astype(np.float32))
+        h = 1e-4
+        fd = np.empty((rows, cols))
+        for j in range(cols):
+            xp = x.astype(np.float64).copy()
+            xm = xp.copy()
+            xp[:, j] += h
+            xm[:, j] -= h
+            sp_ = np.exp(xp - xp.max(1, keepdims=True))
+            sp_ /= sp_.sum(1, keepdims=True)
+            sm_ = np.exp(xm - xm.max(1, keepdims=True))
+            sm_ /= sm_.sum(1, keepdims=True)
+            fd[:, j] = ((g * sp_).sum(1) - (g * sm_).sum(1)) / (2 * h)
+        np.testing.assert_allclose(got, fd, rtol=1e-4, atol=1e-6)

@@ -458,3 +458,33 @@ def test_spmm_index_cache_reuse_and_invalidation(dev):
     assert G.memory_stats()[2] == nmid - 3  # the values and their cached index arrays
     for b in (bd, bc, bx, by):
         b.release()
+
+
+def test_spmm_index_cache_revalidates_for_a_smaller_column_count(dev):
+    """An index copy validated for K columns is not trusted for a call with fewer columns:
+    the same arrays with aCols below the largest column index are refused with -3, as the
+    uncached path refuses them, instead of silently dropping the out-of-range entries."""
+    rows, cols, N = 300, 400, 32
+    rp, col, val = O.random_csr(rows, cols, 10.0, seed=78)
+    D = O.normal((cols, N), 7, 2)
+    bv, bd, bc = G.Buffer.from_array(val), G.Buffer.from_array(D), G.Buffer(rows * N * 4)
+
+    def run(k):
+        return G.call_rc("perform_sparse_dense_matmul", bv.handle, rp.ctypes.data, rp.size, col.ctypes.data, col.size,
+                         rows, k, val.size, bd.handle, k, N, bc.handle, rows, N, None)
+
+    assert run(cols) == (0, "")
+    assert run(cols) == (0, "")  # cached and validated for K = cols
+    k_small = int(col.max())  # at least one column index is now out of range
+    rc, msg = run(k_small)
+    assert rc == -3 and "column" in msg, (rc, msg)
+    # SpMV through the same cached structure with the smaller K is refused too
+    x = O.normal((k_small,), 8, 2)
+    bx, by = G.Buffer.from_array(x), G.Buffer(rows * 4)
+    rc, msg = G.call_rc("perform_sparse_matvec", bv.handle, rp.ctypes.data, rp.size, col.ctypes.data, col.size, rows,
+                        k_small, val.size, bx.handle, k_small, by.handle, rows, None)
+    assert rc == -3, (rc, msg)
+    assert run(cols) == (0, "")  # and the full K still runs
+    np.testing.assert_array_equal(bc.to_array((rows, N)), O.spmm_f32(rp, col, val, D, use_fma=True))
+    for b in (bv, bd, bc, bx, by):
+        b.release()
