@@ -189,3 +189,82 @@ def test_pointer_and_void_entries_are_inert():
     assert fn(b"/nonexistent", None, ctypes.byref(err)) is None
     assert b"memoryMapFile: not provided" in ctypes.string_at(err.message)
     lib.free_c_error_message(err.message)
+
+
+CGO_PSEUDO = {"CString", "GoString", "GoBytes", "GoStringN", "CBytes", "int", "long", "float", "double", "bool", "uint",
+              "size_t", "void", "char", "uchar", "ulong", "schar", "short", "ushort", "longlong", "ulonglong"}
+
+
+def cgo_preamble(text):
+    """The cgo preamble of a Go file: the comment right above `import "C"` (a /* */ block or
+    consecutive // lines), or None."""
+    lines = text.split("\n")
+    idx = next((i for i, l in enumerate(lines) if l.strip() == 'import "C"'), None)
+    if idx is None:
+        return None
+    j = idx - 1
+    if lines[j].strip().endswith("*/"):
+        k = j
+        while "/*" not in lines[k]:
+            k -= 1
+        block = "\n".join(lines[k:j + 1])
+        return block[block.index("/*") + 2:block.rindex("*/")]
+    out = []
+    while j >= 0 and lines[j].lstrip().startswith("//"):
+        out.append(lines[j].lstrip()[2:])
+        j -= 1
+    return "\n".join(reversed(out))
+
+
+def test_integration_script_resolves_every_cgo_name_of_every_go_file():
+    """go-nngpu_amd/integrate_go.sh applied to a copy of the reference's Go packages: then no
+    macOS-only directive is left, and for every Go file with a cgo preamble, that preamble
+    (which includes the replaced internal/cgo/metal_bridge.h) declares every C name the file
+    uses, which is what cgo checks first ("could not determine kind of name for C.x").
+    Each preamble is compiled by gcc with a reference to each such name."""
+    import re
+    import shutil
+
+    if not os.path.exists(REF_HEADER):
+        pytest.skip("reference checkout not present")
+    with tempfile.TemporaryDirectory() as d:
+        for sub in ("gpu", "tensor", "internal"):
+            shutil.copytree(os.path.join(REF, sub), os.path.join(d, sub))
+        r = subprocess.run(["sh", os.path.join(ROOT, "go-nngpu_amd", "integrate_go.sh"), d, ROOT],
+                           capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr
+        assert not [f for f in os.listdir(os.path.join(d, "internal", "cgo")) if f.endswith((".m", ".metal"))]
+        fused = open(os.path.join(d, "gpu", "matrix", "fused-operations.go")).read()
+        assert "activationType := C.int(ReLU)" in fused and "C.int(OpReLU)" not in fused
+        checked = 0
+        for sub in ("gpu", "tensor", "internal"):
+            for root, _, files in os.walk(os.path.join(d, sub)):
+                for fn in sorted(files):
+                    if not fn.endswith(".go") or fn.endswith("_test.go"):
+                        continue
+                    path = os.path.join(root, fn)
+                    text = open(path).read()
+                    pre = cgo_preamble(text)
+                    if pre is None:
+                        continue
+                    directives = [l.strip() for l in pre.split("\n") if l.strip().startswith("#cgo")]
+                    assert directives and all("-lgonngpu" in l and "-framework" not in l for l in directives), \
+                        (path, directives)
+                    code = "\n".join(l for l in text.split("\n") if not l.lstrip().startswith("//"))
+                    names = sorted(set(re.findall(r"\bC\.([A-Za-z_]\w*)", code)) - CGO_PSEUDO)
+                    refs = []
+                    for n in names:
+                        if n in ("GPUPtr", "DevicePtr", "CError", "GPUCounters", "KernelCompileOptions"):
+                            refs.append(f"  (void)sizeof({n});")
+                        else:
+                            refs.append(f"  (void)&{n};")
+                    src = "\n".join(l for l in pre.split("\n") if not l.strip().startswith("#cgo"))
+                    src += "\nvoid cgo_name_check(void) {\n" + "\n".join(refs) + "\n}\n"
+                    cfile = os.path.join(root, "_cgo_check_" + fn[:-3] + ".c")
+                    with open(cfile, "w") as f:
+                        f.write(src)
+                    r = subprocess.run(["gcc", "-std=gnu11", "-fsyntax-only", "-Werror", cfile], capture_output=True,
+                                       text=True)
+                    assert r.returncode == 0, (path, r.stderr[-3000:])
+                    checked += 1
+        assert checked == 35
