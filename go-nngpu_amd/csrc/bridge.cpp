@@ -41,6 +41,11 @@ int sync(hipStream_t s, CError *err, int code) {
   return 0;
 }
 
+// The Part-1 SpMV uses the grouped layout (spmv_grouped.hip) for cached structures from this
+// many stored entries: below it the kernel is launch-bound and the layout's memory and one-time
+// build do not pay.
+constexpr long kGroupedSpmvMinNnz = 1L << 18;
+
 bool fits(const Buffer *b, long rows, long cols, size_t esz) {
   size_t n;
   return gn::matrix_bytes(rows, cols, esz, &n) && n <= b->bytes;
@@ -66,7 +71,14 @@ struct CsrEntry {
   std::vector<int> rp_copy;
   void *d_rp = nullptr, *d_col = nullptr;
   std::atomic<long> validated_bound{-1};  // the K the indices were checked against (-1: none)
+  // The grouped SpMV layout of this structure, built by the first SpMV that finds the entry
+  // validated, for that K (spmv_for: the K the build was tried for; an empty layout then
+  // means the structure does not take it). Under layout_mu.
+  std::mutex layout_mu;
+  gn::SpmvLayout spmv;
+  long spmv_for = -1;
   ~CsrEntry() {  // stream-ordered: after every call already enqueued with this entry
+    gn::free_spmv_layout(&spmv, gn::resolve_stream(nullptr));
     gn::dev_free(d_rp);
     gn::dev_free(d_col);
   }
@@ -136,7 +148,9 @@ void csr_cache_forget(const Buffer *key, const CsrEntry *only) {
 // `values`, when there is one), runs fn, which enqueues the work on s (no
 // synchronisation), waits for it, and converts the kernel's validation flags into the
 // reference's error convention. fn must only write its outputs, so enqueuing it a second
-// time gives the same result.
+// time gives the same result. fn's last argument is the cache entry when the indices it gets
+// are the entry's and already validated for this call's bound (so fn may use data derived
+// from them, such as the grouped SpMV layout), else nullptr.
 template <typename Fn>
 int with_csr(const Buffer *values, const int *rowptr, long rows, const int *cols, long nnz, long bound,
              hipStream_t s, CError *err, Fn fn) {
@@ -155,7 +169,8 @@ int with_csr(const Buffer *values, const int *rowptr, long rows, const int *cols
     std::shared_ptr<CsrEntry> cur = csr_lookup(values);
     if (cur && cur->validated_bound.load(std::memory_order_acquire) == bound && cur->host_rp == rowptr &&
         cur->host_col == cols && cur->rows == rows && cur->nnz == nnz) {
-      if (int rc = fn(static_cast<const int32_t *>(cur->d_rp), static_cast<const int32_t *>(cur->d_col), nullptr))
+      if (int rc = fn(static_cast<const int32_t *>(cur->d_rp), static_cast<const int32_t *>(cur->d_col), nullptr,
+                      cur.get()))
         return rc;
       if (memcmp(cur->rp_copy.data(), rowptr, sizeof(int) * (size_t)(rows + 1)) == 0) return sync(s, err, -6);
       csr_cache_forget(values, cur.get());
@@ -164,14 +179,14 @@ int with_csr(const Buffer *values, const int *rowptr, long rows, const int *cols
     if (!e) return -3;
     const int32_t *d_rp = static_cast<const int32_t *>(e->d_rp), *d_col = static_cast<const int32_t *>(e->d_col);
     if (e->validated_bound.load(std::memory_order_acquire) == bound) {
-      if (int rc = fn(d_rp, d_col, nullptr)) return rc;
+      if (int rc = fn(d_rp, d_col, nullptr, e.get())) return rc;
       return sync(s, err, -6);
     }
     Scratch d_flags;
     d_flags.p = gn::dev_alloc(2 * sizeof(int), err);
     if (!d_flags.p) return -3;
     if (int rc = gn::launch_zero_i32(static_cast<int *>(d_flags.p), 2, s, err)) return rc;
-    if (int rc = fn(d_rp, d_col, static_cast<int *>(d_flags.p))) return rc;
+    if (int rc = fn(d_rp, d_col, static_cast<int *>(d_flags.p), nullptr)) return rc;
     if (int rc = sync(s, err, -6)) return rc;
     int flags[2] = {0, 0};
     if (int rc = gn::download(flags, d_flags.p, sizeof(flags), s, err)) return rc;
@@ -196,7 +211,7 @@ int with_csr(const Buffer *values, const int *rowptr, long rows, const int *cols
     if (int rc = gn::upload(d_col.p, cols, sizeof(int) * (size_t)nnz, s, err)) return rc;
   if (int rc = gn::launch_zero_i32(static_cast<int *>(d_flags.p), 2, s, err)) return rc;
   if (int rc = fn(static_cast<const int32_t *>(d_rp.p), static_cast<const int32_t *>(d_col.p),
-                  static_cast<int *>(d_flags.p)))
+                  static_cast<int *>(d_flags.p), nullptr))
     return rc;
   if (int rc = sync(s, err, -6)) return rc;
   int flags[2] = {0, 0};
@@ -415,7 +430,7 @@ int perform_sparse_dense_matmul(GPUPtr aValuesPtr, int *aRowPtr, long aRowPtrLen
     return set_error(err, -2, "Buffer smaller than the matrix it describes.");
   const float *vals = v ? static_cast<const float *>(v->dptr) : nullptr;
   return with_csr(v, aRowPtr, aRows, aColIndices, aNNZ, aCols, ctx->stream, err,
-                  [&](const int32_t *rp, const int32_t *col, int *flags) -> int {
+                  [&](const int32_t *rp, const int32_t *col, int *flags, CsrEntry *) -> int {
                     int rc = gn::launch_spmm(aRows, bCols, aCols, aNNZ, rp, col, vals,
                                              static_cast<const float *>(b->dptr), bCols,
                                              static_cast<float *>(c->dptr), resultCols, flags, ctx->stream, err);
@@ -441,12 +456,25 @@ int perform_sparse_matvec(GPUPtr aValuesPtr, int *aRowPtr, long aRowPtrLen, int 
   if (!fits(x, 1, xSize, 4) || !fits(y, 1, resultSize, 4) || (v && !fits(v, 1, aNNZ, 4)))
     return set_error(err, -1, "Buffer smaller than the vector it describes.");
   const float *vals = v ? static_cast<const float *>(v->dptr) : nullptr;
+  const float *xp = static_cast<const float *>(x->dptr);
+  float *yp = static_cast<float *>(y->dptr);
   return with_csr(v, aRowPtr, aRows, aColIndices, aNNZ, aCols, ctx->stream, err,
-                  [&](const int32_t *rp, const int32_t *col, int *flags) -> int {
-                    int rc = gn::launch_spmv(aRows, aCols, aNNZ, rp, col, vals,
-                                             static_cast<const float *>(x->dptr), static_cast<float *>(y->dptr),
-                                             flags, ctx->stream, err);
-                    return rc;
+                  [&](const int32_t *rp, const int32_t *col, int *flags, CsrEntry *entry) -> int {
+                    // A cached, validated structure of at least kGroupedSpmvMinNnz entries gets the
+                    // grouped layout (built once, on the first such call) and its kernel.
+                    if (entry && aNNZ >= kGroupedSpmvMinNnz && gn::spmv_grouped_supported(aRows, aCols, aNNZ)) {
+                      std::lock_guard<std::mutex> lk(entry->layout_mu);
+                      if (entry->spmv_for != aCols) {
+                        gn::free_spmv_layout(&entry->spmv, ctx->stream);
+                        // an allocation failure leaves no layout: the flat kernel serves
+                        (void)gn::build_spmv_layout(aRows, aCols, aNNZ, entry->rp_copy.data(), col, ctx->num_cus,
+                                                    ctx->stream, &entry->spmv, nullptr);
+                        entry->spmv_for = aCols;
+                      }
+                      if (entry->spmv.blk) return gn::launch_spmv_grouped(entry->spmv, rp, vals, xp, yp, flags,
+                                                                          ctx->stream, err);
+                    }
+                    return gn::launch_spmv(aRows, aCols, aNNZ, rp, col, vals, xp, yp, flags, ctx->stream, err);
                   });
 }
 
@@ -576,7 +604,7 @@ int perform_dense_sparse_matmul(GPUPtr aMatrixPtr, long aRows, long aCols, GPUPt
   if (rc) return rc;
   const float *vals = bv ? static_cast<const float *>(bv->dptr) : nullptr;
   rc = with_csr(bv, bColPtr, bCols, bRowIndices, bNNZ, aCols, s, err,
-                [&](const int32_t *cp, const int32_t *rows, int *flags) -> int {
+                [&](const int32_t *cp, const int32_t *rows, int *flags, CsrEntry *) -> int {
                   int r = gn::launch_spmm(bCols, aRows, aCols, bNNZ, cp, rows, vals, static_cast<const float *>(at.p),
                                           aRows, static_cast<float *>(ct.p), aRows, flags, s, err);
                   if (!r) r = gn::launch_transpose_f32(static_cast<const float *>(ct.p), bCols, aRows,
@@ -694,7 +722,7 @@ int perform_sparse_to_dense(GPUPtr valuesPtr, int *rowPtr, long rowPtrLen, int *
   if (rows == 0 || cols == 0) return 0;
   const float *vals = v ? static_cast<const float *>(v->dptr) : nullptr;
   return with_csr(v, rowPtr, rows, colIndices, nnz, cols, ctx->stream, err,
-                  [&](const int32_t *rp, const int32_t *col, int *flags) -> int {
+                  [&](const int32_t *rp, const int32_t *col, int *flags, CsrEntry *) -> int {
                     return gn::launch_csr_to_dense(rows, cols, nnz, rp, col, vals, static_cast<float *>(d->dptr), flags,
                                                    ctx->stream, err);
                   });
@@ -869,6 +897,66 @@ int gn_spmv_csr(long M, long K, long nnz, const int32_t *rowptr, const int32_t *
                 const float *x, float *y, int *error_flags, void *stream, CError *err) {
   if (!gn::context(err)) return -1;
   return gn::launch_spmv(M, K, nnz, rowptr, col, val, x, y, error_flags, gn::resolve_stream(stream), err);
+}
+
+}  // extern "C"
+
+namespace {
+struct SpmvPlan {
+  uint64_t magic;
+  long M, K, nnz;
+  const int32_t *rowptr, *col;
+  gn::SpmvLayout layout;  // empty: the plain kernel (no stored entries)
+};
+constexpr uint64_t kSpmvPlanMagic = 0x676E73706D76504CULL;  // "gnspmvPL"
+}  // namespace
+
+extern "C" {
+
+int gn_spmv_plan_create(long M, long K, long nnz, const int32_t *rowptr, const int32_t *col, void **plan,
+                        void *stream, CError *err) {
+  if (!plan) return set_error(err, -1, "spmv plan: NULL plan pointer");
+  *plan = nullptr;
+  gn::Context *ctx = gn::context(err);
+  if (!ctx) return -1;
+  if (M < 0 || K < 0 || nnz < 0) return set_error(err, -1, "spmv plan: negative size");
+  if (!rowptr || (nnz > 0 && !col)) return set_error(err, -1, "spmv plan: NULL pointer");
+  if (nnz > 0x7FFFFFFFL || M > 0x7FFFFFF0L) return set_error(err, -1, "spmv plan: exceeds int32 CSR indexing");
+  hipStream_t s = gn::resolve_stream(stream);
+  std::vector<int32_t> h_rp((size_t)M + 1);
+  if (int rc = gn::download(h_rp.data(), rowptr, sizeof(int32_t) * h_rp.size(), s, err)) return rc;
+  for (long r = 0; r < M; ++r)
+    if (h_rp[r] < 0 || h_rp[r + 1] < h_rp[r] || h_rp[r + 1] > nnz)
+      return set_error(err, -1, "malformed CSR: row pointers are not monotone within [0, nnz]");
+  auto *p = new SpmvPlan{kSpmvPlanMagic, M, K, nnz, rowptr, col, {}};
+  // A structure that does not take the layout (build returns 1) keeps the flat kernel.
+  if (int rc = gn::build_spmv_layout(M, K, nnz, h_rp.data(), col, ctx->num_cus, s, &p->layout, err); rc < 0) {
+    delete p;
+    return rc;
+  }
+  *plan = p;
+  return 0;
+}
+
+int gn_spmv_plan_run(const void *plan, const float *val, const float *x, float *y, int *error_flags, void *stream,
+                     CError *err) {
+  if (!gn::context(err)) return -1;
+  const SpmvPlan *p = static_cast<const SpmvPlan *>(plan);
+  if (!p || p->magic != kSpmvPlanMagic) return set_error(err, -1, "spmv plan: not a live plan");
+  hipStream_t s = gn::resolve_stream(stream);
+  if (p->M == 0) return 0;
+  if (!y || (p->nnz > 0 && !val) || (p->K > 0 && !x)) return set_error(err, -1, "spmv plan: NULL pointer");
+  if (!p->layout.blk)
+    return gn::launch_spmv(p->M, p->K, p->nnz, p->rowptr, p->col, val, x, y, error_flags, s, err);
+  return gn::launch_spmv_grouped(p->layout, p->rowptr, val, x, y, error_flags, s, err);
+}
+
+void gn_spmv_plan_release(void *plan, void *stream) {
+  SpmvPlan *p = static_cast<SpmvPlan *>(plan);
+  if (!p || p->magic != kSpmvPlanMagic) return;
+  gn::free_spmv_layout(&p->layout, gn::resolve_stream(stream));
+  p->magic = 0;
+  delete p;
 }
 
 int gn_fill_uniform_f32(float *out, size_t n, uint64_t seed, uint64_t stream_id, float lo, float hi, void *stream,

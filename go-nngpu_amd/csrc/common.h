@@ -156,6 +156,31 @@ int launch_act_backward_from_output(const float *gout, const float *y, float *gi
 int launch_softmax_backward(const float *g, const float *y, float *gin, long rows, long cols, hipStream_t s,
                             CError *err);
 
+// spmv_grouped.hip: CSR SpMV over a one-time layout of the structure (row blocks, entries
+// of each block grouped by the 128-byte line of x they gather). Bit-identical to an fmaf
+// loop over each row in CSR order.
+struct SpmvLayout {
+  long M = 0, K = 0, nnz = 0;
+  int nblocks = 0, cap = 0;     // blocks (workgroups) and the most entries in one
+  int32_t *blk = nullptr;       // nblocks + 1 row starts, then nblocks + 1 entry offsets
+  uint32_t *word = nullptr;     // K <= 65536: column | CSR position << 16 | bad-column bit 31
+  int32_t *scol = nullptr;      // K > 65536: columns, grouped within each block
+  uint16_t *spos = nullptr;     //   and each one's position in its block's CSR order
+};
+bool spmv_grouped_supported(long M, long K, long nnz);
+// Builds the layout for rows [0, M) of a CSR structure whose row pointers are validated
+// (non-decreasing within [0, nnz]; host copy h_rowptr) and whose columns are on the device
+// (d_col): allocates from the pool and enqueues the grouping kernel on s. Returns 0 when
+// built, 1 when the structure does not take the layout (an unsupported shape, or a row of
+// more than 4096 entries; *out stays empty), a negative code on failure.
+int build_spmv_layout(long M, long K, long nnz, const int32_t *h_rowptr, const int32_t *d_col, int num_cus,
+                      hipStream_t s, SpmvLayout *out, CError *err);
+void free_spmv_layout(SpmvLayout *l, hipStream_t s);  // stream-ordered on s
+// y = S x with the layout; d_rowptr are the structure's row pointers; flags[1] is raised for
+// a column outside [0, K).
+int launch_spmv_grouped(const SpmvLayout &l, const int32_t *d_rowptr, const float *val, const float *x, float *y,
+                        int *flags, hipStream_t s, CError *err);
+
 // bridge.cpp helpers shared with bridge_compat.cpp.
 // Waits for the work enqueued on s, as the reference's waitUntilCompleted does; returns
 // code (with the HIP error in err) on a device error.

@@ -108,6 +108,9 @@ SIGNATURES = {
     "perform_activation_gelu_forward": (_I, [_VP, _L, _VP, _VP, _ERR]),
     "gn_spmm_csr": (_I, [_L, _L, _L, _L, _VP, _VP, _VP, _VP, _L, _VP, _L, _VP, _VP, _ERR]),
     "gn_spmv_csr": (_I, [_L, _L, _L, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _ERR]),
+    "gn_spmv_plan_create": (_I, [_L, _L, _L, _VP, _VP, ctypes.POINTER(_VP), _VP, _ERR]),
+    "gn_spmv_plan_run": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _ERR]),
+    "gn_spmv_plan_release": (None, [_VP, _VP]),
     "gn_fill_uniform_f32": (_I, [_VP, _SZ, _U64, _U64, _F, _F, _VP, _ERR]),
     "gn_fill_normal_f32": (_I, [_VP, _SZ, _U64, _U64, _F, _F, _VP, _ERR]),
     # Part 3: the other reference-bridge entries with a device implementation. The rest of
@@ -328,6 +331,28 @@ def spmm_csr(M, N, K, nnz, rowptr, col, val, D, C, flags=None, ldd=None, ldc=Non
 
 def spmv_csr(M, K, nnz, rowptr, col, val, x, y, flags=None, stream_ptr=None):
     _dispatch(stream_ptr, "gn_spmv_csr", M, K, nnz, _ptr(rowptr), _ptr(col), _ptr(val), _ptr(x), _ptr(y), _ptr(flags))
+
+
+class SpmvPlan:
+    """A grouped-layout SpMV plan over device CSR arrays (gn_spmv_plan_*). The row pointer
+    and column tensors must outlive the plan and stay unchanged."""
+
+    def __init__(self, M, K, nnz, rowptr, col, stream_ptr=None):
+        import torch
+
+        self.handle = _VP()
+        self._keep = (rowptr, col)
+        sp = stream_ptr if stream_ptr is not None else torch.cuda.current_stream().cuda_stream
+        call("gn_spmv_plan_create", M, K, nnz, _ptr(rowptr), _ptr(col), ctypes.byref(self.handle), sp or None)
+        self._stream = sp or None
+
+    def run(self, val, x, y, flags=None, stream_ptr=None):
+        _dispatch(stream_ptr, "gn_spmv_plan_run", self.handle, _ptr(val), _ptr(x), _ptr(y), _ptr(flags))
+
+    def release(self, stream_ptr=None):
+        if self.handle:
+            load().gn_spmv_plan_release(self.handle, stream_ptr if stream_ptr is not None else self._stream)
+            self.handle = _VP()
 
 
 def fill_uniform(out, seed, stream_id, lo=-1.0, hi=1.0, stream_ptr=None):

@@ -404,6 +404,22 @@ int gn_spmm_csr(long M, long N, long K, long nnz, const int32_t *rowptr, const i
 /* CSR SpMV on device arrays: y[M] = S[M,K] * x[K]; error_flags as gn_spmm_csr. */
 int gn_spmv_csr(long M, long K, long nnz, const int32_t *rowptr, const int32_t *col, const float *val,
                 const float *x, float *y, int *error_flags, void *stream, CError *err);
+/* SpMV plan: a one-time analysis of a CSR structure (device arrays) for repeated y = S x
+ * with it. No counterpart in the reference; its perform_sparse_matvec gets the same layout
+ * through the index arrays kept with the values buffer. Create copies the row pointers to the
+ * host and checks them (non-decreasing within [0, nnz]; -1 otherwise), then builds the
+ * grouped layout on the device: rows cut into blocks, each block's entries ordered by the
+ * 128-byte line of x they gather (6 bytes per stored entry). Run sums each row in CSR order
+ * with one fused multiply-add per entry (bit-identical to the reference loop restated with
+ * fmaf); error_flags[1] as gn_spmv_csr. rowptr and col must stay unchanged and allocated
+ * while the plan lives; values and x may change between runs. Release frees the layout in
+ * the order of `stream` (pass the stream of the last run). Codes: -1 invalid argument,
+ * -3 allocation failed, -6 launch error. */
+int gn_spmv_plan_create(long M, long K, long nnz, const int32_t *rowptr, const int32_t *col, void **plan,
+                        void *stream, CError *err);
+int gn_spmv_plan_run(const void *plan, const float *val, const float *x, float *y, int *error_flags, void *stream,
+                     CError *err);
+void gn_spmv_plan_release(void *plan, void *stream);
 
 /* Synthetic data on device: the counter-based SplitMix64 generator
  * (element i of stream s: mix64(seed ^ mix64(s + 0x632BE59BD9B4E019) + (i+1)*0x9E3779B97F4A7C15)),
