@@ -149,8 +149,9 @@ void csr_cache_forget(const Buffer *key, const CsrEntry *only) {
 // synchronisation), waits for it, and converts the kernel's validation flags into the
 // reference's error convention. fn must only write its outputs, so enqueuing it a second
 // time gives the same result. fn's last argument is the cache entry when the indices it gets
-// are the entry's and already validated for this call's bound (so fn may use data derived
-// from them, such as the grouped SpMV layout), else nullptr.
+// are the entry's (so fn may keep data derived from them with it, such as the grouped SpMV
+// layout), else nullptr; its flags argument is nullptr once they are validated for this
+// call's bound.
 template <typename Fn>
 int with_csr(const Buffer *values, const int *rowptr, long rows, const int *cols, long nnz, long bound,
              hipStream_t s, CError *err, Fn fn) {
@@ -186,7 +187,7 @@ int with_csr(const Buffer *values, const int *rowptr, long rows, const int *cols
     d_flags.p = gn::dev_alloc(2 * sizeof(int), err);
     if (!d_flags.p) return -3;
     if (int rc = gn::launch_zero_i32(static_cast<int *>(d_flags.p), 2, s, err)) return rc;
-    if (int rc = fn(d_rp, d_col, static_cast<int *>(d_flags.p), nullptr)) return rc;
+    if (int rc = fn(d_rp, d_col, static_cast<int *>(d_flags.p), e.get())) return rc;
     if (int rc = sync(s, err, -6)) return rc;
     int flags[2] = {0, 0};
     if (int rc = gn::download(flags, d_flags.p, sizeof(flags), s, err)) return rc;
@@ -460,15 +461,24 @@ int perform_sparse_matvec(GPUPtr aValuesPtr, int *aRowPtr, long aRowPtrLen, int 
   float *yp = static_cast<float *>(y->dptr);
   return with_csr(v, aRowPtr, aRows, aColIndices, aNNZ, aCols, ctx->stream, err,
                   [&](const int32_t *rp, const int32_t *col, int *flags, CsrEntry *entry) -> int {
-                    // A cached, validated structure of at least kGroupedSpmvMinNnz entries gets the
-                    // grouped layout (built once, on the first such call) and its kernel.
+                    // A cached structure of at least kGroupedSpmvMinNnz entries gets the grouped
+                    // layout, built by its first call for this K (the validating one, which then
+                    // reads the grouped kernel's column flag), so every call gives the same bits.
+                    // The layout needs row pointers that are non-decreasing within [0, nnz]:
+                    // checked on the host copy first; malformed ones keep the flat kernel, whose
+                    // flag reports them.
                     if (entry && aNNZ >= kGroupedSpmvMinNnz && gn::spmv_grouped_supported(aRows, aCols, aNNZ)) {
                       std::lock_guard<std::mutex> lk(entry->layout_mu);
                       if (entry->spmv_for != aCols) {
                         gn::free_spmv_layout(&entry->spmv, ctx->stream);
+                        const std::vector<int> &h = entry->rp_copy;
+                        bool monotone = true;
+                        for (long r = 0; r < aRows && monotone; ++r)
+                          monotone = h[r] >= 0 && h[r + 1] >= h[r] && h[r + 1] <= aNNZ;
                         // an allocation failure leaves no layout: the flat kernel serves
-                        (void)gn::build_spmv_layout(aRows, aCols, aNNZ, entry->rp_copy.data(), col, ctx->num_cus,
-                                                    ctx->stream, &entry->spmv, nullptr);
+                        if (monotone)
+                          (void)gn::build_spmv_layout(aRows, aCols, aNNZ, h.data(), col, ctx->num_cus, ctx->stream,
+                                                      &entry->spmv, nullptr);
                         entry->spmv_for = aCols;
                       }
                       if (entry->spmv.blk) return gn::launch_spmv_grouped(entry->spmv, rp, vals, xp, yp, flags,

@@ -184,11 +184,12 @@ def test_spmv_plan_rejects_malformed_row_pointers(dev):
         assert not h.value
 
 
-def test_spmv_part1_uses_grouped_layout_after_validation(dev):
-    """perform_sparse_matvec with host index arrays: the first call validates the indices
-    (flat kernel, tolerance), the next ones run the grouped layout kept with the values
-    buffer (bit-exact); a call with a larger column count validates again and rebuilds the
-    layout for it; releasing the values buffer frees the cached copy and the layout."""
+def test_spmv_part1_uses_grouped_layout(dev):
+    """perform_sparse_matvec with host index arrays: the first call uploads the indices,
+    builds the grouped layout and validates the columns through its kernel; every call,
+    the first included, gives the CSR-order fmaf bits. A call with a larger column count
+    validates again and rebuilds the layout for it; a bad column is refused; releasing the
+    values buffer frees the cached copy and the layout."""
     rng = np.random.default_rng(5)
     M, K = 8192, 16384
     lens = rng.poisson(40.0, M).astype(np.int64)  # ~330K entries: above the 2^18 threshold
@@ -197,26 +198,33 @@ def test_spmv_part1_uses_grouped_layout_after_validation(dev):
     ref = O.spmv_f32(rp, col, val, x, use_fma=True)
     bv, bx, by = G.Buffer.from_array(val), G.Buffer.from_array(x), G.Buffer(M * 4)
 
-    def run(k, xb):
-        G.call("perform_sparse_matvec", bv.handle, rp.ctypes.data, rp.size, col.ctypes.data, col.size, M, k, val.size,
-               xb.handle, k, by.handle, M, None)
-        return by.to_array((M,))
+    def run(k, xb, c=col):
+        rc, msg = G.call_rc("perform_sparse_matvec", bv.handle, rp.ctypes.data, rp.size, c.ctypes.data, c.size, M, k,
+                            val.size, xb.handle, k, by.handle, M, None)
+        return rc, msg, (by.to_array((M,)) if rc == 0 else None)
 
     n0 = G.memory_stats()[2]
-    y1 = run(K, bx)
-    assert O.rel_frob(y1, O.spmv_f64(rp, col, val, x)) <= 1e-5
-    n1 = G.memory_stats()[2]
-    y2 = run(K, bx)
-    n2 = G.memory_stats()[2]
-    assert n2 == n1 + 2  # the packed layout (K <= 65536): block offsets, grouped words
-    np.testing.assert_array_equal(y2, ref)
-    np.testing.assert_array_equal(run(K, bx), ref)
+    rc, _, y1 = run(K, bx)
+    assert rc == 0
+    np.testing.assert_array_equal(y1, ref)
+    # the cached row pointers and columns, and the packed layout (K <= 65536): block
+    # offsets and grouped words
+    assert G.memory_stats()[2] == n0 + 4
+    for _ in range(2):
+        np.testing.assert_array_equal(run(K, bx)[2], ref)
+    assert G.memory_stats()[2] == n0 + 4
     # a larger column count (x extended with values the indices never reach)
     K2 = K + 4096
     x_big = np.concatenate([x, rng.standard_normal(4096).astype(np.float32)])
     bxb = G.Buffer.from_array(x_big)
-    run(K2, bxb)  # validates for K2
-    np.testing.assert_array_equal(run(K2, bxb), O.spmv_f32(rp, col, val, x_big, use_fma=True))
+    ref2 = O.spmv_f32(rp, col, val, x_big, use_fma=True)
+    for _ in range(2):
+        np.testing.assert_array_equal(run(K2, bxb)[2], ref2)
+    # a column outside [0, K) in a new host array: refused, through the grouped kernel's flag
+    bad = col.copy()
+    bad[12345] = K + 1
+    rc, msg, _ = run(K, bx, bad)
+    assert rc == -3 and "column" in msg
     bv.release()
     for b in (bx, bxb, by):
         b.release()
