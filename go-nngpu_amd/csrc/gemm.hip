@@ -26,6 +26,7 @@
 //    panels in that XCD's L2.
 #include "act.h"
 #include "common.h"
+#include "ring_plan.h"
 
 namespace gn {
 namespace {
@@ -503,14 +504,14 @@ struct BufRsrc {
   i32x4_t r;
 };
 
-// Raw buffer descriptor: 48-bit base, stride 0, num_records 0x7ffffff0 (offsets at or
-// beyond it read as zero), gfx9 dword3.
+// Raw buffer descriptor: 48-bit base, stride 0, num_records ring::kNumRecords (offsets at
+// or beyond it read as zero), gfx9 dword3.
 __device__ __forceinline__ BufRsrc make_rsrc(const void *base) {
   const unsigned long long b = (unsigned long long)base;
   BufRsrc s;
   s.r.x = __builtin_amdgcn_readfirstlane((int)(b & 0xffffffffu));
   s.r.y = __builtin_amdgcn_readfirstlane((int)(b >> 32) & 0xffff);
-  s.r.z = 0x7ffffff0;
+  s.r.z = (int)ring::kNumRecords;
   s.r.w = 0x00020000;
   return s;
 }
@@ -537,7 +538,11 @@ __device__ __forceinline__ void dma16(const BufRsrc &s, unsigned voff, unsigned 
       : "memory");
 }
 
-constexpr unsigned kOutOfRange = 0x80000000u;
+using ring::hsw;
+using ring::kc8_octet;
+using ring::kc8_slot;
+using ring::kOutOfRange;
+using ring::msw32;
 
 // s_waitcnt immediate that waits for vmcnt <= n only (vmcnt[3:0] in bits 3:0 and
 // vmcnt[5:4] in bits 15:14; expcnt and lgkmcnt at their maxima).
@@ -547,8 +552,6 @@ __device__ __forceinline__ unsigned lds_offset(const void *p) {
   return (unsigned)(unsigned long)(const LDS_AS void *)p;
 }
 
-// 32-byte block XOR of row k of an MN-contiguous tile.
-__device__ __forceinline__ int hsw(int k) { return (k & 3) | ((k >> 1) & 4); }
 
 // K-contiguous tiles: a 1 KiB DMA chunk holds rows 8c..8c+7 with the 64 k of a K-tile
 // pair (128 bytes) each. Lane L copies 16 bytes of row 8c + (L >> 3), so each lane
@@ -557,9 +560,8 @@ __device__ __forceinline__ int hsw(int k) { return (k & 3) | ((k >> 1) & 4); }
 // four rows stalled the address unit on the L1 cache). The hardware writes lane L's
 // bytes to slot L of the chunk, so the octet it loads is permuted: octet o of row r sits
 // in slot 8 (r & 7) + (o ^ ((r >> 1) & 7)), and the 16 rows an MFMA fragment read
-// touches (two chunks, fixed o) land on 16 distinct 16-byte bank groups.
-__device__ __forceinline__ int kc8_slot(int r, int o) { return 8 * (r & 7) + (o ^ ((r >> 1) & 7)); }
-__device__ __forceinline__ int kc8_octet(int r, int j) { return j ^ ((r >> 1) & 7); }
+// touches (two chunks, fixed o) land on 16 distinct 16-byte bank groups (ring::kc8_slot,
+// ring::kc8_octet).
 
 // A scheduling region of NM MFMAs and NR LDS reads, interleaved 1:1 (then the rest).
 template <int NM, int NR>
@@ -620,31 +622,22 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
   unsigned voa[IPA], vob[IPB];
   int kla[IPA], klb[IPB];
   auto plan = [&](bool kcontig, int c, int nchunks, int rb_bytes, long ld, long lim, unsigned &vo, int &kl) {
-    const int h = c / (nchunks / 2), cl = c % (nchunks / 2);
-    if (kcontig) {  // chunk c: rows 8c..8c+7, the pair's 64 k (128 bytes) each
-      const int row = 8 * c + (lane >> 3), q = kc8_octet(row, lane & 7);
-      kl = 8 * q;
-      vo = lim > row ? (unsigned)((long)row * ld * 2 + 16 * q) : kOutOfRange;
-      return;
-    }
-    const int gpr = rb_bytes / 16;
-    const int k = cl * (1024 / rb_bytes) + lane / gpr, qp = lane % gpr;
-    const int q = 2 * ((qp >> 1) ^ hsw(k)) + (qp & 1);
-    kl = 32 * h + k;
-    vo = lim > 8 * q ? (unsigned)((long)(32 * h + k) * ld * 2 + 16 * q) : kOutOfRange;
+    const ring::Copy cp = ring::plan_f16(kcontig, c, nchunks, rb_bytes, ld, lim, lane);
+    vo = cp.vo;
+    kl = cp.kl;
   };
   {
     const _Float16 *A = static_cast<const _Float16 *>(p.A) + z * p.strideA;
     const _Float16 *B = static_cast<const _Float16 *>(p.B) + z * p.strideB;
-    ra = make_rsrc(TA ? A + m0 : A + m0 * p.lda);
-    rb = make_rsrc(TB ? B + n0 * p.ldb : B + n0);
+    ra = make_rsrc(A + ring::base_elems(!TA, m0, p.lda));
+    rb = make_rsrc(B + ring::base_elems(TB, n0, p.ldb));
   }
 #pragma unroll
   for (int i = 0; i < IPA; ++i) plan(!TA, wave * IPA + i, CA, RBA, p.lda, p.M - m0, voa[i], kla[i]);
 #pragma unroll
   for (int i = 0; i < IPB; ++i) plan(TB, wave * IPB + i, CB, RBB, p.ldb, p.N - n0, vob[i], klb[i]);
-  const long a_step = TA ? 2L * BK * p.lda * 2 : 2L * BK * 2;
-  const long b_step = TB ? 2L * BK * 2 : 2L * BK * p.ldb * 2;
+  const long a_step = ring::pair_step_bytes(!TA, BK, p.lda, 2);
+  const long b_step = ring::pair_step_bytes(TB, BK, p.ldb, 2);
   const unsigned sbase = lds_offset(smem);
   const int np = max(1, (nk + 1) >> 1);  // pairs the loop runs; tiles past nk are zeros
 
@@ -653,20 +646,20 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
   // also advances both descriptors to the next pair.
   auto issue = [&](int pp, int slot, int q, int NPRT) {
     const unsigned st = sbase + (unsigned)(slot * SLOT);
-    const long krem_l = p.K - (long)pp * 2 * BK;
-    const int krem = (int)(krem_l < 0 ? 0 : (krem_l > 2 * BK ? 2 * BK : krem_l));
+    const int krem = ring::f16_krem(p.K, pp);
     const int half = NPRT / 2;
     const bool last_call = q == NPRT - 1;
     if (q < half) {
 #pragma unroll
       for (int i = 0; i < IPA; ++i)
         if (i * half / IPA == q)
-          dma16(ra, kla[i] < krem ? voa[i] : kOutOfRange, __builtin_amdgcn_readfirstlane(st + (wave * IPA + i) * 1024));
+          dma16(ra, ring::f16_offset({voa[i], kla[i]}, krem),
+                __builtin_amdgcn_readfirstlane(st + (wave * IPA + i) * 1024));
     } else {
 #pragma unroll
       for (int i = 0; i < IPB; ++i)
         if (i * half / IPB == q - half)
-          dma16(rb, klb[i] < krem ? vob[i] : kOutOfRange,
+          dma16(rb, ring::f16_offset({vob[i], klb[i]}, krem),
                 __builtin_amdgcn_readfirstlane(st + 2 * OPA + (wave * IPB + i) * 1024));
     }
     if (last_call) {
@@ -850,7 +843,6 @@ gemm_f16_ring_kernel(GemmParams p) {
 // with ds_read_b32. Copies are whole 16-byte blocks checked by their first element, so
 // every contiguous extent (K of a K-contiguous operand, M or N of an MN-contiguous one)
 // must be a multiple of 4 floats, as the dispatch's vector path guarantees.
-__device__ __forceinline__ int msw32(int k) { return ((k >> 2) & 1) << 2; }
 
 template <int BM, int BN, int WM, int WN, bool TA, bool TB, int NS>
 __device__ __forceinline__ void ring_mainloop_f32(const GemmParams &p, long m0, long n0, long z, int nk, char *smem,
@@ -880,31 +872,24 @@ __device__ __forceinline__ void ring_mainloop_f32(const GemmParams &p, long m0, 
   unsigned voa[IPA], vob[IPB];
   // Byte offset (from the pair's start) of this lane's 16-byte copy in chunk c; rows or
   // columns past M (or N) get the out-of-range offset.
+  // (K-contiguous chunk c: rows 8c..8c+7, the pair's 32 k (128 bytes) each; MN-contiguous
+  // chunk cl of tile h: k rows cl * (1024 / rb_bytes) .., lane L filling slot L % bpr of its
+  // row with block (L % bpr) ^ msw32(k).)
   auto plan = [&](bool kcontig, int c, int nchunks, int rb_bytes, long ld, long lim, unsigned &vo) {
-    if (kcontig) {  // chunk c: rows 8c..8c+7, the pair's 32 k (128 bytes) each
-      const int row = 8 * c + (lane >> 3), q = kc8_octet(row, lane & 7);
-      vo = lim > row ? (unsigned)((long)row * ld * 4 + 16 * q) : kOutOfRange;
-      return;
-    }
-    // chunk cl of tile h: k rows cl * (1024 / rb_bytes) ..; lane L fills slot L % bpr of
-    // its row with block (L % bpr) ^ msw32(k)
-    const int h = c / (nchunks / 2), cl = c % (nchunks / 2);
-    const int bpr = rb_bytes / 16;
-    const int k = cl * (1024 / rb_bytes) + lane / bpr, b = (lane % bpr) ^ msw32(k);
-    vo = lim > 4 * b ? (unsigned)((long)(BK * h + k) * ld * 4 + 16 * b) : kOutOfRange;
+    vo = ring::plan_f32(kcontig, c, nchunks, rb_bytes, ld, lim, lane);
   };
   {
     const float *A = static_cast<const float *>(p.A) + z * p.strideA;
     const float *B = static_cast<const float *>(p.B) + z * p.strideB;
-    ra = make_rsrc(TA ? A + m0 : A + m0 * p.lda);
-    rb = make_rsrc(TB ? B + n0 * p.ldb : B + n0);
+    ra = make_rsrc(A + ring::base_elems(!TA, m0, p.lda));
+    rb = make_rsrc(B + ring::base_elems(TB, n0, p.ldb));
   }
 #pragma unroll
   for (int i = 0; i < IPA; ++i) plan(!TA, wave * IPA + i, CA, RBA, p.lda, p.M - m0, voa[i]);
 #pragma unroll
   for (int i = 0; i < IPB; ++i) plan(TB, wave * IPB + i, CB, RBB, p.ldb, p.N - n0, vob[i]);
-  const long a_step = TA ? 2L * BK * p.lda * 4 : 2L * BK * 4;
-  const long b_step = TB ? 2L * BK * 4 : 2L * BK * p.ldb * 4;
+  const long a_step = ring::pair_step_bytes(!TA, BK, p.lda, 4);
+  const long b_step = ring::pair_step_bytes(TB, BK, p.ldb, 4);
   const unsigned sbase = lds_offset(smem);
   const int np = max(1, (nk + 1) >> 1);
 
@@ -917,7 +902,7 @@ __device__ __forceinline__ void ring_mainloop_f32(const GemmParams &p, long m0, 
   // Part q of NQ issues the wave's copies d (A's IPA, then B's IPB) with d * NQ / LPW == q;
   // the last part advances both descriptors.
   auto issue_part = [&](int pp, int slot, int q, int NQ) {
-    const bool live = pp < np;
+    const bool live = ring::f32_pair_live(pp, np);
     BufRsrc da = ra, db = rb;
     if (!live) {
       da.r.z = 0;
