@@ -896,6 +896,12 @@ int gn_transpose_f32(const float *in, long rows, long cols, float *out, void *st
   return gn::launch_transpose_f32(in, rows, cols, out, gn::resolve_stream(stream), err);
 }
 
+int gn_add_bias_cyclic_f32(float *y, long n, const float *bias, long len, void *stream, CError *err) {
+  if (!gn::context(err)) return -1;
+  if (n > 0 && (!y || !bias)) return set_error(err, -1, "cyclic bias add: NULL pointer");
+  return gn::launch_add_cyclic_f32(y, n, bias, len, gn::resolve_stream(stream), err);
+}
+
 int gn_spmm_csr(long M, long N, long K, long nnz, const int32_t *rowptr, const int32_t *col, const float *val,
                 const float *D, long ldd, float *C, long ldc, int *error_flags, void *stream, CError *err) {
   if (!gn::context(err)) return -1;

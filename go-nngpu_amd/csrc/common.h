@@ -145,6 +145,8 @@ bool act_supported(int act);
 int launch_binary_f32(int op, const float *a, const float *b, float *c, long n, long *first_zero, hipStream_t s,
                       CError *err);
 // c[i, j] = a[i * sa_r + j * sa_c] + b[i * sb_r + j * sb_c] over an M x N result.
+// y[i] += b[i % L], i < n (L > 0).
+int launch_add_cyclic_f32(float *y, long n, const float *b, long L, hipStream_t s, CError *err);
 int launch_add_broadcast_f32(const float *a, long sa_r, long sa_c, const float *b, long sb_r, long sb_c, float *c,
                              long M, long N, hipStream_t s, CError *err);
 // out = in * scalar (mul) or in + scalar.

@@ -88,6 +88,12 @@ __global__ void __launch_bounds__(kBlock) add_broadcast_kernel(const float *a, l
   }
 }
 
+// y[i] += b[i % L] over the flat array: the bias loop of the reference's ForwardFloat16
+// (mixed-precision.go:352-354) for a bias of any length L.
+__global__ void __launch_bounds__(kBlock) add_cyclic_kernel(float *y, long n, const float *b, long L) {
+  for (long k = (long)blockIdx.x * kBlock + threadIdx.x; k < n; k += (long)gridDim.x * kBlock) y[k] += b[k % L];
+}
+
 // ------------------------------------------------------------------ scalar
 template <bool MUL, bool VEC>
 __global__ void __launch_bounds__(kBlock) scalar_kernel(const float *in, float s, float *out, long n) {
@@ -250,6 +256,15 @@ int launch_add_broadcast_f32(const float *a, long sa_r, long sa_c, const float *
                      sb_r, sb_c, c, M, N);
   hipError_t e = last();
   return e == hipSuccess ? 0 : hip_error(err, -1, "broadcast add launch", e);
+}
+
+int launch_add_cyclic_f32(float *y, long n, const float *b, long L, hipStream_t s, CError *err) {
+  if (n < 0 || L < 0) return set_error(err, -1, "cyclic bias add: negative size");
+  if (n == 0) return 0;
+  if (L == 0) return set_error(err, -1, "cyclic bias add: empty bias");
+  hipLaunchKernelGGL(add_cyclic_kernel, dim3((unsigned)grid_for(n, 1)), dim3(kBlock), 0, s, y, n, b, L);
+  hipError_t e = last();
+  return e == hipSuccess ? 0 : hip_error(err, -6, "cyclic bias add launch", e);
 }
 
 int launch_scalar_f32(bool mul, const float *in, float scalar, float *out, long n, hipStream_t s, CError *err) {

@@ -396,9 +396,10 @@ class MixedPrecisionTrainer {
   explicit MixedPrecisionTrainer(std::shared_ptr<MixedPrecisionConfig> cfg);
   // :192-210: fp32 values rounded through FloatMP16 (stored as fp32).
   Result<TensorPtr> ConvertTensorToFloat16(const Tensor &input) const;
-  // :315-358: input x weights on fp16-rounded operands, plus the fp16-rounded bias
-  // broadcast over rows (bias length must equal the output width). Runs the cast and
-  // an fp16 MFMA GEMM (exact fp16 products, fp32 accumulation) on the device.
+  // :315-358: input x weights on fp16-rounded operands, plus the fp16-rounded bias added as
+  // the reference's loop does, result[i] += bias[i % len(bias)] over the flat output (in the
+  // GEMM epilogue when len is the output width). Runs the cast and an fp16 MFMA GEMM (exact
+  // fp16 products, fp32 accumulation) on the device; an empty bias is an error.
   Result<TensorPtr> ForwardFloat16(Tensor &input, Tensor &weights, Tensor *bias);
   // The same product with weights already converted (Float16Tensor::FromTensor with the
   // default truncation): bit-identical to the call above, without the weights' cast.

@@ -608,30 +608,37 @@ Result<TensorPtr> MixedPrecisionTrainer::ConvertTensorToFloat16(const Tensor &in
 namespace {
 // input (rounded to fp16 by truncation on the device) x w16 [K, N] (device fp16), plus
 // the fp16-rounded bias in the GEMM epilogue; device-resident fp32 result.
+// The bias is added as the reference's loop does, result[i] += bias[i % len] over the flat
+// output (mixed-precision.go:352-354): by the GEMM epilogue when len is the output width
+// (the same sum, one rounding), else by a cyclic add after the product.
 Result<TensorPtr> forward_f16(Tensor &input, const void *w16, long K, long N, Tensor *bias) {
   const long M = input.Shape[0];
-  if (bias && bias->Size() != N)
-    return {nullptr, Errorf("bias length (%ld) must equal the output width (%ld)", bias->Size(), N)};
+  const long L = bias ? bias->Size() : 0;
+  if (bias && L == 0 && M * N > 0)
+    return {nullptr, Errorf("bias is empty: the reference's bias loop would divide by zero")};
   if (Error e = input.EnsureGPU()) return {nullptr, wrap("failed to convert input to float16", e)};
-  if (bias)
+  if (bias && L > 0)
     if (Error e = bias->EnsureGPU()) return {nullptr, wrap("failed to convert bias to float16", e)};
   auto [result, rerr] = Tensor::NewDeviceResult({(int)M, (int)N});
   if (rerr) return {nullptr, wrap("failed to perform float16 matrix multiplication", rerr)};
   DeviceScratch a16, b16, bf;
   if (Error e = a16.alloc((size_t)(M * K) * 2)) return {nullptr, e};
-  if (bias) {
-    if (Error e = b16.alloc((size_t)N * 2)) return {nullptr, e};
-    if (Error e = bf.alloc((size_t)N * 4)) return {nullptr, e};
+  if (L > 0) {
+    if (Error e = b16.alloc((size_t)L * 2)) return {nullptr, e};
+    if (Error e = bf.alloc((size_t)L * 4)) return {nullptr, e};
   }
   CError ce{nullptr};
   int rc = gn_cast_f32_f16(dptr(input), (uint16_t *)a16.p, (size_t)(M * K), GN_ROUND_TOWARD_ZERO, nullptr, &ce);
-  if (rc == 0 && bias) {
-    rc = gn_cast_f32_f16(dptr(*bias), (uint16_t *)b16.p, (size_t)N, GN_ROUND_TOWARD_ZERO, nullptr, &ce);
-    if (rc == 0) rc = gn_cast_f16_f32((const uint16_t *)b16.p, (float *)bf.p, (size_t)N, nullptr, &ce);
+  if (rc == 0 && L > 0) {
+    rc = gn_cast_f32_f16(dptr(*bias), (uint16_t *)b16.p, (size_t)L, GN_ROUND_TOWARD_ZERO, nullptr, &ce);
+    if (rc == 0) rc = gn_cast_f16_f32((const uint16_t *)b16.p, (float *)bf.p, (size_t)L, nullptr, &ce);
   }
+  const bool epilogue = L > 0 && L == N;
   if (rc == 0)
     rc = gn_gemm(GN_F16, 0, 0, M, N, K, 1.0f, a16.p, K, 0, w16, N, 0, 0.0f, dptr(*result), N, 0, 1,
-                 bias ? (const float *)bf.p : nullptr, GN_ACT_NONE, 0.0f, nullptr, &ce);
+                 epilogue ? (const float *)bf.p : nullptr, GN_ACT_NONE, 0.0f, nullptr, &ce);
+  if (rc == 0 && L > 0 && !epilogue)
+    rc = gn_add_bias_cyclic_f32((float *)dptr(*result), M * N, (const float *)bf.p, L, nullptr, &ce);
   if (rc == 0) rc = gn_synchronize(nullptr, &ce);
   if (rc != 0) return {nullptr, op_error("float16 matrix multiplication", rc, ce)};
   return {result, {}};

@@ -388,6 +388,10 @@ int gn_graph_execute(void *compiledGraph, void *stream, GPUPtr const *inputs, lo
 void gn_graph_release(void *graphOrCompiled);
 
 int gn_transpose_f32(const float *in, long rows, long cols, float *out, void *stream, CError *err);
+/* y[i] += bias[i % len] for i < n: the bias loop of the reference's ForwardFloat16
+ * (gpu/matrix/mixed-precision.go:352-354), which adds a bias of any length cyclically over the
+ * flat output (the GEMM epilogue covers len == output width). len == 0 with n > 0: -1. */
+int gn_add_bias_cyclic_f32(float *y, long n, const float *bias, long len, void *stream, CError *err);
 
 /* CSR SpMM on device arrays: C[M,N] = S[M,K] * D[K,N] (ld = row pitch in elements).
  * Accumulates each output in CSR order with one fused multiply-add per stored entry.

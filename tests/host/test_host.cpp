@@ -622,8 +622,26 @@ void TestForwardFloat16() {
   for (int i = 0; i < M; ++i)
     for (int j = 0; j < N; ++j) ref_unrounded[(size_t)i * N + j] += b->Data[j];
   CHECK(rel(Y->Data, ref_unrounded) <= 2e-2);
-  auto wrong = NewTensor({N + 1}, std::vector<float>(N + 1)).value;
-  CHECK_ERR_HAS(mp->ForwardFloat16(*X, *W, wrong.get()).err, "bias length");
+  // A bias of any other length is added cyclically over the flat output, result[i] +=
+  // bias[i % len] (mixed-precision.go:352-354): the same fp32 sums as the product without a
+  // bias plus the rounded bias element, bit for bit.
+  auto [Y0, err0] = mp->ForwardFloat16(*X, *W, nullptr);
+  CHECK_NOERR(err0);
+  if (!Y0) return;
+  CHECK_NOERR(Y0->RetrieveCPU());
+  for (int L : {1, 7, N + 1, 2 * N, M * N}) {
+    auto bl = NewTensor({L}, uniform((size_t)L, 19 + L, -0.5f, 0.5f)).value;
+    auto blh = mp->ConvertTensorToFloat16(*bl).value;
+    auto [Yl, errl] = mp->ForwardFloat16(*X, *W, bl.get());
+    CHECK_NOERR(errl);
+    if (!Yl) continue;
+    CHECK_NOERR(Yl->RetrieveCPU());
+    bool same = true;
+    for (size_t i = 0; i < Yl->Data.size(); ++i) same = same && Yl->Data[i] == Y0->Data[i] + blh->Data[i % (size_t)L];
+    CHECK(same);
+  }
+  auto empty = NewTensor({0}, std::vector<float>()).value;
+  if (empty) CHECK_ERR_HAS(mp->ForwardFloat16(*X, *W, empty.get()).err, "bias is empty");
 }
 
 void TestFloat16Chaining() {
