@@ -526,6 +526,10 @@ def run_ceiling(seconds=3.0):
         res[k]["frac_of_peak"] = round(res[k]["tflops"] / PEAK_F16_TFLOPS, 4)
     log(f"mfma ceiling: {res['gemm_data']['tflops']:.0f} TFLOP/s on the headline's data "
         f"({res['gemm_data']['frac_of_peak']:.3f} of peak), {res['zero_data']['tflops']:.0f} on zeros")
+    big = res.get("mfma_32x32x16")
+    if big:
+        log(f"mfma ceiling, {big['instruction']}: {big['gemm_data']['tflops']:.0f} TFLOP/s on the headline's data, "
+            f"{big['zero_data']['tflops']:.0f} on zeros")
     return res
 
 
