@@ -27,13 +27,20 @@ __device__ __forceinline__ float apply_act(int act, float x, float a) {
     case 5: return x > 0.0f ? x : a * (ex(fmaxf(-88.0f, x)) - 1.0f);
     case 6: { float c = fmaxf(-88.0f, fminf(88.0f, x)); return c * inv(1.0f + ex(-c)); }
     case 7: {
-      float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-      inner = fmaxf(-88.0f, fminf(88.0f, inner));
-      if (!FAST) return 0.5f * x * (1.0f + tanhf(inner));
-      // 0.5 (1 + tanh(u)) = 1 / (1 + e^(-2u)): one exp and one reciprocal, no
-      // cancellation near u = 0, and the clamped limits are exact (e^(-2u) underflows
-      // to 0 at u = 88, giving x; it overflows to inf at u = -88, giving x * 0).
-      return x * inv(1.0f + __expf(-2.0f * inner));
+      if (!FAST) {
+        float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+        inner = fmaxf(-88.0f, fminf(88.0f, inner));
+        return 0.5f * x * (1.0f + tanhf(inner));
+      }
+      // 0.5 (1 + tanh(u)) = 1 / (1 + e^(-2u)), u = sqrt(2/pi) (x + 0.044715 x^3): one
+      // base-2 exponential and one reciprocal, no cancellation near u = 0. The constants
+      // are folded, e^(-2u) = 2^(x (k0 + k1 x^2)) with k0 = -2 sqrt(2/pi) log2(e) and
+      // k1 = 0.044715 k0: 5 VALU and 2 transcendental instructions per element. The clamp
+      // of u to [-88, 88] needs no instruction here: 2^t saturates as e^(-2u) does at
+      // those bounds (to 0 for t < -126, giving x; to inf for t > 128, giving x * 0).
+      constexpr float k0 = -2.302208198f, k1 = -0.1029432309f;
+      const float t = x * __builtin_fmaf(k1, x * x, k0);
+      return x * inv(1.0f + __builtin_amdgcn_exp2f(t));
     }
     default: return x;
   }
