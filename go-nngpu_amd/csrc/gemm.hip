@@ -1153,9 +1153,18 @@ inline double f16_rounds1(long t, double r, double fl = 0.75) {
   const long u = t % 256;
   return (double)(t / 256) * r + (u ? r * fmax(fl, u / 256.0) : 0.0);
 }
+// A last round of two-per-CU tiles with more than 256 tiles (some CUs run two, some one)
+// costs 0.325 + 0.69 u / 512 of a full one, and never less than a full round of one per CU:
+// 512 x 12288 x 4096 NT with 384 tiles of 128 x 128 took 0.84 of the 512-tile round
+// (57.2 against 67.9 us), 512 x 14336 x 4096 with 448 tiles 0.93 (63.0 us). With the 0.75
+// floor alone the model took those 384 tiles (57.2 us) over one full round of 256 tiles of
+// 128 x 192 (51.5 us); same at 1024 x 6144 and 2048 x 3072.
 inline double f16_rounds2(long t, double r2, double r1, double fl = 0.75) {
   const long u = t % 512;
-  return (double)(t / 512) * r2 + (u == 0 ? 0.0 : u <= 256 ? r1 * fmax(fl, u / 256.0) : r2 * fmax(fl, u / 512.0));
+  if (u == 0) return (double)(t / 512) * r2;
+  if (u <= 256) return (double)(t / 512) * r2 + r1 * fmax(fl, u / 256.0);
+  const double f = fmax(fmax(fl, u / 512.0), fmax(0.325 + 0.69 * (u / 512.0), r1 / r2));
+  return (double)(t / 512) * r2 + r2 * f;
 }
 
 template <bool TB>
