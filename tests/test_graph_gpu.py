@@ -1,6 +1,6 @@
 """HIP graph capture of the device-pointer API: the GEMM (fp16 ring and register-staged
-kernels, fp32), CSR SpMM and SpMV launch no memset and allocate nothing, so a caller can
-capture them once and replay the graph. Each replay is compared with the eager result
+kernels, fp32), CSR SpMM, SpMV and the grouped-layout SpMV of a plan built before the capture
+launch no memset and allocate nothing, so a caller can capture them once and replay the graph. Each replay is compared with the eager result
 for inputs changed between replays (with the program's own eager work and
 synchronisations in between), bit for bit."""
 import sys
@@ -40,6 +40,9 @@ def test_graph_replays_match_eager(dev):
     y32 = torch.empty(700, 500, device=dev)
     S = torch.empty(4000, 64, device=dev)
     yv = torch.empty(4000, device=dev)
+    yp = torch.empty(4000, device=dev)
+    torch.cuda.synchronize()
+    plan = G.SpmvPlan(4000, 3000, val.size, d_rp, d_col)  # reads the row pointers back: not capturable
 
     def work():
         G.gemm(a16, b16, c16)
@@ -47,6 +50,7 @@ def test_graph_replays_match_eager(dev):
         G.gemm(x32, w32, y32, bias=bias, act=G.ACT_GELU)
         G.spmm_csr(4000, 64, 3000, val.size, d_rp, d_col, d_val, D, S)
         G.spmv_csr(4000, 3000, val.size, d_rp, d_col, d_val, xv, yv)
+        plan.run(d_val, xv, yp)
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -60,7 +64,7 @@ def test_graph_replays_match_eager(dev):
     torch.cuda.synchronize()
 
     assert val.size >= 1 << 16
-    outs = (c16, c2, y32, S, yv)
+    outs = (c16, c2, y32, S, yv, yp)
     for rep in range(3):
         # new inputs, eager work and a synchronisation between replays
         with torch.no_grad():
@@ -69,16 +73,22 @@ def test_graph_replays_match_eager(dev):
             w32.mul_(0.5).add_(0.1)
             D.copy_(torch.randn_like(D))
             xv.mul_(-1.5)
+            d_val.mul_(0.75)
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
         got = [t.clone() for t in outs]
         work()  # eager, on the current stream
         torch.cuda.synchronize()
-        for name, gt, ref in zip(("gemm f16", "gemm f16 row split", "gemm f32", "spmm", "spmv"), got, outs):
+        for name, gt, ref in zip(("gemm f16", "gemm f16 row split", "gemm f32", "spmm", "spmv", "spmv plan"), got,
+                                 outs):
             same = torch.equal(gt, ref)
             _say("replay", rep, name, "bit-identical" if same else "DIFFERS")
             assert same, (rep, name)
+        # the plan's replayed result is also the reference loop's, bit for bit
+        np.testing.assert_array_equal(got[5].cpu().numpy(),
+                                      O.spmv_f32(rp, col, d_val.cpu().numpy(), xv.cpu().numpy(), use_fma=True))
+    plan.release()
 
 
 def _ptrs(*bufs):
