@@ -22,21 +22,55 @@ struct Scratch {  // device scratch released on scope exit (after the stream is 
   ~Scratch() { gn::dev_free(p); }
 };
 
-// Waits for the work enqueued on s, as the reference's waitUntilCompleted does. The stream is
-// polled for up to 5 ms before the blocking wait, whose wake-up is slower: the C5 SpMM through
-// perform_sparse_dense_matmul took 0.400 ms per synchronous call with the blocking wait alone
-// and 0.385 ms with the polling, against 0.366 ms of kernels. Longer work pays the blocking
-// wait's latency once, against milliseconds of kernel time.
-int sync(hipStream_t s, CError *err, int code) {
-  const auto t0 = std::chrono::steady_clock::now();
-  hipError_t e;
-  while ((e = hipStreamQuery(s)) == hipErrorNotReady) {
-    if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(5)) {
-      e = hipStreamSynchronize(s);
-      break;
+// Idle completion events of sync(), created on demand and kept for the life of the process
+// (one per thread that has waited at the same time).
+std::mutex g_sync_mu;
+std::vector<hipEvent_t> g_sync_events;
+
+hipError_t take_sync_event(hipEvent_t *ev) {
+  {
+    std::lock_guard<std::mutex> lk(g_sync_mu);
+    if (!g_sync_events.empty()) {
+      *ev = g_sync_events.back();
+      g_sync_events.pop_back();
+      return hipSuccess;
     }
-    std::this_thread::yield();  // threads waiting side by side leave the CPU (and the stream) to each other
   }
+  return hipEventCreateWithFlags(ev, hipEventDisableTiming);
+}
+
+void give_sync_event(hipEvent_t ev) {
+  std::lock_guard<std::mutex> lk(g_sync_mu);
+  g_sync_events.push_back(ev);
+}
+
+// Waits for the work enqueued on s, as the reference's waitUntilCompleted does. A timing-free
+// event recorded behind that work is polled for up to 5 ms, then waited on: the blocking wait's
+// wake-up is slower (the C5 SpMM through perform_sparse_dense_matmul took 0.400 ms per
+// synchronous call with it alone and 0.385 ms with the polling, against 0.366 ms of kernels), and
+// polling the stream itself (hipStreamQuery) is slower still for short work: a 1-element kernel's
+// synchronous round trip took 26.6 us that way against 12.7 us through the event, the C5 SpMV
+// 27.7 against 22.2 us. A capturing stream has no completion to wait for and is an error, as
+// hipStreamQuery reports it.
+int sync(hipStream_t s, CError *err, int code) {
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(s, &cap);
+  if (e == hipSuccess && cap != hipStreamCaptureStatusNone) e = hipErrorStreamCaptureUnsupported;
+  hipEvent_t ev = nullptr;
+  if (e == hipSuccess) e = take_sync_event(&ev);
+  if (e == hipSuccess) e = hipEventRecord(ev, s);
+  if (e == hipSuccess) {
+    const auto t0 = std::chrono::steady_clock::now();
+    while ((e = hipEventQuery(ev)) == hipErrorNotReady) {
+      if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(5)) {
+        e = hipEventSynchronize(ev);
+        break;
+      }
+      std::this_thread::yield();  // threads waiting side by side leave the CPU to each other
+    }
+  }
+  if (ev) give_sync_event(ev);
+  (void)hipGetLastError();  // the polls' hipErrorNotReady must not reach a later launch check
   if (e != hipSuccess) return gn::hip_error(err, code, "device execution", e);
   return 0;
 }
