@@ -85,18 +85,18 @@ constexpr int kActRuntime = -1000;  // ActCode value: apply p.act, decided per e
 // the next is staged. alpha, beta*C, bias and the activation are applied on the way;
 // scalar stores at ragged edges or when ldc / C do not allow aligned 16-byte stores.
 // The pass loop is unrolled so every accumulator index is static (a runtime index would
-// move the accumulators to scratch memory).
-template <int BM, int BN, int WM, int WN>
-__device__ __forceinline__ void store_tile_rows(const GemmParams &p, long m0, long n0, long z, float *stg,
-                                                const float4_t (&acc)[BM / WM / 16][BN / WN / 16]) {
-  constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 16, FN = WTN / 16;
+// move the accumulators to scratch memory). stage(f) writes the wave's rows of pass f (wave
+// tile rows 16 f .. 16 f + 15) into stg at rows wm * 16 + 0..15, pitch BN + 4, columns
+// wn * (BN / WN) + 0..BN / WN - 1.
+template <int BM, int BN, int WM, int WN, typename Stage>
+__device__ __forceinline__ void store_tile_passes(const GemmParams &p, long m0, long n0, long z, float *stg,
+                                                  Stage &&stage) {
+  constexpr int WTM = BM / WM, FM = WTM / 16;
   constexpr int LP = BN + 4, CPR = BN / 4, NTH = WM * WN * 64;
   constexpr int ROWS = WM * 16;       // tile rows staged per pass
   constexpr int RPS = NTH / CPR;      // rows one sweep of the workgroup's threads covers
   constexpr int SWEEPS = (ROWS + RPS - 1) / RPS;
   static_assert(BN % 4 == 0 && CPR <= NTH, "row vectors");
-  const int wave = threadIdx.x >> 6, wm = wave / WN, wn = wave % WN, lane = threadIdx.x & 63;
-  const int c = lane & 15, g = lane >> 4;
   const int c4 = threadIdx.x % CPR, r0 = threadIdx.x / CPR;  // threads with r0 >= RPS only stage
   const long col = n0 + 4 * c4;
   float *C = p.C + z * p.strideC;
@@ -107,10 +107,7 @@ __device__ __forceinline__ void store_tile_rows(const GemmParams &p, long m0, lo
 #pragma unroll
   for (int f = 0; f < FM; ++f) {
     lds_barrier();  // the previous pass (or the main loop) is done with stg
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) stg[(wm * 16 + 4 * g + r) * LP + wn * WTN + 16 * j + c] = acc[f][j][r];
+    stage(f);
     lds_barrier();
     // The common activations get their own copy of the row sweep with the code fixed at
     // compile time: the generic one inlines every case of apply_act for every element,
@@ -154,6 +151,22 @@ __device__ __forceinline__ void store_tile_rows(const GemmParams &p, long m0, lo
       default: sweep(ActCode<kActRuntime>{}); break;
     }
   }
+}
+
+// store_tile_passes for 16 x 16 MFMA accumulators: lane (c, g) of block (f, j) holds rows
+// 4 g + 0..3 of column c.
+template <int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void store_tile_rows(const GemmParams &p, long m0, long n0, long z, float *stg,
+                                                const float4_t (&acc)[BM / WM / 16][BN / WN / 16]) {
+  constexpr int WTN = BN / WN, FN = WTN / 16, LP = BN + 4;
+  const int wave = threadIdx.x >> 6, wm = wave / WN, wn = wave % WN, lane = threadIdx.x & 63;
+  const int c = lane & 15, g = lane >> 4;
+  store_tile_passes<BM, BN, WM, WN>(p, m0, n0, z, stg, [&](int f) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) stg[(wm * 16 + 4 * g + r) * LP + wn * WTN + 16 * j + c] = acc[f][j][r];
+  });
 }
 
 // Grouped + XCD-aware mapping of the linear workgroup id to a (tile_m, tile_n) pair.
@@ -576,79 +589,61 @@ __device__ __forceinline__ void sched_interleave() {
   if constexpr (NR > NP) __builtin_amdgcn_sched_group_barrier(0x100, NR - NP, 0);
 }
 
-// Main loop of the ring kernel for one output tile (rows m0.., columns n0.., batch z),
-// nk K-tiles: adds the products into acc. K-tiles go in pairs: slot pp & 1 holds tiles
-// 2pp and 2pp+1 of A, then of B (a K-contiguous operand holds both tiles in each of its
-// chunks; an MN-contiguous one has a region per tile). Per pair, the even step
-// multiplies tile 2pp while reading tile 2pp+1's fragments from the same, already
-// visible slot; the odd step waits for pair pp+1, passes the pair's one barrier,
-// refills the slot just consumed with pair pp+2 and reads tile 2pp+2's fragments.
-// Measured against a 4-stage ring of single K-tiles with one barrier per tile: NN
-// 1139 -> 1170, TN 1139 -> 1179, TT 1145 -> 1156, NT equal (TFLOP/s, 8192^3). Leaves
-// every DMA complete and every wave past a barrier, so the caller may reuse smem.
-template <int BM, int BN, int WM, int WN, bool TA, bool TB, int NS>
-__device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long n0, long z, int nk, char *smem,
-                                              float4_t (&acc)[BM / WM / 16][BN / WN / 16]) {
-  constexpr int BK = 32;
-  constexpr int NW = WM * WN;
-  constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int FM = WTM / 16, FN = WTN / 16;
-  constexpr int OPA = BM * BK * 2, OPB = BN * BK * 2;  // bytes of one K-tile of A / B
-  constexpr int SLOT = 2 * (OPA + OPB);                // A tiles 2pp, 2pp+1, then B tiles
-  constexpr int CA = 2 * OPA / 1024, CB = 2 * OPB / 1024;
-  constexpr int IPA = CA / NW, IPB = CB / NW;  // 1 KiB DMA chunks per wave per pair
-  constexpr int LPW = IPA + IPB;
-  constexpr int RBA = BM * 2, RBB = BN * 2;  // LDS row bytes of MN-contiguous tiles (one k row)
+// The copy side of the fp16 ring for one output tile: each wave's share of a K-tile pair's
+// 1 KiB DMA chunks into a ring slot. For a K-contiguous operand chunk c of a pair holds rows
+// 8c..8c+7 of both K-tiles, octets as kc8_slot lays out. For an MN-contiguous one it belongs
+// to tile h = c / (nchunks / 2) and holds k rows cl * (1024 / row bytes).. (cl = c %
+// (nchunks / 2)) with 32-byte blocks XOR-swizzled by hsw(k). Each lane keeps its offset from
+// the pair's start and the k (0..63) it covers; lanes whose rows or columns lie past M (or N)
+// get the out-of-range offset.
+template <int BM, int BN, int WM, int WN, bool TA, bool TB>
+struct F16RingCopies {
+  static constexpr int BK = 32, NW = WM * WN;
+  static constexpr int OPA = BM * BK * 2, OPB = BN * BK * 2;  // bytes of one K-tile of A / B
+  static constexpr int SLOT = 2 * (OPA + OPB);                // A tiles 2pp, 2pp+1, then B tiles
+  static constexpr int CA = 2 * OPA / 1024, CB = 2 * OPB / 1024;
+  static constexpr int IPA = CA / NW, IPB = CB / NW;  // 1 KiB DMA chunks per wave per pair
+  static constexpr int LPW = IPA + IPB;
+  static constexpr int RBA = BM * 2, RBB = BN * 2;  // LDS row bytes of MN-contiguous tiles (one k row)
   static_assert(CA % NW == 0 && CB % NW == 0 && IPA >= 1 && IPB >= 1, "DMA split");
-  static_assert(NS >= 2 && (NS - 1) * LPW < 64, "ring slots within the vmcnt range");
-  // Splitting each pair's DMA into two bursts (A at the barrier, B halfway through the
-  // MFMAs) measured 2-4% faster at 256 x 256 with 8 waves (8192^3: NN 884 -> 851 us, NT
-  // 872 -> 851 us) and 10% slower for the 4-wave 128 x 96 tiles of the C4 shape; four
-  // bursts (A and B halves at quarter points) measured within 1% of two.
-  constexpr int kDmaParts = NW >= 8 ? 2 : 1;
-  static_assert(kDmaParts == 1 || FM % 4 == 0, "DMA burst split rows");
-  static_assert((!TA || BM >= 128) && (TB || BN >= 128), "MN-contiguous rows need 8 XOR blocks of 32 B");
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int wm = wave / WN, wn = wave % WN;
-
-  // Per-lane DMA plan. For a K-contiguous operand chunk c of a pair holds rows
-  // 8c..8c+7 of both K-tiles, octets as kc8_slot lays out. For an MN-contiguous one it
-  // belongs to tile h = c / (nchunks / 2) and holds k rows cl * (1024 / row bytes)..
-  // (cl = c % (nchunks / 2)) with 32-byte blocks XOR-swizzled by hsw(k). Each lane
-  // keeps its offset from the pair's start and the k (0..63) it covers; lanes whose
-  // rows or columns lie past M (or N) get the out-of-range offset.
   BufRsrc ra, rb;
   unsigned voa[IPA], vob[IPB];
   int kla[IPA], klb[IPB];
-  auto plan = [&](bool kcontig, int c, int nchunks, int rb_bytes, long ld, long lim, unsigned &vo, int &kl) {
-    const ring::Copy cp = ring::plan_f16(kcontig, c, nchunks, rb_bytes, ld, lim, lane);
-    vo = cp.vo;
-    kl = cp.kl;
-  };
-  {
+  long K, a_step, b_step;
+  unsigned sbase;
+  int wave;
+
+  __device__ __forceinline__ F16RingCopies(const GemmParams &p, long m0, long n0, long z, const char *smem, int w,
+                                           int lane)
+      : K(p.K), wave(w) {
     const _Float16 *A = static_cast<const _Float16 *>(p.A) + z * p.strideA;
     const _Float16 *B = static_cast<const _Float16 *>(p.B) + z * p.strideB;
     ra = make_rsrc(A + ring::base_elems(!TA, m0, p.lda));
     rb = make_rsrc(B + ring::base_elems(TB, n0, p.ldb));
+#pragma unroll
+    for (int i = 0; i < IPA; ++i) {
+      const ring::Copy cp = ring::plan_f16(!TA, wave * IPA + i, CA, RBA, p.lda, p.M - m0, lane);
+      voa[i] = cp.vo;
+      kla[i] = cp.kl;
+    }
+#pragma unroll
+    for (int i = 0; i < IPB; ++i) {
+      const ring::Copy cp = ring::plan_f16(TB, wave * IPB + i, CB, RBB, p.ldb, p.N - n0, lane);
+      vob[i] = cp.vo;
+      klb[i] = cp.kl;
+    }
+    a_step = ring::pair_step_bytes(!TA, BK, p.lda, 2);
+    b_step = ring::pair_step_bytes(TB, BK, p.ldb, 2);
+    sbase = lds_offset(smem);
   }
-#pragma unroll
-  for (int i = 0; i < IPA; ++i) plan(!TA, wave * IPA + i, CA, RBA, p.lda, p.M - m0, voa[i], kla[i]);
-#pragma unroll
-  for (int i = 0; i < IPB; ++i) plan(TB, wave * IPB + i, CB, RBB, p.ldb, p.N - n0, vob[i], klb[i]);
-  const long a_step = ring::pair_step_bytes(!TA, BK, p.lda, 2);
-  const long b_step = ring::pair_step_bytes(TB, BK, p.ldb, 2);
-  const unsigned sbase = lds_offset(smem);
-  const int np = max(1, (nk + 1) >> 1);  // pairs the loop runs; tiles past nk are zeros
 
-  // DMA of pair pp (K-tiles 2pp, 2pp+1) into slot `slot`, in parts: part q of NP copies
-  // the q-th share of the wave's A chunks (q < NP / 2) or of its B chunks; the last part
+  // DMA of pair pp (K-tiles 2pp, 2pp+1) into slot `slot`, in parts: part q of NPRT copies
+  // the q-th share of the wave's A chunks (q < NPRT / 2) or of its B chunks; the last part
   // also advances both descriptors to the next pair.
-  auto issue = [&](int pp, int slot, int q, int NPRT) {
+  __device__ __forceinline__ void issue(int pp, int slot, int q, int NPRT) {
     const unsigned st = sbase + (unsigned)(slot * SLOT);
-    const int krem = ring::f16_krem(p.K, pp);
+    const int krem = ring::f16_krem(K, pp);
     const int half = NPRT / 2;
-    const bool last_call = q == NPRT - 1;
     if (q < half) {
 #pragma unroll
       for (int i = 0; i < IPA; ++i)
@@ -662,11 +657,46 @@ __device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long
           dma16(rb, ring::f16_offset({vob[i], klb[i]}, krem),
                 __builtin_amdgcn_readfirstlane(st + 2 * OPA + (wave * IPB + i) * 1024));
     }
-    if (last_call) {
+    if (q == NPRT - 1) {
       rsrc_advance(ra, a_step);
       rsrc_advance(rb, b_step);
     }
-  };
+  }
+};
+
+// Main loop of the ring kernel for one output tile (rows m0.., columns n0.., batch z),
+// nk K-tiles: adds the products into acc. K-tiles go in pairs: slot pp & 1 holds tiles
+// 2pp and 2pp+1 of A, then of B (a K-contiguous operand holds both tiles in each of its
+// chunks; an MN-contiguous one has a region per tile). Per pair, the even step
+// multiplies tile 2pp while reading tile 2pp+1's fragments from the same, already
+// visible slot; the odd step waits for pair pp+1, passes the pair's one barrier,
+// refills the slot just consumed with pair pp+2 and reads tile 2pp+2's fragments.
+// Measured against a 4-stage ring of single K-tiles with one barrier per tile: NN
+// 1139 -> 1170, TN 1139 -> 1179, TT 1145 -> 1156, NT equal (TFLOP/s, 8192^3). Leaves
+// every DMA complete and every wave past a barrier, so the caller may reuse smem.
+template <int BM, int BN, int WM, int WN, bool TA, bool TB, int NS>
+__device__ __forceinline__ void ring_mainloop(const GemmParams &p, long m0, long n0, long z, int nk, char *smem,
+                                              float4_t (&acc)[BM / WM / 16][BN / WN / 16]) {
+  constexpr int NW = WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 16, FN = WTN / 16;
+  using Copies = F16RingCopies<BM, BN, WM, WN, TA, TB>;
+  constexpr int OPA = Copies::OPA, OPB = Copies::OPB, SLOT = Copies::SLOT, LPW = Copies::LPW;
+  constexpr int RBA = Copies::RBA, RBB = Copies::RBB;
+  static_assert(NS >= 2 && (NS - 1) * LPW < 64, "ring slots within the vmcnt range");
+  // Splitting each pair's DMA into two bursts (A at the barrier, B halfway through the
+  // MFMAs) measured 2-4% faster at 256 x 256 with 8 waves (8192^3: NN 884 -> 851 us, NT
+  // 872 -> 851 us) and 10% slower for the 4-wave 128 x 96 tiles of the C4 shape; four
+  // bursts (A and B halves at quarter points) measured within 1% of two.
+  constexpr int kDmaParts = NW >= 8 ? 2 : 1;
+  static_assert(kDmaParts == 1 || FM % 4 == 0, "DMA burst split rows");
+  static_assert((!TA || BM >= 128) && (TB || BN >= 128), "MN-contiguous rows need 8 XOR blocks of 32 B");
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wm = wave / WN, wn = wave % WN;
+  Copies dma(p, m0, n0, z, smem, wave, lane);
+  const int np = max(1, (nk + 1) >> 1);  // pairs the loop runs; tiles past nk are zeros
+  auto issue = [&](int pp, int slot, int q, int NPRT) { dma.issue(pp, slot, q, NPRT); };
 
   auto frag_t = [&](const char *base, int col0, int rowb) -> half8_t {
     const int s = lane & 15, g = lane >> 4;
@@ -830,6 +860,156 @@ gemm_f16_ring_kernel(GemmParams p) {
   ring_mainloop<BM, BN, WM, WN, TA, TB, NS>(p, m0, n0, z, (int)((p.K + 31) / 32), smem, acc);
   static_assert(WM * 16 * (BN + 4) * 4 <= RING, "epilogue staging exceeds the ring");
   store_tile_rows<BM, BN, WM, WN>(p, m0, n0, z, reinterpret_cast<float *>(smem), acc);
+}
+
+// ------------------------------------------------------------------ 32 x 32 x 16 variant
+// The NN 256 x 256 ring kernel on v_mfma_f32_32x32x16_f16, selected with
+// GONNGPU_F16_MFMA32=1 (for measurement; the dispatch otherwise keeps 16 x 16 x 32). Same ring,
+// copies, barriers and DMA bursts; each wave's 128 x 64 tile is 4 x 2 blocks of 32 x 32, and
+// per K-tile it runs 16 MFMAs of 32 cycles where the product kernel runs 32 of 16, reading the
+// same 16 fragments, and gives the product kernel's bits (the matrix unit accumulates K in the
+// same order for both shapes). Measured at 8192^3 on one box, alternating libraries:
+// 0.878-0.908 ms against 0.790-0.817 ms, the same MFMA-busy cycles and no LDS bank conflicts,
+// but at the 1400 W board limit the clock settles at 1.60-1.72 GHz against 1.76-1.86 GHz. Each
+// 32 x 32 x 16 instruction reads and writes 16 accumulator registers per lane in 32 cycles, the
+// 16 x 16 x 32 one 4 in 16: twice the accumulator register traffic per flop.
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+template <int BM, int BN, int WM, int WN, int NS>
+__device__ __forceinline__ void ring_mainloop_mf32(const GemmParams &p, long m0, long n0, long z, int nk, char *smem,
+                                                   float16_t (&acc)[BM / WM / 32][BN / WN / 32]) {
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 32, FN = WTN / 32;
+  constexpr int NU = 2 * FM;  // MFMA units per K-tile: (k-step, 32-row block), FN instructions each
+  using Copies = F16RingCopies<BM, BN, WM, WN, false, false>;
+  constexpr int OPA = Copies::OPA, OPB = Copies::OPB, SLOT = Copies::SLOT, LPW = Copies::LPW;
+  constexpr int RBB = Copies::RBB;
+  static_assert(NS >= 2 && (NS - 1) * LPW < 64, "ring slots within the vmcnt range");
+  static_assert(WM * WN >= 8 && BN >= 128 && NU >= 8, "two DMA bursts, 8 XOR blocks per B row");
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wm = wave / WN, wn = wave % WN;
+  Copies dma(p, m0, n0, z, smem, wave, lane);
+  const int np = max(1, (nk + 1) >> 1);
+  // B (MN-contiguous): 16-lane group G reads k rows 16 st + 8 (G >> 1) + 0..3 (then + 4) of
+  // columns col0 + 16 (G & 1) + 0..15, so lane l holds column col0 + (l & 31) with k
+  // 16 st + 8 (l >> 5) + 0..7. With hsw(k), the 32 lanes of each half-wave read 8 distinct
+  // 32-byte blocks (as the 16 x 16 fragment reads do).
+  auto frag_t = [&](const char *base, int col0, int stp) -> half8_t {
+    const int s = lane & 15, G = lane >> 4;
+    const int k = 16 * stp + 8 * (G >> 1) + (s >> 2);
+    const int col = col0 + 16 * (G & 1) + 4 * (s & 3);
+    const char *p0 = base + k * RBB + (((col >> 4) ^ hsw(k)) << 5) + ((col & 15) << 1);
+    const trh4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((LDS_AS trh4_t *)(p0));
+    const trh4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((LDS_AS trh4_t *)(p0 + 4 * RBB));
+    const half4_t l4 = __builtin_bit_cast(half4_t, lo);
+    const half4_t h4 = __builtin_bit_cast(half4_t, hi);
+    return __builtin_shufflevector(l4, h4, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+  // A (K-contiguous): lane l reads row row0 + (l & 31), octet 4 h + 2 st + (l >> 5) of the pair
+  auto frag_k = [&](const char *base, int row0, int h, int stp) -> half8_t {
+    const int row = row0 + (lane & 31);
+    return *reinterpret_cast<const half8_t *>(base + (row >> 3) * 1024 +
+                                              16 * kc8_slot(row, 4 * h + 2 * stp + (lane >> 5)));
+  };
+  half8_t fa[2][2][FM], fb[2][2][FN];  // [register set][k-step][block]
+  auto read_part = [&](int slot, int h, int set, int q, int NPRT) {
+    const char *sa = smem + slot * SLOT;
+    const char *sb = smem + slot * SLOT + 2 * OPA + h * OPB;
+#pragma unroll
+    for (int a = 0; a < 2 * FM; ++a)
+      if (a * NPRT / (2 * FM) == q) fa[set][a / FM][a % FM] = frag_k(sa, wm * WTM + (a % FM) * 32, h, a / FM);
+#pragma unroll
+    for (int b = 0; b < 2 * FN; ++b)
+      if (b * NPRT / (2 * FN) == q) fb[set][b / FN][b % FN] = frag_t(sb, wn * WTN + (b % FN) * 32, b / FN);
+  };
+  constexpr int NDS = 2 * FM + 4 * FN;  // LDS read instructions per K-tile
+  constexpr int NMT = NU * FN;          // MFMAs per K-tile
+  // units in k-step-major order, so an accumulator's two updates per K-tile are FM units apart
+  auto mfma_units = [&](int set, int u0, int u1) {
+#pragma unroll
+    for (int u = u0; u < u1; ++u)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[u % FM][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[set][u / FM][u % FM], fb[set][u / FM][j],
+                                                                acc[u % FM][j], 0, 0, 0);
+  };
+#pragma unroll
+  for (int q = 0; q < NS; ++q) {
+    dma.issue(q, q, 0, 2);
+    dma.issue(q, q, 1, 2);
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 1) * LPW));
+  __syncthreads();
+  read_part(0, 0, 0, 0, 1);
+  int cur = 0, nxt = 1;
+  for (int pp = 0; pp < np; ++pp) {
+    // even step: tile 2pp, reading tile 2pp+1's fragments
+    __builtin_amdgcn_sched_barrier(0);
+    read_part(cur, 1, 1, 0, 1);
+    mfma_units(0, 0, NU);
+    sched_interleave<NMT, NDS>();
+    // odd step: wait for pair pp+1, refill this slot with pair pp+NS in two bursts (A after
+    // the first unit, B after 3/4 of them), reading tile 2pp+2's fragments in between
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * LPW));
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    constexpr int R0 = 3 * NU / 4;
+    constexpr int NRH = FM + 2 * FN;  // LDS reads per part
+    mfma_units(1, 0, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    dma.issue(pp + NS, cur, 0, 2);
+    read_part(nxt, 0, 0, 0, 2);
+    mfma_units(1, 1, R0);
+    sched_interleave<(R0 - 1) * FN, NRH>();
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_units(1, R0, R0 + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    dma.issue(pp + NS, cur, 1, 2);
+    read_part(nxt, 0, 0, 1, 2);
+    mfma_units(1, R0 + 1, NU);
+    sched_interleave<(NU - R0 - 1) * FN, NRH>();
+    cur = nxt;
+    nxt = nxt + 1 == NS ? 0 : nxt + 1;
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  __syncthreads();
+}
+
+template <int BM, int BN, int WM, int WN, int WPE, int NS>
+__global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+gemm_f16_ring_mf32_kernel(GemmParams p) {
+  constexpr int WTN = BN / WN, FM = BM / WM / 32, FN = WTN / 32, LP = BN + 4;
+  constexpr int RING = NS * 2 * (BM + BN) * 32 * 2;
+  __shared__ __attribute__((aligned(1024))) char smem[RING];
+  static_assert(WM * 16 * (BN + 4) * 4 <= RING, "epilogue staging exceeds the ring");
+  int tm, tn;
+  tile_coords(p, tm, tn);
+  float16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+  const long m0 = (long)tm * BM, n0 = (long)tn * BN, z = blockIdx.z;
+  ring_mainloop_mf32<BM, BN, WM, WN, NS>(p, m0, n0, z, (int)((p.K + 31) / 32), smem, acc);
+  // lane l of a 32 x 32 block holds column l & 31, rows 8 (e >> 2) + 4 (l >> 5) + (e & 3);
+  // pass f stages the block's rows 16 (f & 1) .. + 15, i.e. its elements e = 8 (f & 1) .. + 7
+  const int wave = threadIdx.x >> 6, wm = wave / WN, wn = wave % WN, lane = threadIdx.x & 63;
+  float *stg = reinterpret_cast<float *>(smem);
+  store_tile_passes<BM, BN, WM, WN>(p, m0, n0, z, stg, [&](int f) {
+    const int b = f >> 1, hh = f & 1;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int ii = 0; ii < 8; ++ii) {
+        const int e = 8 * hh + ii;
+        const int rr = 8 * ((e >> 2) - 2 * hh) + 4 * (lane >> 5) + (e & 3);
+        stg[(wm * 16 + rr) * LP + wn * WTN + 32 * j + (lane & 31)] = acc[b][j][e];
+      }
+  });
 }
 
 // ------------------------------------------------------------------ fp32 DMA-ring kernel
@@ -1196,6 +1376,17 @@ template <bool TA, bool TB>
 hipError_t launch_f16_tile(const GemmParams &p, long batch, hipStream_t s, F16Tile t) {
   switch (t) {
     case F16Tile::k256:
+      if constexpr (!TA && !TB) {
+        const char *mf = getenv("GONNGPU_F16_MFMA32");  // the measured 32 x 32 x 16 variant
+        if (mf && mf[0] == '1') {
+          GemmParams q = p;
+          q.tiles_m = (int)((q.M + 255) / 256);
+          q.tiles_n = (int)((q.N + 255) / 256);
+          dim3 grid((unsigned)(q.tiles_m * q.tiles_n), 1, (unsigned)batch);
+          hipLaunchKernelGGL((gemm_f16_ring_mf32_kernel<256, 256, 2, 4, 2, 2>), grid, dim3(512), 0, s, q);
+          return hipGetLastError();
+        }
+      }
       return launch_f16_ring<256, 256, 2, 4, TA, TB>(p, batch, s);
     case F16Tile::k128w8:
       return launch_f16_ring<128, 128, 2, 4, TA, TB>(p, batch, s);

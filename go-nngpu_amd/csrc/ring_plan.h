@@ -25,8 +25,11 @@ constexpr unsigned kOutOfRange = 0x80000000u;  // an offset beyond it: the copy 
 // hardware writes to slot L: octet o of row r sits in slot kc8_slot(r, o).
 constexpr int kc8_slot(int r, int o) { return 8 * (r & 7) + (o ^ ((r >> 1) & 7)); }
 constexpr int kc8_octet(int r, int j) { return j ^ ((r >> 1) & 7); }
-// 32-byte block XOR of k row k of an fp16 MN-contiguous tile.
-constexpr int hsw(int k) { return (k & 3) | ((k >> 1) & 4); }
+// 32-byte block XOR of k row k of an fp16 MN-contiguous tile: 2 (k & 3) + ((k >> 3) & 1). The
+// rows a half-wave's ds_read_b64_tr_b16 touches get 8 distinct blocks of one 256-byte bank
+// row: k0 + 0..3 and k0 + 8..11 at one column block (16 x 16 x 32 fragments), and k0 + 0..3 at
+// two adjacent column blocks (32 x 32 x 16 fragments).
+constexpr int hsw(int k) { return ((k & 3) << 1) | ((k >> 3) & 1); }
 // 16-byte block XOR of k row k of an fp32 MN-contiguous tile.
 constexpr int msw32(int k) { return ((k >> 2) & 1) << 2; }
 

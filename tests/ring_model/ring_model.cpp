@@ -38,8 +38,9 @@ struct Config {
 
 // gemm.hip: launch_f16_tile (256x256 2x4; 128x128 2x4 and 2x2; 128x192 2x4 with three
 // slots and 128x96 2x2, TB only) and launch_f32_ring_best (256x256 2x4 for NN, 4x2 for the
-// other layouts; 128x128 2x2, 2x4 or 4x2; 64x64 2x2). The test runner checks this table
-// against the launches in gemm.hip.
+// other layouts; 128x128 2x2, 2x4 or 4x2; 64x64 2x2). gemm_f16_ring_mf32_kernel (the 32x32x16 NN
+// variant) issues the same copies as the fp16 256x256 2x4 two-slot ring. The test runner checks
+// this table against the launches in gemm.hip.
 const Config kConfigs[] = {
     {true, 256, 256, 2, 4, 2, false}, {true, 128, 128, 2, 4, 2, false}, {true, 128, 128, 2, 2, 2, false},
     {true, 128, 192, 2, 4, 3, true},  {true, 128, 96, 2, 2, 2, true},   {false, 256, 256, 2, 4, 2, false},

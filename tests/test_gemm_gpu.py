@@ -817,6 +817,39 @@ def test_f16_ring_ragged_all_transposes(dev, tA, tB, M, N):
     assert np.isfinite(C).all()
 
 
+@pytest.mark.parametrize("M,N,K", [(4000, 4000, 1000), (4096, 4096, 4096)])
+def test_f16_mfma32_variant_nn(dev, monkeypatch, M, N, K):
+    """GONNGPU_F16_MFMA32=1 runs NN products on the 256x256 tiles through the 32x32x16 MFMA
+    kernel (kept for measurement). Ragged M, N and a K tail (4000 x 4000 x 1000, one round of
+    256 tiles) and a square case: sampled rows within 1e-5 of the float64 product of the
+    rounded inputs, whole-output row and column sums from a NaN-filled output, and the same
+    bits as the 16x16x32 kernel (the matrix unit accumulates K in the same order for both
+    instruction shapes)."""
+    import torch
+
+    rng = np.random.default_rng(53)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
+    base = _gemm_dev(dev, A, B, False, False, G.GN_F16)
+    monkeypatch.setenv("GONNGPU_F16_MFMA32", "1")
+    a16 = torch.empty((M, K), dtype=torch.float16, device=dev)
+    b16 = torch.empty((K, N), dtype=torch.float16, device=dev)
+    G.cast_f32_f16(torch.from_numpy(A).to(dev), a16)
+    G.cast_f32_f16(torch.from_numpy(B).to(dev), b16)
+    cd = _nan_like(dev, M, N)
+    G.gemm(a16, b16, cd)
+    torch.cuda.synchronize()
+    row_err, col_err = _sum_invariants(a16, b16, cd)
+    C = cd.cpu().numpy()
+    rows = np.concatenate([np.arange(0, 16), rng.choice(M, 24, replace=False), np.arange(M - 16, M)])
+    ref_r = O.gemm_f64_rows(O.round_f16(A[rows], False), O.round_f16(B, False), np.arange(rows.size))
+    err = O.rel_frob(C[rows], ref_r)
+    _say("mfma32 variant", M, N, K, err, row_err, col_err)
+    assert np.isfinite(C).all()
+    assert err <= 1e-5 and row_err <= 1e-5 and col_err <= 1e-5
+    np.testing.assert_array_equal(C, base)
+
+
 def test_f16_ring_transpose_variants_bit_identical(dev):
     rng = np.random.default_rng(37)
     A = rng.standard_normal((4096, 512)).astype(np.float32)

@@ -63,5 +63,12 @@ def test_model_covers_every_ring_launch_in_the_dispatch(model):
             continue  # the template definitions
         ns = int(a[7]) if len(a) > 7 else 2
         launched.add((dt, int(a[0]), int(a[1]), int(a[2]), int(a[3]), ns))
+    # the 32x32x16 NN variant launches its kernel directly: <BM, BN, WM, WN, WPE, NS>, the same
+    # copies (F16RingCopies) as the fp16 ring of that tile
+    for args in re.findall(r"gemm_f16_ring_mf32_kernel<([^>]*)>\)", src):
+        a = [x.strip() for x in args.split(",")]
+        if a[0].isdigit():
+            launched.add(("f16", int(a[0]), int(a[1]), int(a[2]), int(a[3]), int(a[5])))
     assert launched, "no ring launches found in gemm.hip"
+    assert any(x[1:] == (256, 256, 2, 4, 2) for x in launched if x[0] == "f16")
     assert launched <= listed, launched - listed
