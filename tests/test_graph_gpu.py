@@ -91,6 +91,43 @@ def test_graph_replays_match_eager(dev):
     plan.release()
 
 
+def test_synchronize_on_a_capturing_stream_is_an_error(dev):
+    """gn_synchronize (the completion wait every synchronous entry uses) on a stream under
+    capture has nothing to wait for: it returns -6 without touching the stream, and the capture
+    goes on. The captured GEMM then replays with the eager result's bits."""
+    import torch
+
+    torch.manual_seed(11)
+    a = torch.randn(512, 256, device=dev)
+    b = torch.randn(256, 384, device=dev)
+    c = torch.empty(512, 384, device=dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        G.gemm(a, b, c)  # warm-up outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        G.gemm(a, b, c)
+        rc, msg = G.call_rc("gn_synchronize", s.cuda_stream)
+        G.gemm(a, b, c, beta=1.0)  # c = ab + ab after the refused wait
+    _say("gn_synchronize under capture:", rc, msg)
+    assert rc == -6 and "device execution" in msg
+    torch.cuda.synchronize()
+    for rep in range(2):
+        with torch.no_grad():
+            a.mul_(0.5)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = c.clone()
+        G.gemm(a, b, c)
+        G.gemm(a, b, c, beta=1.0)
+        torch.cuda.synchronize()
+        assert torch.equal(got, c), rep
+
+
 def _ptrs(*bufs):
     import ctypes
 
