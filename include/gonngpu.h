@@ -301,6 +301,11 @@ void gn_memory_stats(long *current_bytes, long *peak_bytes, long *num_allocation
 int gn_malloc(void **ptr, size_t bytes, CError *err);
 int gn_free(void *ptr);
 int gn_free_async(void *ptr, void *stream);
+/* Waits for the work enqueued on `stream` (NULL = the library stream), as every synchronous
+ * Part-1 call does before it returns: an event recorded behind that work is polled for up to
+ * 5 ms, then waited on. -6 with the runtime's message when the work failed, and when `stream`
+ * is capturing (a capture has no completion to wait for; the stream and its capture are left
+ * as they were). */
 int gn_synchronize(void *stream, CError *err);
 
 /* General GEMM on device pointers:
