@@ -229,6 +229,130 @@ def vendor_reference(c, a, b, flop, steps, name):
                     "(out_dtype=float32, this library's contract); fp16_out_*: torch's default fp16 output"}
 
 
+def sparse_vendor_reference(c, csr, dense, out, steps, b_streamed, kind):
+    """The same C5 product through torch's CSR tensor (hipSPARSE over rocSPARSE) on the same
+    device arrays, for scale only: torch.mm for SpMM, torch.mv for SpMV. Its sums run in
+    another order, so its result is checked against this library's loosely (relFrob 1e-5)."""
+    t = c.torch
+    M, K, nnz, d_rp, d_col, d_val = csr
+    S = t.sparse_csr_tensor(d_rp, d_col, d_val, size=(M, K))
+    op = (lambda: t.mm(S, dense)) if kind == "spmm" else (lambda: t.mv(S, dense))
+    ref = op()
+    t.cuda.synchronize()
+    err = (t.linalg.vector_norm((ref - out).double()) / t.linalg.vector_norm(out.double())).item()
+    ms = timed(op, steps, 10, c.stream, MIN_WARM_MS)
+    gbs = b_streamed / (ms * 1e-3) / 1e9
+    log(f"{kind} torch CSR (hipSPARSE): {ms * 1e3:.1f} us, {gbs:.0f} GB/s streamed-bytes model, "
+        f"relFrob {err:.1e} against this library's result")
+    return {"ms": round(ms, 5), "GB/s_streamed": round(gbs, 1), "relFrob_vs_this_library": err,
+            "what": f"torch.{'mm' if kind == 'spmm' else 'mv'} on a torch.sparse_csr_tensor over the same device "
+                    "arrays (hipSPARSE / rocSPARSE), a new output tensor per call"}
+
+
+def rocsparse_reference(c, csr, dense, out, steps, b_streamed, kind):
+    """The same C5 product through rocSPARSE's generic API (rocsparse_spmm / rocsparse_spmv,
+    librocsparse.so through ctypes) on the same device arrays and stream, for scale only: the
+    buffer-size and preprocess (analysis) stages run once, then only the compute stage is timed,
+    for each CSR algorithm that accepts the problem. Results are checked against this
+    library's loosely (relFrob 1e-5; the sums run in another order)."""
+    import ctypes
+
+    t = c.torch
+    try:
+        R = ctypes.CDLL("librocsparse.so")
+    except OSError as e:
+        return {"skipped": f"librocsparse.so not loadable: {e}"}
+    vp, i64, ci = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    OP_NONE, I32, BASE0, F32, ROW = 111, 2, 0, 151, 0
+    M, K, nnz, d_rp, d_col, d_val = csr
+
+    def ok(st, what):
+        if st != 0:
+            raise RuntimeError(f"{what}: rocsparse status {st}")
+
+    h, A, X, Y = vp(), vp(), vp(), vp()
+    ok(R.rocsparse_create_handle(ctypes.byref(h)), "create_handle")
+    ok(R.rocsparse_set_stream(h, vp(c.sp)), "set_stream")
+    ok(R.rocsparse_create_csr_descr(ctypes.byref(A), i64(M), i64(K), i64(nnz), vp(d_rp.data_ptr()),
+                                    vp(d_col.data_ptr()), vp(d_val.data_ptr()), ci(I32), ci(I32), ci(BASE0), ci(F32)),
+       "create_csr_descr")
+    res = t.empty_like(out)
+    alpha, beta = ctypes.c_float(1.0), ctypes.c_float(0.0)
+    if kind == "spmm":
+        N = dense.shape[1]
+        ok(R.rocsparse_create_dnmat_descr(ctypes.byref(X), i64(K), i64(N), i64(N), vp(dense.data_ptr()), ci(F32),
+                                          ci(ROW)), "create_dnmat_descr B")
+        ok(R.rocsparse_create_dnmat_descr(ctypes.byref(Y), i64(M), i64(N), i64(N), vp(res.data_ptr()), ci(F32),
+                                          ci(ROW)), "create_dnmat_descr C")
+        algs = {"default": 0, "csr": 1, "csr_row_split": 4, "csr_nnz_split": 5, "csr_merge_path": 9}
+
+        def call(alg, stage, size, buf):
+            return R.rocsparse_spmm(h, ci(OP_NONE), ci(OP_NONE), ctypes.byref(alpha), A, X, ctypes.byref(beta), Y,
+                                    ci(F32), ci(alg), ci(stage), size, buf)
+    else:
+        ok(R.rocsparse_create_dnvec_descr(ctypes.byref(X), i64(K), vp(dense.data_ptr()), ci(F32)), "create x")
+        ok(R.rocsparse_create_dnvec_descr(ctypes.byref(Y), i64(M), vp(res.data_ptr()), ci(F32)), "create y")
+        algs = {"default": 0, "csr_adaptive": 2, "csr_rowsplit": 3, "csr_lrb": 7, "csr_nnzsplit": 8}
+
+        def call(alg, stage, size, buf):
+            return R.rocsparse_spmv(h, ci(OP_NONE), ctypes.byref(alpha), A, X, ctypes.byref(beta), Y, ci(F32),
+                                    ci(alg), ci(stage), size, buf)
+    per_alg = {}
+    try:
+        for name, alg in algs.items():
+            size = ctypes.c_size_t(0)
+            if call(alg, 1, ctypes.byref(size), None) != 0:  # buffer size
+                per_alg[name] = "not supported"
+                continue
+            buf = t.empty(max(int(size.value), 256), dtype=t.uint8, device=out.device)
+            if call(alg, 2, ctypes.byref(size), vp(buf.data_ptr())) != 0:  # preprocess (analysis), once
+                per_alg[name] = "preprocess failed"
+                continue
+            if call(alg, 3, ctypes.byref(size), vp(buf.data_ptr())) != 0:
+                per_alg[name] = "compute failed"
+                continue
+            t.cuda.synchronize()
+            err = (t.linalg.vector_norm((res - out).double()) / t.linalg.vector_norm(out.double())).item()
+            # wall clock between device-wide synchronisations: some algorithms launch on a stream
+            # of their own, which events recorded on this stream would not see
+            for _ in range(10):
+                call(alg, 3, ctypes.byref(size), vp(buf.data_ptr()))
+            res.zero_()
+            t.cuda.synchronize()
+            n = max(steps, 50)
+            bad = 0
+            t0 = time.perf_counter()
+            for _ in range(n):
+                bad += call(alg, 3, ctypes.byref(size), vp(buf.data_ptr())) != 0
+            t.cuda.synchronize()
+            ms = (time.perf_counter() - t0) * 1e3 / n
+            err2 = (t.linalg.vector_norm((res - out).double()) / t.linalg.vector_norm(out.double())).item()
+            if bad or not err2 <= 1e-5:  # the timed calls must each have computed the product
+                per_alg[name] = f"repeated compute calls: {bad} of {n} failed, result relFrob {err2:.1e}"
+                continue
+            per_alg[name] = {"ms": round(ms, 5), "GB/s_streamed": round(b_streamed / (ms * 1e-3) / 1e9, 1),
+                             "relFrob_vs_this_library": err}
+    finally:
+        t.cuda.synchronize()
+        destroy_dense = R.rocsparse_destroy_dnmat_descr if kind == "spmm" else R.rocsparse_destroy_dnvec_descr
+        destroy_dense(X)
+        destroy_dense(Y)
+        R.rocsparse_destroy_spmat_descr(A)
+        R.rocsparse_destroy_handle(h)
+    timed_algs = {k: v for k, v in per_alg.items() if isinstance(v, dict) and v["relFrob_vs_this_library"] <= 1e-5}
+    best = min(timed_algs, key=lambda k: timed_algs[k]["ms"]) if timed_algs else None
+    if best:
+        b = timed_algs[best]
+        log(f"{kind} rocSPARSE ({best}, analysis done once): {b['ms'] * 1e3:.1f} us, {b['GB/s_streamed']:.0f} GB/s "
+            f"streamed-bytes model, relFrob {b['relFrob_vs_this_library']:.1e} against this library's result")
+    else:
+        log(f"{kind} rocSPARSE: no algorithm timed ({per_alg})")
+    return {"best_alg": best, "ms": timed_algs[best]["ms"] if best else None, "per_alg": per_alg,
+            "what": "rocsparse_spmm / rocsparse_spmv compute stage on the same device arrays, after one "
+                    "buffer-size and preprocess call per algorithm; wall clock per call over back-to-back calls "
+                    "between device-wide synchronisations (includes each call's launch cost)"}
+
+
 def run_c2(c, steps, warmup):
     m = 4096
     A, B, C = c.empty((m, m)), c.empty((m, m)), c.empty((m, m))
@@ -440,6 +564,8 @@ def run_spmm(c, steps, warmup, csr):
         out["GB/s_l2_refill"] = round(refill, 1)
         out["frac_8TBps_l2_refill"] = round(refill / PEAK_HBM_GBS, 4)
         log(f"spmm: {refill:.0f} GB/s of measured L2 refill traffic ({traffic / 1e9:.2f} GB per call)")
+    out["torch_sparse_reference"] = sparse_vendor_reference(c, csr, D, Cs, steps, b_s, "spmm")
+    out["rocsparse_reference"] = rocsparse_reference(c, csr, D, Cs, steps, b_s, "spmm")
     return out
 
 
@@ -458,6 +584,8 @@ def run_spmv(c, steps, warmup, csr):
     ms = timed(lambda: plan.run(d_val, x, y, stream_ptr=c.sp), steps, warmup, c.stream, MIN_WARM_MS)
     flat_ms = timed(lambda: c.G.spmv_csr(M, K, nnz, d_rp, d_col, d_val, x, y, stream_ptr=c.sp), steps, warmup,
                     c.stream, MIN_WARM_MS)
+    plan.run(d_val, x, y, stream_ptr=c.sp)  # y = the grouped kernel's result, for the reference check
+    c.torch.cuda.synchronize()
     plan.release(stream_ptr=c.sp)
     # compulsory bytes: row pointers, values, x and y once, and the layout per entry (one
     # 4-byte word of column and CSR position for K <= 65536, else 4 + 2 bytes)
@@ -471,7 +599,7 @@ def run_spmv(c, steps, warmup, csr):
     gbs_streamed = b_streamed / (ms * 1e-3) / 1e9
     log(f"spmv: grouped {ms * 1e3:.1f} us, {gbs_streamed:.0f} GB/s streamed-bytes model, {gbs:.0f} GB/s of "
         f"compulsory bytes (plan built in {plan_ms:.1f} ms); flat kernel {flat_ms * 1e3:.1f} us")
-    return {"ms": round(ms, 5), "kernel": "spmv_grouped_kernel", "GB/s_streamed": round(gbs_streamed, 1),
+    res = {"ms": round(ms, 5), "kernel": "spmv_grouped_kernel", "GB/s_streamed": round(gbs_streamed, 1),
             "frac_hbm_streamed": round(gbs_streamed / PEAK_HBM_GBS, 4), "bytes_streamed": b_streamed,
             "GB/s_compulsory": round(gbs, 1),
             "frac_hbm_compulsory": round(gbs / PEAK_HBM_GBS, 4), "bytes_compulsory": b_s,
@@ -479,6 +607,9 @@ def run_spmv(c, steps, warmup, csr):
             "flat_kernel_ms": round(flat_ms, 5), "flat_GB/s_compulsory": round(b_flat / (flat_ms * 1e-3) / 1e9, 1),
             "what": "grouped layout (gn_spmv_plan_run) on resident device arrays; flat_kernel_*: gn_spmv_csr "
                     "(no layout) on the same arrays"}
+    res["torch_sparse_reference"] = sparse_vendor_reference(c, csr, x, y, steps, b_streamed, "spmv")
+    res["rocsparse_reference"] = rocsparse_reference(c, csr, x, y, steps, b_streamed, "spmv")
+    return res
 
 
 def run_e2e(c, steps, warmup):
