@@ -366,6 +366,18 @@ def run_c2(c, steps, warmup):
         res[f"c2_f32_4096_{name}"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 2),
                                       "frac_fp32_peak": round(tf / PEAK_F32_TFLOPS, 4)}
         log(f"c2 {name}: {ms:.3f} ms, {tf:.1f} TFLOP/s ({100 * tf / PEAK_F32_TFLOPS:.1f}% of fp32 peak)")
+    # the same NN product through torch.mm (hipBLASLt, fp32 in and out), for scale only
+    t = c.torch
+    prev_tf32 = t.backends.cuda.matmul.allow_tf32
+    t.backends.cuda.matmul.allow_tf32 = False  # full fp32, as this library computes
+    try:
+        ms = timed(lambda: t.mm(A, B), steps, 10, c.stream, MIN_WARM_MS)
+    finally:
+        t.backends.cuda.matmul.allow_tf32 = prev_tf32
+    tf = 2.0 * m ** 3 / (ms * 1e-3) / 1e12
+    res["c2_torch_matmul_reference"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 2),
+                                        "what": "torch.mm on the same fp32 NN operands (hipBLASLt), TF32 off"}
+    log(f"c2 torch.mm (hipBLASLt) NN: {ms:.3f} ms, {tf:.1f} TFLOP/s")
     return res
 
 
