@@ -9,8 +9,9 @@
 //
 // Two kernel families share the epilogue and the tile order: the DMA-ring kernels
 // gemm_f16_ring_kernel and gemm_f32_ring_kernel (large fp16 and fp32 problems; described
-// at their definitions) and the register-staged gemm_f16_kernel / gemm_f32_kernel for
-// every other shape, structured as follows
+// at their definitions; gemm_f16_ring_mf32_kernel is the NN 256 x 256 ring on 32 x 32 x 16
+// instructions, kept for measurement behind GONNGPU_F16_MFMA32=1) and the register-staged
+// gemm_f16_kernel / gemm_f32_kernel for every other shape, structured as follows
 // (one workgroup per BM x BN output tile, WM x WN waves, 64 lanes each):
 //  * global -> VGPR prefetch of the next BK slice overlaps the MFMAs of the current
 //    one; LDS is double buffered, one barrier per BK slice;
