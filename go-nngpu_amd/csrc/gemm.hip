@@ -491,6 +491,127 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32_kernel(GemmParams p) {
   store_tile_rows<BM, BN, WM, WN>(p, m0, n0, z, smem, acc);
 }
 
+// ------------------------------------------------------------------ fp32 kernel, small products
+// Products too small to fill the chip with the tiled kernels (256^3 makes 16 workgroups of
+// 64 x 64, on 16 of the 256 CUs, each wave a chain of 256 MFMAs). Here a workgroup computes
+// a BM x BN = 16 FM x 16 FN tile and its KW waves split K: wave w sums the 16-element K steps
+// [w S / KW, (w + 1) S / KW) of the S = ceil(K / 16) steps. No operand is reused between
+// waves, so the fragments go from global memory (L2) straight into the MFMA source
+// registers, without LDS staging: lane (i, g) of a fragment takes row i and, for MFMA step
+// s, k = 16 t + 4 g + s, as the tiled fp32 kernel does (a K-contiguous operand as one
+// 16-byte vector when aligned). Four K steps are loaded before their MFMAs run (a second
+// register set that loads the next four during the MFMAs measured 10-20% slower: fewer
+// waves fit). The KW partial tiles are added in LDS in wave order, ((w0 + w1) + w2) + ...,
+// before the epilogue, so each element's summation order depends on K and KW alone: the
+// same for all four transpose layouts, aligned or not.
+template <int KW, int FM, int FN, bool TA, bool TB, bool VEC>
+__global__ void __launch_bounds__(KW * 64) gemm_f32_small_kernel(GemmParams p) {
+  constexpr int BM = 16 * FM, BN = 16 * FN, NF = FM * FN, U = 4;
+  __shared__ float4_t red[KW][NF][64];
+  const long m0 = (long)(blockIdx.x / p.tiles_n) * BM, n0 = (long)(blockIdx.x % p.tiles_n) * BN;
+  const long z = blockIdx.z;
+  const float *A = static_cast<const float *>(p.A) + z * p.strideA;
+  const float *B = static_cast<const float *>(p.B) + z * p.strideB;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+  const long steps = (p.K + 15) / 16;
+  const long sb = steps * wave / KW, se = steps * (wave + 1) / KW;
+
+  // One lane's four elements (k .. k + 3) of row r of op(A) or column r of op(B): rows past
+  // the product and k past K read as zero.
+  auto frag = [&](const float *X, long ld, bool kcontig, long r, bool rin, long k) {
+    float4_t v{0.f, 0.f, 0.f, 0.f};
+    if (!rin) return v;
+    if (kcontig) {
+      const float *q = X + r * ld + k;
+      if (VEC) {  // K is a multiple of 4: the four are all inside or all past K
+        if (k < p.K) v = *reinterpret_cast<const float4_t *>(q);
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) v[s] = k + s < p.K ? q[s] : 0.0f;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) v[s] = k + s < p.K ? X[(k + s) * ld + r] : 0.0f;
+    }
+    return v;
+  };
+
+  typedef float4_t FragA[U][FM];
+  typedef float4_t FragB[U][FN];
+  auto load = [&](FragA &af, FragB &bf, long t0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool live = t0 + u < se;
+      const long k = (t0 + u) * 16 + 4 * lg;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const long r = m0 + 16 * i + li;
+        af[u][i] = frag(A, p.lda, !TA, r, live && r < p.M, k);
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const long c = n0 + 16 * j + li;
+        bf[u][j] = frag(B, p.ldb, TB, c, live && c < p.N, k);
+      }
+    }
+  };
+  float4_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+  auto mma = [&](const FragA &af, const FragB &bf) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[u][i][s], bf[u][j][s], acc[i][j], 0, 0, 0);
+  };
+  for (long t0 = sb; t0 < se; t0 += U) {
+    FragA af;
+    FragB bf;
+    load(af, bf, t0);
+    mma(af, bf);
+  }
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) red[wave][i * FN + j][lane] = acc[i][j];
+  __syncthreads();
+  if (threadIdx.x >= NF * 64) return;
+  // thread (f, l) finishes lane l's four elements of fragment f: rows 4 (l >> 4) + 0..3,
+  // column l & 15
+  const int f = threadIdx.x >> 6, l = threadIdx.x & 63;
+  float4_t v = red[0][f][l];
+#pragma unroll
+  for (int w = 1; w < KW; ++w) v = v + red[w][f][l];
+  const long col = n0 + 16 * (f % FN) + (l & 15), row0 = m0 + 16 * (f / FN) + 4 * (l >> 4);
+  if (col >= p.N) return;
+  float *C = p.C + z * p.strideC;
+  const float bv = p.bias ? p.bias[col] : 0.0f;
+  auto finish = [&](auto act_c) {
+    constexpr int ACT = decltype(act_c)::value;
+    const int act = ACT == kActRuntime ? p.act : ACT;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (row0 + e >= p.M) break;
+      float *dst = C + (row0 + e) * p.ldc + col;
+      const float old = p.beta != 0.0f ? *dst : 0.0f;
+      *dst = apply_act(act, p.alpha * v[e] + p.beta * old + bv, p.act_alpha);
+    }
+  };
+  switch (p.act) {
+    case -1: finish(ActCode<-1>{}); break;
+    case 0: finish(ActCode<0>{}); break;
+    case 7: finish(ActCode<7>{}); break;
+    default: finish(ActCode<kActRuntime>{}); break;
+  }
+}
+
 // ------------------------------------------------------------------ fp16 DMA-ring kernel
 // Large aligned fp16 GEMMs. Differences from gemm_f16_kernel:
 //  * global -> LDS copies are buffer loads with the LDS-direct bit (16 bytes per lane
@@ -1280,6 +1401,15 @@ hipError_t launch_f16(GemmParams p, long batch, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int KW, int FM, int FN, bool TA, bool TB, bool VEC>
+hipError_t launch_f32_small(GemmParams p, long batch, hipStream_t s) {
+  p.tiles_m = (int)((p.M + 16 * FM - 1) / (16 * FM));
+  p.tiles_n = (int)((p.N + 16 * FN - 1) / (16 * FN));
+  dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
+  hipLaunchKernelGGL((gemm_f32_small_kernel<KW, FM, FN, TA, TB, VEC>), grid, dim3(KW * 64), 0, s, p);
+  return hipGetLastError();
+}
+
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VEC>
 hipError_t launch_f32(GemmParams p, long batch, hipStream_t s) {
   p.tiles_m = (int)((p.M + BM - 1) / BM);
@@ -1493,8 +1623,44 @@ hipError_t launch_f32_ring_best(const GemmParams &p, long batch, hipStream_t s) 
   return launch_f32_ring<64, 64, 2, 2, TA, TB>(p, batch, s);
 }
 
+// The small-product kernel's shape for an fp32 product, as 100 KW + 10 FM + FN, or 0 for the
+// tiled kernels. It is taken while the 64 x 64 tiles would leave at least three quarters of
+// the CUs idle (at most 64 tiles), for K up to 1024, for K up to 4096 at 4 tiles or fewer,
+// and for any K below 2^24 multiply-adds in all (where the tiled path has no split-K).
+// Workgroups of 16 x 16 tiles while there are at most 256 of them (or K is at most 32),
+// 32 x 32 beyond; as many K-splitting waves (4, 8, or 16 with 16 x 16 tiles) as leave each
+// wave at least three 16-element K steps and the grid at most 2048 waves. Kernel times on
+// MI355X (rocprofv3 kernel trace), tiled -> small: 256^3 7.7 -> 4.2 us; 128 x 784 x 784
+// 21.5 -> 10.1 us; 100 x 130 x 1000 49.7 -> 10.6 us; 512^2 x 1024 16.3 -> 11.1 us;
+// 16 x 16 x 4096 66.3 -> 13.6 us. At 768^2 (144 tiles), at 256^2 x 4096 and at 64^2 x 16384
+// the tiled path (split-K for the long K) is as fast or faster.
+inline int f32_small_tile(long M, long N, long K, long batch) {
+  const long tiles64 = ((M + 63) / 64) * ((N + 63) / 64) * batch;
+  if (tiles64 > 64) return 0;
+  const bool few_macs = (double)M * N * K * batch < (double)(1L << 24);
+  if (!(K <= 1024 || (tiles64 <= 4 && K <= 4096) || few_macs)) return 0;
+  const long t16 = ((M + 15) / 16) * ((N + 15) / 16) * batch, steps = (K + 15) / 16;
+  const bool f11 = t16 <= 256 || steps <= 2;
+  const long wgs = f11 ? t16 : (t16 + 3) / 4;
+  int kw = 4;
+  for (int c : {16, 8}) {
+    if ((c == 16 && !f11) || 3 * c > steps || wgs * c > 2048) continue;
+    kw = c;
+    break;
+  }
+  return kw * 100 + (f11 ? 11 : 22);
+}
+
 template <bool TA, bool TB, bool VEC>
 hipError_t pick_f32(const GemmParams &p, long batch, hipStream_t s) {
+  switch (f32_small_tile(p.M, p.N, p.K, batch)) {
+    case 411: return launch_f32_small<4, 1, 1, TA, TB, VEC>(p, batch, s);
+    case 811: return launch_f32_small<8, 1, 1, TA, TB, VEC>(p, batch, s);
+    case 1611: return launch_f32_small<16, 1, 1, TA, TB, VEC>(p, batch, s);
+    case 422: return launch_f32_small<4, 2, 2, TA, TB, VEC>(p, batch, s);
+    case 822: return launch_f32_small<8, 2, 2, TA, TB, VEC>(p, batch, s);
+    default: break;
+  }
   if constexpr (!VEC) {
     return launch_f32<64, 64, 16, 2, 2, TA, TB, VEC>(p, batch, s);
   } else {
@@ -1855,13 +2021,14 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
         (size_t)((a_ok ? 0 : d.M) + (b_ok ? 0 : d.N)) * (size_t)Kp * esz * (size_t)std::min(kMaxZ, d.batch);
     const bool big = (double)d.M * d.N * d.K >= (double)(1L << 24);
     const long pack_grid_y = (a_ok ? 0 : (d.M + 63) / 64) + (b_ok ? 0 : (d.N + 63) / 64);
-    bool pack = !vec && big && pack_bytes <= ((size_t)4 << 30) && pack_grid_y <= 65535;
+    const bool small = d.dtype == GN_F32 && f32_small_tile(d.M, d.N, d.K, d.batch) != 0;
+    bool pack = !vec && big && !small && pack_bytes <= ((size_t)4 << 30) && pack_grid_y <= 65535;
     // Split-K (choose_split) for a batch-1 product on the aligned path, packed or not, whose
     // operands suit the DMA ring; the partial products take S x M x N floats of the scratch
     // (each M x N rounded up to a multiple of 4), ahead of the packed copies.
     const long k_aligned = (!a_ok && !b_ok) ? Kp : d.K;  // the K the aligned kernels see
     int S = 1;
-    if (d.batch == 1 && big && (vec || pack) && (a_ok ? d.lda : Kp) < (1L << 21) && (b_ok ? d.ldb : Kp) < (1L << 21))
+    if (d.batch == 1 && big && !small && (vec || pack) && (a_ok ? d.lda : Kp) < (1L << 21) && (b_ok ? d.ldb : Kp) < (1L << 21))
       S = choose_split(d.dtype, d.M, d.N, k_aligned, d.beta != 0.0f);
     const size_t part_bytes = S > 1 ? ((size_t)S * splitk_stride(d.M, d.N) * sizeof(float) + 255) / 256 * 256 : 0;
     if (part_bytes > ((size_t)1 << 30)) S = 1;

@@ -172,13 +172,14 @@ def test_f32_ring_ragged_all_transposes_bit_identical(dev, K):
     assert err <= 1e-5
 
 
-@pytest.mark.parametrize("M,N,K", [(2000, 2010, 96), (2000, 4000, 96), (2000, 2100, 96), (300, 500, 64), (68, 132, 96),
-                                   (4, 4, 32)])
+@pytest.mark.parametrize("M,N,K", [(2000, 2010, 96), (2000, 4000, 96), (2000, 2100, 96), (600, 700, 64),
+                                   (520, 1100, 96)])
 def test_f32_ring_small_tiles_all_transposes_bit_identical(dev, M, N, K):
     """The fp32 ring's smaller tiles with ragged M, N and K of one or three 32-deep K-tile
     pairs: 128x128 with 8 waves (2000 x 2010: 256 tiles, one round), 128x128 with 4 waves
     (2000 x 4000: 512 tiles, two per CU), 64x64 (the other shapes; 2000 x 2100 has 1056 of
-    them). NaN start, row and column sums, rows against float64, all four layouts bit for bit."""
+    them, 600 x 700 has 110, more than the small-product kernel takes). NaN start, row and
+    column sums, rows against float64, all four layouts bit for bit."""
     import torch
 
     rng = np.random.default_rng(M + N + K)
@@ -201,7 +202,7 @@ def test_f32_ring_small_tiles_all_transposes_bit_identical(dev, M, N, K):
     assert O.rel_frob(outs[0][rows], O.gemm_f64_rows(A, B, rows)) <= 1e-5
 
 
-@pytest.mark.parametrize("M,N,K,pad", [(300, 500, 64, 4), (2000, 2100, 32, 8)])
+@pytest.mark.parametrize("M,N,K,pad", [(600, 700, 64, 4), (2000, 2100, 32, 8)])
 def test_f32_ring_padded_leading_dims(dev, M, N, K, pad):
     """Leading dimensions wider than the rows (views into wider buffers, still 16-byte
     aligned) on the fp32 ring, all four layouts: the copies step by lda / ldb, not by the
@@ -227,11 +228,11 @@ def test_f32_ring_padded_leading_dims(dev, M, N, K, pad):
 
 
 def test_f32_ring_small_tiles_batched(dev):
-    """Batched strides on the 64x64 fp32 ring (3 x 128^2 x 64: 12 tiles)."""
+    """Batched strides on the 64x64 fp32 ring (6 x 256^2 x 64: 96 tiles)."""
     import torch
 
     rng = np.random.default_rng(47)
-    bs, M, N, K = 3, 128, 128, 64
+    bs, M, N, K = 6, 256, 256, 64
     A = rng.standard_normal((bs, M, K)).astype(np.float32)
     B = rng.standard_normal((bs, K, N)).astype(np.float32)
     C = torch.full((bs, M, N), float("nan"), dtype=torch.float32, device=dev)
@@ -596,6 +597,80 @@ def test_f32_unaligned_leading_dims_and_batch(dev):
     C3 = bc.to_array((bs, M, N))
     for i in range(bs):
         assert O.rel_frob(C3[i], A3[i].astype(np.float64) @ B3[i]) <= 1e-5
+
+
+# Products the fp32 small-product kernel takes (at most 64 tiles of 64 x 64), one per shape
+# of it: 16 x 16 workgroup tiles with 4 / 8 / 16 K-splitting waves, 32 x 32 tiles with 4 / 8.
+SMALL_SHAPES = [
+    (256, 256, 256),   # config C1: 256 tiles of 16 x 16, 4 waves
+    (37, 53, 71),      # ragged M, N and a K tail inside a 16-element step
+    (17, 200, 5),      # K shorter than one step
+    (100, 100, 500),   # 8 waves
+    (64, 128, 784),    # 16 waves
+    (512, 512, 256),   # 32 x 32 tiles, 4 waves
+    (384, 384, 1024),  # 32 x 32 tiles, 8 waves
+    (512, 512, 32),    # K of two steps: 16 x 16 tiles, 1024 workgroups
+    (16, 16, 16384),   # long K under 2^24 multiply-adds
+    (128, 128, 4096),  # 4 tiles of 64 x 64, K up to 4096
+]
+
+
+@pytest.mark.parametrize("M,N,K", SMALL_SHAPES)
+def test_f32_small_kernel_all_layouts_aligned_or_not(dev, M, N, K):
+    """The small-product kernel: NaN start, the whole output against float64 (relFrob 1e-5),
+    all four layouts bit for bit, and the unaligned loads (leading dimensions one wider than
+    the rows, so no 16-byte vectors) bit for bit with the aligned ones: each element's
+    summation order depends on K alone."""
+    import torch
+
+    rng = np.random.default_rng(M * 7 + N * 3 + K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    ref = A.astype(np.float64) @ B
+    outs = []
+    for pad in (0, 1):
+        for tA, tB in VARIANTS:
+            _say("f32 small kernel", M, N, K, tA, tB, "pad", pad)
+            As, Bs = _stored(A, tA), _stored(B, tB)
+            aw = torch.full((As.shape[0], As.shape[1] + pad), float("nan"), dtype=torch.float32, device=dev)
+            bw = torch.full((Bs.shape[0], Bs.shape[1] + pad), float("nan"), dtype=torch.float32, device=dev)
+            aw[:, :As.shape[1]] = torch.from_numpy(As).to(dev)
+            bw[:, :Bs.shape[1]] = torch.from_numpy(Bs).to(dev)
+            cd = _nan_like(dev, M, N)
+            G.gemm(aw[:, :As.shape[1]], bw[:, :Bs.shape[1]], cd, transA=tA, transB=tB)
+            C = cd.cpu().numpy()
+            err = O.rel_frob(C, ref)
+            assert err <= 1e-5, (tA, tB, pad, err)
+            outs.append(C)
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])
+
+
+@pytest.mark.parametrize("tA,tB", VARIANTS)
+def test_f32_small_kernel_batched_alpha_beta_bias_act(dev, tA, tB):
+    """Batched strides and the alpha / beta / bias / activation epilogue on the small-product
+    kernel (5 x 96 x 80 x 300: 20 tiles of 64 x 64; and 4 x 200 x 150 x 40 on 32 x 32 tiles),
+    against float64 with the oracle's activation formulas."""
+    import torch
+
+    for bs, M, N, K in [(5, 96, 80, 300), (4, 200, 150, 40)]:
+        rng = np.random.default_rng(bs + M + K)
+        A = rng.standard_normal((bs, M, K)).astype(np.float32)
+        B = rng.standard_normal((bs, K, N)).astype(np.float32)
+        C0 = rng.standard_normal((bs, M, N)).astype(np.float32)
+        bias = rng.standard_normal(N).astype(np.float32)
+        As = np.ascontiguousarray(A.transpose(0, 2, 1)) if tA else A
+        Bs = np.ascontiguousarray(B.transpose(0, 2, 1)) if tB else B
+        ad, bd = torch.from_numpy(As).to(dev), torch.from_numpy(Bs).to(dev)
+        base = np.einsum("zmk,zkn->zmn", A.astype(np.float64), B.astype(np.float64))
+        for act, aa in [(G.ACT_NONE, 0.0), (G.ACT_RELU, 0.0), (G.ACT_GELU, 0.0), (G.ACT_LEAKY_RELU, 0.1)]:
+            _say("f32 small kernel epilogue", bs, M, N, K, tA, tB, act)
+            C = torch.from_numpy(C0).to(dev)
+            G.gemm(ad, bd, C, transA=tA, transB=tB, alpha=0.75, beta=-0.5, bias=torch.from_numpy(bias).to(dev),
+                   act=act, act_alpha=aa, M=M, N=N, K=K, batch=bs, strideA=M * K, strideB=K * N, strideC=M * N)
+            pre = 0.75 * base - 0.5 * C0 + bias
+            ref = pre if act == G.ACT_NONE else O.act_f64(act, pre, aa)
+            assert O.rel_frob(C.cpu().numpy(), ref) <= 1e-5, (bs, M, act)
 
 
 def test_f32_k_zero_and_empty(dev):
