@@ -491,92 +491,14 @@ __global__ void __launch_bounds__(WM * WN * 64) gemm_f32_kernel(GemmParams p) {
   store_tile_rows<BM, BN, WM, WN>(p, m0, n0, z, smem, acc);
 }
 
-// ------------------------------------------------------------------ fp32 kernel, small products
-// Products too small to fill the chip with the tiled kernels (256^3 makes 16 workgroups of
-// 64 x 64, on 16 of the 256 CUs, each wave a chain of 256 MFMAs). Here a workgroup computes
-// a BM x BN = 16 FM x 16 FN tile and its KW waves split K: wave w sums the 16-element K steps
-// [w S / KW, (w + 1) S / KW) of the S = ceil(K / 16) steps. No operand is reused between
-// waves, so the fragments go from global memory (L2) straight into the MFMA source
-// registers, without LDS staging: lane (i, g) of a fragment takes row i and, for MFMA step
-// s, k = 16 t + 4 g + s, as the tiled fp32 kernel does (a K-contiguous operand as one
-// 16-byte vector when aligned). Four K steps are loaded before their MFMAs run (a second
-// register set that loads the next four during the MFMAs measured 10-20% slower: fewer
-// waves fit). The KW partial tiles are added in LDS in wave order, ((w0 + w1) + w2) + ...,
-// before the epilogue, so each element's summation order depends on K and KW alone: the
-// same for all four transpose layouts, aligned or not.
-template <int KW, int FM, int FN, bool TA, bool TB, bool VEC>
-__global__ void __launch_bounds__(KW * 64) gemm_f32_small_kernel(GemmParams p) {
-  constexpr int BM = 16 * FM, BN = 16 * FN, NF = FM * FN, U = 4;
-  __shared__ float4_t red[KW][NF][64];
-  const long m0 = (long)(blockIdx.x / p.tiles_n) * BM, n0 = (long)(blockIdx.x % p.tiles_n) * BN;
-  const long z = blockIdx.z;
-  const float *A = static_cast<const float *>(p.A) + z * p.strideA;
-  const float *B = static_cast<const float *>(p.B) + z * p.strideB;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
-  const long steps = (p.K + 15) / 16;
-  const long sb = steps * wave / KW, se = steps * (wave + 1) / KW;
-
-  // One lane's four elements (k .. k + 3) of row r of op(A) or column r of op(B): rows past
-  // the product and k past K read as zero.
-  auto frag = [&](const float *X, long ld, bool kcontig, long r, bool rin, long k) {
-    float4_t v{0.f, 0.f, 0.f, 0.f};
-    if (!rin) return v;
-    if (kcontig) {
-      const float *q = X + r * ld + k;
-      if (VEC) {  // K is a multiple of 4: the four are all inside or all past K
-        if (k < p.K) v = *reinterpret_cast<const float4_t *>(q);
-      } else {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) v[s] = k + s < p.K ? q[s] : 0.0f;
-      }
-    } else {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) v[s] = k + s < p.K ? X[(k + s) * ld + r] : 0.0f;
-    }
-    return v;
-  };
-
-  typedef float4_t FragA[U][FM];
-  typedef float4_t FragB[U][FN];
-  auto load = [&](FragA &af, FragB &bf, long t0) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const bool live = t0 + u < se;
-      const long k = (t0 + u) * 16 + 4 * lg;
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const long r = m0 + 16 * i + li;
-        af[u][i] = frag(A, p.lda, !TA, r, live && r < p.M, k);
-      }
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const long c = n0 + 16 * j + li;
-        bf[u][j] = frag(B, p.ldb, TB, c, live && c < p.N, k);
-      }
-    }
-  };
-  float4_t acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-  auto mma = [&](const FragA &af, const FragB &bf) {
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-          for (int j = 0; j < FN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[u][i][s], bf[u][j][s], acc[i][j], 0, 0, 0);
-  };
-  for (long t0 = sb; t0 < se; t0 += U) {
-    FragA af;
-    FragB bf;
-    load(af, bf, t0);
-    mma(af, bf);
-  }
+// The small-product kernels' end: wave w's partial tile goes to red[w], the workgroup adds
+// the KW partials in wave order, ((w0 + w1) + w2) + ..., and applies the epilogue
+// C = act(alpha * sum + beta * C + bias[col]) (C is not read when beta = 0).
+template <int KW, int FM, int FN>
+__device__ __forceinline__ void small_reduce_store(const GemmParams &p, float4_t (&red)[KW][FM * FN][64],
+                                                   const float4_t (&acc)[FM][FN], long m0, long n0, long z) {
+  constexpr int NF = FM * FN;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -610,6 +532,112 @@ __global__ void __launch_bounds__(KW * 64) gemm_f32_small_kernel(GemmParams p) {
     case 7: finish(ActCode<7>{}); break;
     default: finish(ActCode<kActRuntime>{}); break;
   }
+}
+
+// ------------------------------------------------------------------ fp32 kernel, small products
+// Products too small to fill the chip with the tiled kernels (256^3 makes 16 workgroups of
+// 64 x 64, on 16 of the 256 CUs, each wave a chain of 256 MFMAs). Here a workgroup computes
+// a BM x BN = 16 FM x 16 FN tile and its KW waves split K: wave w sums the 16-element K steps
+// [w S / KW, (w + 1) S / KW) of the S = ceil(K / 16) steps. No operand is reused between
+// waves, so the fragments go from global memory (L2) straight into the MFMA source
+// registers, without LDS staging: lane (i, g) of a fragment takes row i and, for MFMA step
+// s, k = 16 t + 4 g + s, as the tiled fp32 kernel does (a K-contiguous operand as one
+// 16-byte vector when aligned). Four K steps are loaded before their MFMAs run (a second
+// register set that loads the next four during the MFMAs measured 10-20% slower: fewer
+// waves fit). The KW partial tiles are added in LDS in wave order, ((w0 + w1) + w2) + ...,
+// before the epilogue, so each element's summation order depends on K and KW alone: the
+// same for all four transpose layouts, aligned or not.
+// Per element type: the fragment vector V (E elements per lane and K step of KS elements)
+// and the MFMA steps MPS of one K step.
+template <typename T>
+struct SmallOps;
+template <>
+struct SmallOps<float> {
+  typedef float4_t V;
+  static constexpr int E = 4, KS = 16, MPS = 4;
+  static __device__ __forceinline__ float4_t mma(const V &a, const V &b, int s, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], c, 0, 0, 0);
+  }
+};
+template <>
+struct SmallOps<_Float16> {
+  typedef half8_t V;
+  static constexpr int E = 8, KS = 32, MPS = 1;
+  static __device__ __forceinline__ float4_t mma(const V &a, const V &b, int, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <typename T, int KW, int FM, int FN, bool TA, bool TB, bool VEC>
+__global__ void __launch_bounds__(KW * 64) gemm_small_kernel(GemmParams p) {
+  typedef SmallOps<T> Ops;
+  typedef typename Ops::V V;
+  constexpr int NF = FM * FN, U = 64 / Ops::KS, E = Ops::E, KS = Ops::KS;  // 64 elements of K per batch
+  __shared__ float4_t red[KW][NF][64];
+  const long m0 = (long)(blockIdx.x / p.tiles_n) * 16 * FM, n0 = (long)(blockIdx.x % p.tiles_n) * 16 * FN;
+  const long z = blockIdx.z;
+  const T *A = static_cast<const T *>(p.A) + z * p.strideA;
+  const T *B = static_cast<const T *>(p.B) + z * p.strideB;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+  const long steps = (p.K + KS - 1) / KS;
+  const long sb = steps * wave / KW, se = steps * (wave + 1) / KW;
+
+  // One lane's E elements (k .. k + E - 1) of row r of op(A) or column r of op(B): rows past
+  // the product and k past K read as zero.
+  auto frag = [&](const T *X, long ld, bool kcontig, long r, bool rin, long k) {
+    V v;
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = T(0);
+    if (!rin) return v;
+    if (kcontig) {
+      const T *q = X + r * ld + k;
+      if (VEC) {  // K is a multiple of E: the E elements are all inside or all past K
+        if (k < p.K) v = *reinterpret_cast<const V *>(q);
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+          if (k + e < p.K) v[e] = q[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+        if (k + e < p.K) v[e] = X[(k + e) * ld + r];
+    }
+    return v;
+  };
+
+  float4_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (long t0 = sb; t0 < se; t0 += U) {
+    V af[U][FM], bf[U][FN];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool live = t0 + u < se;
+      const long k = (t0 + u) * KS + E * lg;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const long r = m0 + 16 * i + li;
+        af[u][i] = frag(A, p.lda, !TA, r, live && r < p.M, k);
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const long c = n0 + 16 * j + li;
+        bf[u][j] = frag(B, p.ldb, TB, c, live && c < p.N, k);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int s = 0; s < Ops::MPS; ++s)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) acc[i][j] = Ops::mma(af[u][i], bf[u][j], s, acc[i][j]);
+  }
+  small_reduce_store<KW, FM, FN>(p, red, acc, m0, n0, z);
 }
 
 // ------------------------------------------------------------------ fp16 DMA-ring kernel
@@ -1401,13 +1429,27 @@ hipError_t launch_f16(GemmParams p, long batch, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int KW, int FM, int FN, bool TA, bool TB, bool VEC>
-hipError_t launch_f32_small(GemmParams p, long batch, hipStream_t s) {
+template <typename T, int KW, int FM, int FN, bool TA, bool TB, bool VEC>
+hipError_t launch_small(GemmParams p, long batch, hipStream_t s) {
   p.tiles_m = (int)((p.M + 16 * FM - 1) / (16 * FM));
   p.tiles_n = (int)((p.N + 16 * FN - 1) / (16 * FN));
   dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
-  hipLaunchKernelGGL((gemm_f32_small_kernel<KW, FM, FN, TA, TB, VEC>), grid, dim3(KW * 64), 0, s, p);
+  hipLaunchKernelGGL((gemm_small_kernel<T, KW, FM, FN, TA, TB, VEC>), grid, dim3(KW * 64), 0, s, p);
   return hipGetLastError();
+}
+
+// The small-product kernel of shape code 100 KW + 10 FM + FN; hipErrorInvalidValue for
+// another code.
+template <typename T, bool TA, bool TB, bool VEC>
+hipError_t launch_small_code(int code, const GemmParams &p, long batch, hipStream_t s) {
+  switch (code) {
+    case 411: return launch_small<T, 4, 1, 1, TA, TB, VEC>(p, batch, s);
+    case 811: return launch_small<T, 8, 1, 1, TA, TB, VEC>(p, batch, s);
+    case 1611: return launch_small<T, 16, 1, 1, TA, TB, VEC>(p, batch, s);
+    case 422: return launch_small<T, 4, 2, 2, TA, TB, VEC>(p, batch, s);
+    case 822: return launch_small<T, 8, 2, 2, TA, TB, VEC>(p, batch, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VEC>
@@ -1535,8 +1577,27 @@ hipError_t launch_f16_tile(const GemmParams &p, long batch, hipStream_t s, F16Ti
   }
 }
 
+// The small-product kernel's shape for an fp16 product (100 KW + 10 FM + FN), or 0 for the
+// tiled kernels. fp16 MFMAs are 8x the fp32 rate, so the 64 x 64 register-staged kernel stays
+// ahead from fewer tiles than in fp32: the small kernel is taken for at most 16 of them, for
+// K up to 1024 or below 2^24 multiply-adds in all (no split-K there), always with 16 x 16
+// workgroup tiles and 16 waves from 24 32-element K steps (K > 736), 8 from 8 (K > 224), else
+// 4: with fp16 a wave's K step is one MFMA, and more waves with fewer steps each measured
+// faster. Kernel times on MI355X (rocprofv3 kernel trace), tiled -> small, NN: 256^3 5.70 ->
+// 4.47 us; 100 x 130 x 1000 30.9 -> 9.5 us; 64 x 128 x 784 9.0 -> 6.1 us; 256^2 x 1024 10.2
+// -> 6.9 us; 16 x 16 x 4096 29.1 -> 12.8 us. 384^2 and larger, and 64^2 x 4096, stay on the
+// tiled kernels (4.5 against 4.6 us at 384^2 x 64, 11.9 against 13.9 us at 64^2 x 4096).
+inline int f16_small_tile(long M, long N, long K, long batch) {
+  const long tiles64 = ((M + 63) / 64) * ((N + 63) / 64) * batch;
+  if (tiles64 > 16) return 0;
+  if (!(K <= 1024 || (double)M * N * K * batch < (double)(1L << 24))) return 0;
+  const long steps = (K + 31) / 32;
+  return steps >= 24 ? 1611 : steps >= 8 ? 811 : 411;
+}
+
 template <bool TA, bool TB, bool VEC>
 hipError_t pick_f16(const GemmParams &p, long batch, hipStream_t s) {
+  if (const int code = f16_small_tile(p.M, p.N, p.K, batch)) return launch_small_code<_Float16, TA, TB, VEC>(code, p, batch, s);
   if constexpr (!VEC) {
     // Unaligned shapes take the element-wise load path on the smallest tile only.
     return launch_f16<64, 64, 64, 2, 2, TA, TB, VEC>(p, batch, s);
@@ -1653,14 +1714,7 @@ inline int f32_small_tile(long M, long N, long K, long batch) {
 
 template <bool TA, bool TB, bool VEC>
 hipError_t pick_f32(const GemmParams &p, long batch, hipStream_t s) {
-  switch (f32_small_tile(p.M, p.N, p.K, batch)) {
-    case 411: return launch_f32_small<4, 1, 1, TA, TB, VEC>(p, batch, s);
-    case 811: return launch_f32_small<8, 1, 1, TA, TB, VEC>(p, batch, s);
-    case 1611: return launch_f32_small<16, 1, 1, TA, TB, VEC>(p, batch, s);
-    case 422: return launch_f32_small<4, 2, 2, TA, TB, VEC>(p, batch, s);
-    case 822: return launch_f32_small<8, 2, 2, TA, TB, VEC>(p, batch, s);
-    default: break;
-  }
+  if (const int code = f32_small_tile(p.M, p.N, p.K, batch)) return launch_small_code<float, TA, TB, VEC>(code, p, batch, s);
   if constexpr (!VEC) {
     return launch_f32<64, 64, 16, 2, 2, TA, TB, VEC>(p, batch, s);
   } else {
@@ -2021,7 +2075,7 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
         (size_t)((a_ok ? 0 : d.M) + (b_ok ? 0 : d.N)) * (size_t)Kp * esz * (size_t)std::min(kMaxZ, d.batch);
     const bool big = (double)d.M * d.N * d.K >= (double)(1L << 24);
     const long pack_grid_y = (a_ok ? 0 : (d.M + 63) / 64) + (b_ok ? 0 : (d.N + 63) / 64);
-    const bool small = d.dtype == GN_F32 && f32_small_tile(d.M, d.N, d.K, d.batch) != 0;
+    const bool small = (d.dtype == GN_F32 ? f32_small_tile(d.M, d.N, d.K, d.batch) : f16_small_tile(d.M, d.N, d.K, d.batch)) != 0;
     bool pack = !vec && big && !small && pack_bytes <= ((size_t)4 << 30) && pack_grid_y <= 65535;
     // Split-K (choose_split) for a batch-1 product on the aligned path, packed or not, whose
     // operands suit the DMA ring; the partial products take S x M x N floats of the scratch

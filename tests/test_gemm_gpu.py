@@ -269,7 +269,7 @@ def test_f32_ring_batched_alpha_beta_bias_act(dev, tA, tB):
 
 
 @pytest.mark.parametrize("M,N,K,tA,tB", [(1000, 1000, 1000, False, False), (1000, 1000, 1000, False, True),
-                                           (1000, 1000, 1000, True, True), (300, 500, 100, False, False),
+                                           (1000, 1000, 1000, True, True), (600, 700, 100, False, False),
                                            (2000, 2012, 1001, True, False), (4000, 4000, 40, True, False),
                                            (2048, 2048, 36, False, True)])
 def test_f32_k_tail_split_alpha_beta_bias_act(dev, M, N, K, tA, tB):
@@ -615,29 +615,44 @@ SMALL_SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("M,N,K", SMALL_SHAPES)
-def test_f32_small_kernel_all_layouts_aligned_or_not(dev, M, N, K):
-    """The small-product kernel: NaN start, the whole output against float64 (relFrob 1e-5),
-    all four layouts bit for bit, and the unaligned loads (leading dimensions one wider than
-    the rows, so no 16-byte vectors) bit for bit with the aligned ones: each element's
-    summation order depends on K alone."""
+# The fp16 kernel's shapes (16 x 16 tiles, at most 16 tiles of 64 x 64): 4, 8 and 16 waves.
+SMALL_SHAPES_F16 = [
+    (37, 53, 71),      # 4 waves, ragged, K tail inside a 32-element step
+    (17, 200, 5),      # K shorter than one step
+    (256, 256, 256),   # 8 waves
+    (100, 130, 1000),  # 16 waves
+    (64, 128, 784),    # 16 waves
+    (16, 16, 4096),    # long K under 2^24 multiply-adds
+]
+
+
+@pytest.mark.parametrize("dtype,M,N,K", [(G.GN_F32,) + s for s in SMALL_SHAPES] +
+                         [(G.GN_F16,) + s for s in SMALL_SHAPES_F16])
+def test_small_kernel_all_layouts_aligned_or_not(dev, dtype, M, N, K):
+    """The small-product kernel: NaN start, the whole output against float64 of the stored
+    (for fp16 the rounded) operands (relFrob 1e-5), all four layouts bit for bit, and the
+    unaligned loads (leading dimensions one wider than the rows, so no 16-byte vectors) bit
+    for bit with the aligned ones: each element's summation order depends on K alone."""
     import torch
 
+    tdt = torch.float16 if dtype == G.GN_F16 else torch.float32
     rng = np.random.default_rng(M * 7 + N * 3 + K)
     A = rng.standard_normal((M, K)).astype(np.float32)
     B = rng.standard_normal((K, N)).astype(np.float32)
+    if dtype == G.GN_F16:
+        A, B = A.astype(np.float16).astype(np.float32), B.astype(np.float16).astype(np.float32)
     ref = A.astype(np.float64) @ B
     outs = []
     for pad in (0, 1):
         for tA, tB in VARIANTS:
-            _say("f32 small kernel", M, N, K, tA, tB, "pad", pad)
+            _say("small kernel", dtype, M, N, K, tA, tB, "pad", pad)
             As, Bs = _stored(A, tA), _stored(B, tB)
-            aw = torch.full((As.shape[0], As.shape[1] + pad), float("nan"), dtype=torch.float32, device=dev)
-            bw = torch.full((Bs.shape[0], Bs.shape[1] + pad), float("nan"), dtype=torch.float32, device=dev)
-            aw[:, :As.shape[1]] = torch.from_numpy(As).to(dev)
-            bw[:, :Bs.shape[1]] = torch.from_numpy(Bs).to(dev)
+            aw = torch.full((As.shape[0], As.shape[1] + pad), float("nan"), dtype=tdt, device=dev)
+            bw = torch.full((Bs.shape[0], Bs.shape[1] + pad), float("nan"), dtype=tdt, device=dev)
+            aw[:, :As.shape[1]] = torch.from_numpy(As).to(dev).to(tdt)
+            bw[:, :Bs.shape[1]] = torch.from_numpy(Bs).to(dev).to(tdt)
             cd = _nan_like(dev, M, N)
-            G.gemm(aw[:, :As.shape[1]], bw[:, :Bs.shape[1]], cd, transA=tA, transB=tB)
+            G.gemm(aw[:, :As.shape[1]], bw[:, :Bs.shape[1]], cd, transA=tA, transB=tB, dtype=dtype)
             C = cd.cpu().numpy()
             err = O.rel_frob(C, ref)
             assert err <= 1e-5, (tA, tB, pad, err)
@@ -647,27 +662,34 @@ def test_f32_small_kernel_all_layouts_aligned_or_not(dev, M, N, K):
 
 
 @pytest.mark.parametrize("tA,tB", VARIANTS)
-def test_f32_small_kernel_batched_alpha_beta_bias_act(dev, tA, tB):
+@pytest.mark.parametrize("dtype", [G.GN_F32, G.GN_F16])
+def test_small_kernel_batched_alpha_beta_bias_act(dev, dtype, tA, tB):
     """Batched strides and the alpha / beta / bias / activation epilogue on the small-product
-    kernel (5 x 96 x 80 x 300: 20 tiles of 64 x 64; and 4 x 200 x 150 x 40 on 32 x 32 tiles),
-    against float64 with the oracle's activation formulas."""
+    kernel (5 x 96 x 80 x 300: 20 tiles of 64 x 64 in fp32, too many for the fp16 rule; 3 x 96
+    x 80 x 300: 12; and in fp32 4 x 200 x 150 x 40 on 32 x 32 tiles), against float64 of the
+    stored operands with the oracle's activation formulas."""
     import torch
 
-    for bs, M, N, K in [(5, 96, 80, 300), (4, 200, 150, 40)]:
+    tdt = torch.float16 if dtype == G.GN_F16 else torch.float32
+    cases = [(5, 96, 80, 300), (4, 200, 150, 40)] if dtype == G.GN_F32 else [(3, 96, 80, 300)]
+    for bs, M, N, K in cases:
         rng = np.random.default_rng(bs + M + K)
         A = rng.standard_normal((bs, M, K)).astype(np.float32)
         B = rng.standard_normal((bs, K, N)).astype(np.float32)
+        if dtype == G.GN_F16:
+            A, B = A.astype(np.float16).astype(np.float32), B.astype(np.float16).astype(np.float32)
         C0 = rng.standard_normal((bs, M, N)).astype(np.float32)
         bias = rng.standard_normal(N).astype(np.float32)
         As = np.ascontiguousarray(A.transpose(0, 2, 1)) if tA else A
         Bs = np.ascontiguousarray(B.transpose(0, 2, 1)) if tB else B
-        ad, bd = torch.from_numpy(As).to(dev), torch.from_numpy(Bs).to(dev)
+        ad, bd = torch.from_numpy(As).to(dev).to(tdt), torch.from_numpy(Bs).to(dev).to(tdt)
         base = np.einsum("zmk,zkn->zmn", A.astype(np.float64), B.astype(np.float64))
         for act, aa in [(G.ACT_NONE, 0.0), (G.ACT_RELU, 0.0), (G.ACT_GELU, 0.0), (G.ACT_LEAKY_RELU, 0.1)]:
-            _say("f32 small kernel epilogue", bs, M, N, K, tA, tB, act)
+            _say("small kernel epilogue", dtype, bs, M, N, K, tA, tB, act)
             C = torch.from_numpy(C0).to(dev)
             G.gemm(ad, bd, C, transA=tA, transB=tB, alpha=0.75, beta=-0.5, bias=torch.from_numpy(bias).to(dev),
-                   act=act, act_alpha=aa, M=M, N=N, K=K, batch=bs, strideA=M * K, strideB=K * N, strideC=M * N)
+                   act=act, act_alpha=aa, M=M, N=N, K=K, batch=bs, strideA=M * K, strideB=K * N, strideC=M * N,
+                   dtype=dtype)
             pre = 0.75 * base - 0.5 * C0 + bias
             ref = pre if act == G.ACT_NONE else O.act_f64(act, pre, aa)
             assert O.rel_frob(C.cpu().numpy(), ref) <= 1e-5, (bs, M, act)
