@@ -534,19 +534,20 @@ __device__ __forceinline__ void small_reduce_store(const GemmParams &p, float4_t
   }
 }
 
-// ------------------------------------------------------------------ fp32 kernel, small products
+// ------------------------------------------------------------------ small products (fp32, fp16)
 // Products too small to fill the chip with the tiled kernels (256^3 makes 16 workgroups of
-// 64 x 64, on 16 of the 256 CUs, each wave a chain of 256 MFMAs). Here a workgroup computes
-// a BM x BN = 16 FM x 16 FN tile and its KW waves split K: wave w sums the 16-element K steps
-// [w S / KW, (w + 1) S / KW) of the S = ceil(K / 16) steps. No operand is reused between
-// waves, so the fragments go from global memory (L2) straight into the MFMA source
-// registers, without LDS staging: lane (i, g) of a fragment takes row i and, for MFMA step
-// s, k = 16 t + 4 g + s, as the tiled fp32 kernel does (a K-contiguous operand as one
-// 16-byte vector when aligned). Four K steps are loaded before their MFMAs run (a second
-// register set that loads the next four during the MFMAs measured 10-20% slower: fewer
-// waves fit). The KW partial tiles are added in LDS in wave order, ((w0 + w1) + w2) + ...,
-// before the epilogue, so each element's summation order depends on K and KW alone: the
-// same for all four transpose layouts, aligned or not.
+// 64 x 64, on 16 of the 256 CUs, each wave a chain of 256 fp32 MFMAs). Here a workgroup
+// computes a BM x BN = 16 FM x 16 FN tile and its KW waves split K: wave w sums the K steps
+// [w S / KW, (w + 1) S / KW) of the S = ceil(K / KS) steps (KS = 16 elements for fp32, 32 for
+// fp16). No operand is reused between waves, so the fragments go from global memory (L2)
+// straight into the MFMA source registers, without LDS staging: lane (i, g) of a fragment
+// takes row i and k = KS t + E g + s, s < E, as the tiled kernels do (fp32: E = 4, one
+// v_mfma_f32_16x16x4_f32 per s; fp16: E = 8, one v_mfma_f32_16x16x32_f16 per step), a
+// K-contiguous operand as one 16-byte vector when aligned. 64 elements of K are loaded before
+// their MFMAs run (a second register set that loads the next ones during the MFMAs measured
+// 10-20% slower: fewer waves fit). The KW partial tiles are added in LDS in wave order before
+// the epilogue (small_reduce_store), so each element's summation order depends on K and KW
+// alone: the same for all four transpose layouts, aligned or not.
 // Per element type: the fragment vector V (E elements per lane and K step of KS elements)
 // and the MFMA steps MPS of one K step.
 template <typename T>
