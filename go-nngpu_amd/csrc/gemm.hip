@@ -504,33 +504,34 @@ __device__ __forceinline__ void small_reduce_store(const GemmParams &p, float4_t
 #pragma unroll
     for (int j = 0; j < FN; ++j) red[wave][i * FN + j][lane] = acc[i][j];
   __syncthreads();
-  if (threadIdx.x >= NF * 64) return;
   // thread (f, l) finishes lane l's four elements of fragment f: rows 4 (l >> 4) + 0..3,
-  // column l & 15
-  const int f = threadIdx.x >> 6, l = threadIdx.x & 63;
-  float4_t v = red[0][f][l];
-#pragma unroll
-  for (int w = 1; w < KW; ++w) v = v + red[w][f][l];
-  const long col = n0 + 16 * (f % FN) + (l & 15), row0 = m0 + 16 * (f / FN) + 4 * (l >> 4);
-  if (col >= p.N) return;
+  // column l & 15; wave w takes fragments w, w + KW, ...
+  const int l = threadIdx.x & 63;
   float *C = p.C + z * p.strideC;
-  const float bv = p.bias ? p.bias[col] : 0.0f;
-  auto finish = [&](auto act_c) {
-    constexpr int ACT = decltype(act_c)::value;
-    const int act = ACT == kActRuntime ? p.act : ACT;
+  for (int f = threadIdx.x >> 6; f < NF; f += KW) {
+    float4_t v = red[0][f][l];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (row0 + e >= p.M) break;
-      float *dst = C + (row0 + e) * p.ldc + col;
-      const float old = p.beta != 0.0f ? *dst : 0.0f;
-      *dst = apply_act(act, p.alpha * v[e] + p.beta * old + bv, p.act_alpha);
+    for (int w = 1; w < KW; ++w) v = v + red[w][f][l];
+    const long col = n0 + 16 * (f % FN) + (l & 15), row0 = m0 + 16 * (f / FN) + 4 * (l >> 4);
+    if (col >= p.N) continue;
+    const float bv = p.bias ? p.bias[col] : 0.0f;
+    auto finish = [&](auto act_c) {
+      constexpr int ACT = decltype(act_c)::value;
+      const int act = ACT == kActRuntime ? p.act : ACT;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (row0 + e >= p.M) break;
+        float *dst = C + (row0 + e) * p.ldc + col;
+        const float old = p.beta != 0.0f ? *dst : 0.0f;
+        *dst = apply_act(act, p.alpha * v[e] + p.beta * old + bv, p.act_alpha);
+      }
+    };
+    switch (p.act) {
+      case -1: finish(ActCode<-1>{}); break;
+      case 0: finish(ActCode<0>{}); break;
+      case 7: finish(ActCode<7>{}); break;
+      default: finish(ActCode<kActRuntime>{}); break;
     }
-  };
-  switch (p.act) {
-    case -1: finish(ActCode<-1>{}); break;
-    case 0: finish(ActCode<0>{}); break;
-    case 7: finish(ActCode<7>{}); break;
-    default: finish(ActCode<kActRuntime>{}); break;
   }
 }
 
@@ -569,11 +570,11 @@ struct SmallOps<_Float16> {
   }
 };
 
-template <typename T, int KW, int FM, int FN, bool TA, bool TB, bool VEC>
+template <typename T, int KW, int FM, int FN, bool TA, bool TB, bool VEC, int KB = 64>
 __global__ void __launch_bounds__(KW * 64) gemm_small_kernel(GemmParams p) {
   typedef SmallOps<T> Ops;
   typedef typename Ops::V V;
-  constexpr int NF = FM * FN, U = 64 / Ops::KS, E = Ops::E, KS = Ops::KS;  // 64 elements of K per batch
+  constexpr int NF = FM * FN, U = KB / Ops::KS, E = Ops::E, KS = Ops::KS;  // KB elements of K per load batch
   __shared__ float4_t red[KW][NF][64];
   const long m0 = (long)(blockIdx.x / p.tiles_n) * 16 * FM, n0 = (long)(blockIdx.x % p.tiles_n) * 16 * FN;
   const long z = blockIdx.z;
@@ -1430,12 +1431,12 @@ hipError_t launch_f16(GemmParams p, long batch, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <typename T, int KW, int FM, int FN, bool TA, bool TB, bool VEC>
+template <typename T, int KW, int FM, int FN, bool TA, bool TB, bool VEC, int KB = 64>
 hipError_t launch_small(GemmParams p, long batch, hipStream_t s) {
   p.tiles_m = (int)((p.M + 16 * FM - 1) / (16 * FM));
   p.tiles_n = (int)((p.N + 16 * FN - 1) / (16 * FN));
   dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
-  hipLaunchKernelGGL((gemm_small_kernel<T, KW, FM, FN, TA, TB, VEC>), grid, dim3(KW * 64), 0, s, p);
+  hipLaunchKernelGGL((gemm_small_kernel<T, KW, FM, FN, TA, TB, VEC, KB>), grid, dim3(KW * 64), 0, s, p);
   return hipGetLastError();
 }
 
@@ -1578,6 +1579,31 @@ hipError_t launch_f16_tile(const GemmParams &p, long batch, hipStream_t s, F16Ti
   }
 }
 
+// Skinny products in the linear-layer layout Y = X W^T (A row-major, B = W stored N x K,
+// K-contiguous; at most 16 rows, batch 1, N and K of 2048 and more) are bound by reading W
+// once from HBM. The small-product kernel with 16 x 16 tiles reads each W element once, as one
+// 16-byte vector per lane and K step, and each tile's A rows from L2, and its K-splitting waves
+// keep more loads in flight than the tiled kernels' few workgroups: up to 4096 waves (16 per
+// workgroup while ceil(N / 16) <= 256, 8 while <= 512, else 4). Kernel times on MI355X (tiled
+// -> this): fp32 1 x 11008 x 4096 54.9 -> 33.9 us (5.3 TB/s of W), 8 x 4096 x 8192 38.9 ->
+// 28.4 us, 16 x 16384 x 4096 81.8 -> 63.5 us; fp16 1 x 4096 x 2048 17.0 -> 6.1 us, 2 x 11008 x
+// 4096 22.1 -> 16.5 us, 16 x 4096 x 4096 14.0 -> 10.4 us. The bounds leave out the shapes where
+// it lost on a grid of M 1-16, N 2048-16384, K 2048-8192: fp32 past 2 rows needs N >= 4096 (16 x
+// 2048 x 8192: 25.6 against 31.6 us) and M N K < 2^31; fp16 past 2 rows needs M N <= 65536 and
+// K <= 4096 (8 x 16384 x 8192: 45.8 against 50.5 us). With W stored K x N (NN) the kernel's W
+// loads are 4- or 2-byte scalars and it ran 1.1-5x slower than the tiled kernels, so other
+// layouts keep them; a skinny NT product therefore differs from the same product in NN in its
+// rounding (K summed in four to sixteen wave ranges), both within the fp32 bar.
+inline int skinny_tile(long M, long N, long K, long batch, bool f16, bool ta, bool tb) {
+  if (ta || !tb || batch != 1 || M > 16 || N < 2048 || K < 2048) return 0;
+  if (M > 2) {
+    if (f16 && (M * N > 65536 || K > 4096)) return 0;
+    if (!f16 && (N < 4096 || (double)M * N * K >= (double)(1L << 31))) return 0;
+  }
+  const long t16 = (N + 15) / 16;
+  return t16 * 16 <= 4096 ? 1611 : t16 * 8 <= 4096 ? 811 : 411;
+}
+
 // The small-product kernel's shape for an fp16 product (100 KW + 10 FM + FN), or 0 for the
 // tiled kernels. fp16 MFMAs are 8x the fp32 rate, so the 64 x 64 register-staged kernel stays
 // ahead from fewer tiles than in fp32: the small kernel is taken for at most 16 of them, for
@@ -1588,7 +1614,8 @@ hipError_t launch_f16_tile(const GemmParams &p, long batch, hipStream_t s, F16Ti
 // 4.47 us; 100 x 130 x 1000 30.9 -> 9.5 us; 64 x 128 x 784 9.0 -> 6.1 us; 256^2 x 1024 10.2
 // -> 6.9 us; 16 x 16 x 4096 29.1 -> 12.8 us. 384^2 and larger, and 64^2 x 4096, stay on the
 // tiled kernels (4.5 against 4.6 us at 384^2 x 64, 11.9 against 13.9 us at 64^2 x 4096).
-inline int f16_small_tile(long M, long N, long K, long batch) {
+inline int f16_small_tile(long M, long N, long K, long batch, bool ta, bool tb) {
+  if (const int c = skinny_tile(M, N, K, batch, true, ta, tb)) return c;
   const long tiles64 = ((M + 63) / 64) * ((N + 63) / 64) * batch;
   if (tiles64 > 16) return 0;
   if (!(K <= 1024 || (double)M * N * K * batch < (double)(1L << 24))) return 0;
@@ -1598,7 +1625,7 @@ inline int f16_small_tile(long M, long N, long K, long batch) {
 
 template <bool TA, bool TB, bool VEC>
 hipError_t pick_f16(const GemmParams &p, long batch, hipStream_t s) {
-  if (const int code = f16_small_tile(p.M, p.N, p.K, batch)) return launch_small_code<_Float16, TA, TB, VEC>(code, p, batch, s);
+  if (const int code = f16_small_tile(p.M, p.N, p.K, batch, TA, TB)) return launch_small_code<_Float16, TA, TB, VEC>(code, p, batch, s);
   if constexpr (!VEC) {
     // Unaligned shapes take the element-wise load path on the smallest tile only.
     return launch_f16<64, 64, 64, 2, 2, TA, TB, VEC>(p, batch, s);
@@ -1696,7 +1723,8 @@ hipError_t launch_f32_ring_best(const GemmParams &p, long batch, hipStream_t s) 
 // 21.5 -> 10.1 us; 100 x 130 x 1000 49.7 -> 10.6 us; 512^2 x 1024 16.3 -> 11.1 us;
 // 16 x 16 x 4096 66.3 -> 13.6 us. At 768^2 (144 tiles), at 256^2 x 4096 and at 64^2 x 16384
 // the tiled path (split-K for the long K) is as fast or faster.
-inline int f32_small_tile(long M, long N, long K, long batch) {
+inline int f32_small_tile(long M, long N, long K, long batch, bool ta, bool tb) {
+  if (const int c = skinny_tile(M, N, K, batch, false, ta, tb)) return c;
   const long tiles64 = ((M + 63) / 64) * ((N + 63) / 64) * batch;
   if (tiles64 > 64) return 0;
   const bool few_macs = (double)M * N * K * batch < (double)(1L << 24);
@@ -1715,7 +1743,7 @@ inline int f32_small_tile(long M, long N, long K, long batch) {
 
 template <bool TA, bool TB, bool VEC>
 hipError_t pick_f32(const GemmParams &p, long batch, hipStream_t s) {
-  if (const int code = f32_small_tile(p.M, p.N, p.K, batch)) return launch_small_code<float, TA, TB, VEC>(code, p, batch, s);
+  if (const int code = f32_small_tile(p.M, p.N, p.K, batch, TA, TB)) return launch_small_code<float, TA, TB, VEC>(code, p, batch, s);
   if constexpr (!VEC) {
     return launch_f32<64, 64, 16, 2, 2, TA, TB, VEC>(p, batch, s);
   } else {
@@ -2076,7 +2104,8 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
         (size_t)((a_ok ? 0 : d.M) + (b_ok ? 0 : d.N)) * (size_t)Kp * esz * (size_t)std::min(kMaxZ, d.batch);
     const bool big = (double)d.M * d.N * d.K >= (double)(1L << 24);
     const long pack_grid_y = (a_ok ? 0 : (d.M + 63) / 64) + (b_ok ? 0 : (d.N + 63) / 64);
-    const bool small = (d.dtype == GN_F32 ? f32_small_tile(d.M, d.N, d.K, d.batch) : f16_small_tile(d.M, d.N, d.K, d.batch)) != 0;
+    const bool small = (d.dtype == GN_F32 ? f32_small_tile(d.M, d.N, d.K, d.batch, d.ta, d.tb)
+                                          : f16_small_tile(d.M, d.N, d.K, d.batch, d.ta, d.tb)) != 0;
     bool pack = !vec && big && !small && pack_bytes <= ((size_t)4 << 30) && pack_grid_y <= 65535;
     // Split-K (choose_split) for a batch-1 product on the aligned path, packed or not, whose
     // operands suit the DMA ring; the partial products take S x M x N floats of the scratch

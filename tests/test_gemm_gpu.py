@@ -695,6 +695,44 @@ def test_small_kernel_batched_alpha_beta_bias_act(dev, dtype, tA, tB):
             assert O.rel_frob(C.cpu().numpy(), ref) <= 1e-5, (bs, M, act)
 
 
+@pytest.mark.parametrize("dtype,M,N,K", [(G.GN_F32, 1, 4096, 2048), (G.GN_F32, 2, 2048, 3000),
+                                         (G.GN_F32, 8, 4100, 4096), (G.GN_F32, 13, 11008, 2048),
+                                         (G.GN_F16, 1, 2048, 4096), (G.GN_F16, 2, 11008, 2048),
+                                         (G.GN_F16, 16, 4096, 2056), (G.GN_F16, 5, 3001, 2048)])
+def test_skinny_linear_layer_all_layouts(dev, dtype, M, N, K):
+    """Skinny products Y = act(X W^T + b) (a few rows, W of N x K): in the NT layout (W
+    K-contiguous) they run the small-product kernel with 4 to 16 K-splitting waves, in the
+    other layouts the tiled kernels. NaN start, bias + ReLU and then alpha / beta, each layout
+    against float64 of the stored operands (relFrob 1e-5), and the layouts against each other
+    within the same bar (they sum K in different orders)."""
+    import torch
+
+    tdt = torch.float16 if dtype == G.GN_F16 else torch.float32
+    rng = np.random.default_rng(M * 11 + N + K)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    W = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
+    if dtype == G.GN_F16:
+        X, W = X.astype(np.float16).astype(np.float32), W.astype(np.float16).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    pre = X.astype(np.float64) @ W.T.astype(np.float64)
+    outs = []
+    for tA, tB in VARIANTS:
+        _say("skinny", dtype, M, N, K, tA, tB)
+        ad = torch.from_numpy(_stored(X, tA)).to(dev).to(tdt)
+        bd = torch.from_numpy(W if tB else np.ascontiguousarray(W.T)).to(dev).to(tdt)
+        cd = _nan_like(dev, M, N)
+        G.gemm(ad, bd, cd, transA=tA, transB=tB, bias=torch.from_numpy(bias).to(dev), act=G.ACT_RELU, dtype=dtype)
+        C = cd.cpu().numpy()
+        assert O.rel_frob(C, np.maximum(pre + bias, 0.0)) <= 1e-5, (tA, tB)
+        outs.append(C)
+        cd = torch.from_numpy(C0).to(dev)
+        G.gemm(ad, bd, cd, transA=tA, transB=tB, alpha=-0.5, beta=2.0, dtype=dtype)
+        assert O.rel_frob(cd.cpu().numpy(), -0.5 * pre + 2.0 * C0) <= 1e-5, (tA, tB)
+    for o in outs[1:]:
+        assert O.rel_frob(o, outs[0]) <= 1e-5
+
+
 def test_f32_k_zero_and_empty(dev):
     import torch
 
