@@ -2094,9 +2094,10 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
     // the product keeps its K, and a 16-byte block of a packed row that straddles K reads the
     // padding's zeros, while the aligned kernels mask an unpacked operand's rows at or past K
     // (per copy in the fp16 ring, by the K-tail split of the fp32 path). The result is the
-    // aligned path's on the same values. The element-wise-load kernel stays for small
-    // products, for scratch beyond 4 GiB, and under HIP graph capture (the scratch may need an
-    // allocation).
+    // aligned path's on the same values. Products the small-product kernel takes are not
+    // packed (its loads need no alignment); the element-wise-load kernel stays for the other
+    // products below 2^24 multiply-adds, for scratch beyond 4 GiB, and under HIP graph capture
+    // (the scratch may need an allocation).
     const long Kp = (d.K + 63) / 64 * 64;
     const bool a_ok = aligned(d.A, d.lda, d.strideA) && a_contig % epv == 0;
     const bool b_ok = aligned(d.B, d.ldb, d.strideB) && b_contig % epv == 0;
