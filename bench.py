@@ -459,7 +459,36 @@ def run_c4(c, steps, warmup):
                                     "frac_fp16_peak": round(tf / PEAK_F16_TFLOPS, 4)}
         log(f"c4 {name}: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s")
     res["c4_torch_matmul_reference"] = reference_or_note(vendor_reference, c, X16, W16.t(), flop, steps, "c4")
+    res["c4_interleaved"] = reference_or_note(c4_interleaved, c, X16, W16, bias, Y, flop, steps)
     return res
+
+
+def c4_interleaved(c, X16, W16, bias, Y, flop, steps, rounds=7):
+    """The C4 lines again in alternation: each round times ReLU, GELU and torch.mm (hipBLASLt,
+    fp32 and fp16 output) back to back on the same operands, and each line reports its median
+    over the rounds, so that no line is favoured by its place in the order (the board's power
+    limit moves the clock between legs run one after the other)."""
+    import statistics
+
+    t = c.torch
+    Wt = W16.t()
+    fns = {"relu": lambda: c.G.gemm(X16, W16, Y, transB=True, bias=bias, act=c.G.ACT_RELU, stream_ptr=c.sp),
+           "gelu": lambda: c.G.gemm(X16, W16, Y, transB=True, bias=bias, act=c.G.ACT_GELU, stream_ptr=c.sp),
+           "torch_fp32_out": lambda: t.mm(X16, Wt, out_dtype=t.float32),
+           "torch_fp16_out": lambda: t.mm(X16, Wt)}
+    n = max(20, steps // rounds)
+    per = {k: [] for k in fns}
+    for _ in range(rounds):
+        for k, fn in fns.items():
+            per[k].append(timed(fn, n, 5, c.stream))
+    med = {k: statistics.median(v) for k, v in per.items()}
+    log("c4 interleaved (median of %d rounds of %d launches): " % (rounds, n) +
+        ", ".join(f"{k} {v * 1e3:.1f} us" for k, v in med.items()))
+    out = {f"{k}_ms": round(v, 5) for k, v in med.items()}
+    out.update({f"{k}_TFLOP/s": round(flop / (v * 1e-3) / 1e12, 2) for k, v in med.items()})
+    out["what"] = ("the four C4 lines timed in alternation, %d rounds of %d launches each, median per line "
+                   "(this library's ReLU and GELU with bias; torch.mm without an epilogue)" % (rounds, n))
+    return out
 
 
 def csr_workload(c):
