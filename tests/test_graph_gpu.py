@@ -1,5 +1,5 @@
 """HIP graph capture of the device-pointer API: the GEMM (fp16 ring and register-staged
-kernels, fp32), CSR SpMM, SpMV and the grouped-layout SpMV of a plan built before the capture
+kernels, fp32, and the small-product kernel in fp32 and for a skinny fp16 X W^T), CSR SpMM, SpMV and the grouped-layout SpMV of a plan built before the capture
 launch no memset and allocate nothing, so a caller can capture them once and replay the graph. Each replay is compared with the eager result
 for inputs changed between replays (with the program's own eager work and
 synchronisations in between), bit for bit."""
@@ -26,6 +26,10 @@ def test_graph_replays_match_eager(dev):
     a16 = torch.randn(4096, 512, device=dev).half()      # ring kernel: 16 x 16 tiles of 256
     b16 = torch.randn(512, 4096, device=dev).half()
     x32 = torch.randn(700, 300, device=dev)              # fp32 register-staged kernel
+    xs = torch.randn(96, 200, device=dev)                # fp32 small-product kernel
+    ws = torch.randn(200, 80, device=dev)
+    xk = torch.randn(2, 4096, device=dev).half()         # fp16 skinny X W^T: small-product kernel
+    wk = (0.05 * torch.randn(2048, 4096, device=dev)).half()
     w32 = torch.randn(300, 500, device=dev)
     bias = torch.randn(500, device=dev)
     a2 = torch.randn(4600, 64, device=dev).half()        # fp16 row split: two launches
@@ -38,6 +42,8 @@ def test_graph_replays_match_eager(dev):
     c16 = torch.empty(4096, 4096, device=dev)
     c2 = torch.empty(4600, 4608, device=dev)
     y32 = torch.empty(700, 500, device=dev)
+    ys = torch.empty(96, 80, device=dev)
+    yk = torch.empty(2, 2048, device=dev)
     S = torch.empty(4000, 64, device=dev)
     yv = torch.empty(4000, device=dev)
     yp = torch.empty(4000, device=dev)
@@ -48,6 +54,8 @@ def test_graph_replays_match_eager(dev):
         G.gemm(a16, b16, c16)
         G.gemm(a2, b2, c2)
         G.gemm(x32, w32, y32, bias=bias, act=G.ACT_GELU)
+        G.gemm(xs, ws, ys, bias=bias[:80], act=G.ACT_RELU)
+        G.gemm(xk, wk, yk, transB=True)
         G.spmm_csr(4000, 64, 3000, val.size, d_rp, d_col, d_val, D, S)
         G.spmv_csr(4000, 3000, val.size, d_rp, d_col, d_val, xv, yv)
         plan.run(d_val, xv, yp)
@@ -64,13 +72,15 @@ def test_graph_replays_match_eager(dev):
     torch.cuda.synchronize()
 
     assert val.size >= 1 << 16
-    outs = (c16, c2, y32, S, yv, yp)
+    outs = (c16, c2, y32, S, yv, yp, ys, yk)
     for rep in range(3):
         # new inputs, eager work and a synchronisation between replays
         with torch.no_grad():
             a16.copy_(torch.randn_like(a16, dtype=torch.float32).half())
             b2.copy_(torch.randn_like(b2, dtype=torch.float32).half())
             w32.mul_(0.5).add_(0.1)
+            ws.mul_(-0.5).add_(0.2)
+            xk.copy_(torch.randn_like(xk, dtype=torch.float32).half())
             D.copy_(torch.randn_like(D))
             xv.mul_(-1.5)
             d_val.mul_(0.75)
@@ -80,7 +90,8 @@ def test_graph_replays_match_eager(dev):
         got = [t.clone() for t in outs]
         work()  # eager, on the current stream
         torch.cuda.synchronize()
-        for name, gt, ref in zip(("gemm f16", "gemm f16 row split", "gemm f32", "spmm", "spmv", "spmv plan"), got,
+        for name, gt, ref in zip(("gemm f16", "gemm f16 row split", "gemm f32", "spmm", "spmv", "spmv plan",
+                                  "gemm f32 small", "gemm f16 skinny"), got,
                                  outs):
             same = torch.equal(gt, ref)
             _say("replay", rep, name, "bit-identical" if same else "DIFFERS")
