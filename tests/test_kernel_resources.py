@@ -56,7 +56,8 @@ def test_no_kernel_uses_scratch_or_spills():
     assert len(res) > 100, len(res)
     # the kernels whose performance depends on it most must be among those checked
     for key in ("gemm_f16_ring_kernelILi256ELi256ELi2ELi4ELb0ELb0", "gemm_f32_ring_kernelILi256ELi256",
-                "spmv_grouped_kernel", "spmm_band"):
+                "spmv_grouped_kernel", "spmm_band", "gemm_small_kernelIfLi4ELi1ELi1E",
+                "gemm_small_kernelIDF16_Li16ELi1ELi1E"):
         assert any(key in k for k in res), key
     bad = {k: v for k, v in res.items() if any(v)}
     assert not bad, bad
