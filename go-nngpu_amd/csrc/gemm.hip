@@ -1440,6 +1440,90 @@ hipError_t launch_small(GemmParams p, long batch, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ------------------------------------------------------------------ NN products of 1-4 rows (GEMV)
+// C = act(alpha X W + beta C + bias) for X of R <= 4 rows (row-major), W stored K x N
+// (N-contiguous), batch 1: HBM-bound on reading W once, at 2 R flops per W element, so the MFMA
+// layout's 16-row fragments would be mostly padding and the tiled kernels' few column tiles
+// stream W from few CUs. Lane l of a workgroup owns columns n0 + E l .. + E - 1 (4 bytes of each
+// row of W, so a wave's load is 256 contiguous bytes); the KW waves split K into contiguous
+// ranges, each summed in k order with fmaf on the VALU, and the partials are added in LDS in wave
+// order before the epilogue. X's entries are uniform across the workgroup.
+template <typename T, int R, int E, int KW>
+__global__ void __launch_bounds__(KW * 64) gemv_nn_kernel(GemmParams p) {
+  __shared__ float red[KW][R][64 * E];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const long nb = (long)blockIdx.x * 64 * E, n0 = nb + (long)lane * E;
+  const T *__restrict__ W = static_cast<const T *>(p.B);
+  const T *__restrict__ X = static_cast<const T *>(p.A);
+  const long kb = p.K * wave / KW, ke = p.K * (wave + 1) / KW;
+  float acc[R][E];
+#pragma unroll
+  for (int m = 0; m < R; ++m)
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[m][e] = 0.0f;
+  if (n0 < p.N) {  // N is a multiple of E: the E columns are all inside or all past N
+    typedef T VE __attribute__((ext_vector_type(E == 1 ? 2 : E)));
+    auto step = [&](long k) {
+      T w[E];
+      if constexpr (E == 1) {
+        w[0] = W[k * p.ldb + n0];
+      } else {  // n0 and the pitch are even: one 4-byte load
+        const VE v = *reinterpret_cast<const VE *>(W + k * p.ldb + n0);
+#pragma unroll
+        for (int e = 0; e < E; ++e) w[e] = v[e];
+      }
+#pragma unroll
+      for (int m = 0; m < R; ++m) {
+        const float x = (float)X[m * p.lda + k];
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[m][e] = fmaf(x, (float)w[e], acc[m][e]);
+      }
+    };
+    long k = kb;
+    for (; k + 8 <= ke; k += 8) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) step(k + u);
+    }
+    for (; k < ke; ++k) step(k);
+  }
+#pragma unroll
+  for (int m = 0; m < R; ++m)
+#pragma unroll
+    for (int e = 0; e < E; ++e) red[wave][m][lane * E + e] = acc[m][e];
+  __syncthreads();
+  float *C = p.C;
+  for (int o = threadIdx.x; o < R * 64 * E; o += KW * 64) {
+    const int m = o / (64 * E), c = o % (64 * E);
+    const long n = nb + c;
+    if (n >= p.N) continue;
+    float v = red[0][m][c];
+#pragma unroll
+    for (int w = 1; w < KW; ++w) v += red[w][m][c];
+    float *dst = C + m * p.ldc + n;
+    const float old = p.beta != 0.0f ? *dst : 0.0f;
+    *dst = apply_act(p.act, p.alpha * v + p.beta * old + (p.bias ? p.bias[n] : 0.0f), p.act_alpha);
+  }
+}
+
+template <typename T, int R>
+hipError_t launch_gemv_r(const GemmParams &p, hipStream_t s) {
+  constexpr int E = sizeof(T) == 2 ? 2 : 1;  // 4 bytes per lane and row of W
+  const unsigned grid = (unsigned)((p.N + 64 * E - 1) / (64 * E));
+  hipLaunchKernelGGL((gemv_nn_kernel<T, R, E, 16>), dim3(grid), dim3(1024), 0, s, p);
+  return hipGetLastError();
+}
+
+// The NN GEMV kernel for a product of M <= 4 rows (batch 1, W aligned, N a multiple of 4 or 8).
+template <typename T>
+hipError_t launch_gemv(const GemmParams &p, hipStream_t s) {
+  switch (p.M) {
+    case 1: return launch_gemv_r<T, 1>(p, s);
+    case 2: return launch_gemv_r<T, 2>(p, s);
+    case 3: return launch_gemv_r<T, 3>(p, s);
+    default: return launch_gemv_r<T, 4>(p, s);
+  }
+}
+
 // The small-product kernel of shape code 100 KW + 10 FM + FN; hipErrorInvalidValue for
 // another code.
 template <typename T, bool TA, bool TB, bool VEC>
@@ -1577,6 +1661,21 @@ hipError_t launch_f16_tile(const GemmParams &p, long batch, hipStream_t s, F16Ti
       }
       return hipErrorInvalidValue;  // f16_best offers these tiles only for a K-contiguous B
   }
+}
+
+// NN products of at most 4 rows (batch 1) take the GEMV kernel where it measured faster than the
+// tiled and small-product kernels on a grid of M 1-4, N 512-32768, K 512-11008 (kernel times,
+// tiled -> GEMV): fp32 1 x 11008 x 4096 54.4 -> 28.5 us (6.3 TB/s of W), 2 x 16384 x 2048 37.3 ->
+// 21.0 us, 4 x 11008 x 4096 54.9 -> 43.4 us, 1 x 4096 x 4096 24.8 -> 20.2 us; fp16 1 x 16384 x
+// 2048 18.2 -> 12.1 us, 2 x 2048 x 2048 16.8 -> 9.7 us, 4 x 32768 x 1024 15.2 -> 12.1 us. With
+// fewer columns its grid has too few workgroups (N / 64 or N / 128 of them) and with more rows
+// the VALU work grows: fp32 2 x 4096 x 11008 52.8 against 70.0 us, fp16 4 x 4096 x 4096 13.7
+// against 27.1 us stay on the other kernels.
+inline bool gemv_nn(long M, long N, long K, long batch, bool f16) {
+  if (batch != 1 || M > 4) return false;
+  if (!f16) return N >= 11008 || (M <= 2 && N >= 8192) || (M == 1 && N >= 4096);
+  if (M <= 2 && (N >= 8192 || (N >= 1024 && N <= 2048 && K >= 1024))) return true;
+  return N >= 16384;
 }
 
 // Skinny products in the linear-layer layout Y = X W^T (A row-major, B = W stored N x K,
@@ -2101,11 +2200,14 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
     const long Kp = (d.K + 63) / 64 * 64;
     const bool a_ok = aligned(d.A, d.lda, d.strideA) && a_contig % epv == 0;
     const bool b_ok = aligned(d.B, d.ldb, d.strideB) && b_contig % epv == 0;
+    // NN products of 1-4 rows on the GEMV kernel, which needs only W aligned (X is read element
+    // by element)
+    const bool gemv = b_ok && !d.ta && !d.tb && gemv_nn(d.M, d.N, d.K, d.batch, d.dtype == GN_F16);
     const size_t pack_bytes =
         (size_t)((a_ok ? 0 : d.M) + (b_ok ? 0 : d.N)) * (size_t)Kp * esz * (size_t)std::min(kMaxZ, d.batch);
     const bool big = (double)d.M * d.N * d.K >= (double)(1L << 24);
     const long pack_grid_y = (a_ok ? 0 : (d.M + 63) / 64) + (b_ok ? 0 : (d.N + 63) / 64);
-    const bool small = (d.dtype == GN_F32 ? f32_small_tile(d.M, d.N, d.K, d.batch, d.ta, d.tb)
+    const bool small = gemv || (d.dtype == GN_F32 ? f32_small_tile(d.M, d.N, d.K, d.batch, d.ta, d.tb)
                                           : f16_small_tile(d.M, d.N, d.K, d.batch, d.ta, d.tb)) != 0;
     bool pack = !vec && big && !small && pack_bytes <= ((size_t)4 << 30) && pack_grid_y <= 65535;
     // Split-K (choose_split) for a batch-1 product on the aligned path, packed or not, whose
@@ -2135,6 +2237,10 @@ int launch_gemm(const GemmDesc &d, hipStream_t s, CError *err) {
       q.B = static_cast<const char *>(d.B) + z0 * d.strideB * (long)esz;
       q.C = d.C + z0 * d.strideC;
       const long nb = std::min(kMaxZ, d.batch - z0);
+      if (gemv) {
+        e = d.dtype == GN_F16 ? launch_gemv<_Float16>(q, s) : launch_gemv<float>(q, s);
+        continue;
+      }
       if (!pack && S == 1) {
         e = vec ? dispatch<true>(d, q, nb, s) : dispatch<false>(d, q, nb, s);
         continue;

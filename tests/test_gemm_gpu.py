@@ -733,6 +733,49 @@ def test_skinny_linear_layer_all_layouts(dev, dtype, M, N, K):
         assert O.rel_frob(o, outs[0]) <= 1e-5
 
 
+@pytest.mark.parametrize("dtype,M,N,K", [(G.GN_F32, 1, 4096, 4096), (G.GN_F32, 2, 8192, 2048),
+                                         (G.GN_F32, 3, 11008, 1000), (G.GN_F32, 4, 16384, 777),
+                                         (G.GN_F16, 1, 2048, 2048), (G.GN_F16, 2, 1024, 3001),
+                                         (G.GN_F16, 2, 8200, 1024), (G.GN_F16, 4, 16384, 515)])
+def test_gemv_nn_rows_all_layouts(dev, dtype, M, N, K):
+    """Products of 1-4 rows with W stored K x N (NN, the reference LinearLayer's input @ Weight)
+    run on the GEMV kernel (K split over 16 waves, fp32 sums on the VALU). NaN start; bias +
+    GELU, then alpha / beta with a prior C, each against float64 of the stored operands (relFrob
+    1e-5); the same product in the other layouts (other kernels, other summation orders) within
+    the same bar; and two runs bit for bit."""
+    import torch
+
+    tdt = torch.float16 if dtype == G.GN_F16 else torch.float32
+    rng = np.random.default_rng(M * 13 + N + K)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    W = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
+    if dtype == G.GN_F16:
+        X, W = X.astype(np.float16).astype(np.float32), W.astype(np.float16).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    pre = X.astype(np.float64) @ W.astype(np.float64)
+    outs = []
+    for tA, tB in VARIANTS:
+        _say("gemv nn", dtype, M, N, K, tA, tB)
+        ad = torch.from_numpy(_stored(X, tA)).to(dev).to(tdt)
+        bd = torch.from_numpy(_stored(W, tB)).to(dev).to(tdt)
+        cd = _nan_like(dev, M, N)
+        G.gemm(ad, bd, cd, transA=tA, transB=tB, bias=torch.from_numpy(bias).to(dev), act=G.ACT_GELU, dtype=dtype)
+        C = cd.cpu().numpy()
+        assert O.rel_frob(C, O.act_f64(G.ACT_GELU, pre + bias, 0.0)) <= 1e-5, (tA, tB)
+        outs.append(C)
+        if not tA and not tB:
+            cd2 = _nan_like(dev, M, N)
+            G.gemm(ad, bd, cd2, transA=tA, transB=tB, bias=torch.from_numpy(bias).to(dev), act=G.ACT_GELU,
+                   dtype=dtype)
+            np.testing.assert_array_equal(cd2.cpu().numpy(), C)
+        cd = torch.from_numpy(C0).to(dev)
+        G.gemm(ad, bd, cd, transA=tA, transB=tB, alpha=1.5, beta=-1.0, dtype=dtype)
+        assert O.rel_frob(cd.cpu().numpy(), 1.5 * pre - C0) <= 1e-5, (tA, tB)
+    for o in outs[1:]:
+        assert O.rel_frob(o, outs[0]) <= 1e-5
+
+
 def test_f32_k_zero_and_empty(dev):
     import torch
 
