@@ -1,5 +1,5 @@
 """HIP graph capture of the device-pointer API: the GEMM (fp16 ring and register-staged
-kernels, fp32, and the small-product kernel in fp32 and for a skinny fp16 X W^T), CSR SpMM, SpMV and the grouped-layout SpMV of a plan built before the capture
+kernels, fp32, the small-product kernel in fp32 and for a skinny fp16 X W^T, the NN GEMV), CSR SpMM, SpMV and the grouped-layout SpMV of a plan built before the capture
 launch no memset and allocate nothing, so a caller can capture them once and replay the graph. Each replay is compared with the eager result
 for inputs changed between replays (with the program's own eager work and
 synchronisations in between), bit for bit."""
@@ -30,6 +30,8 @@ def test_graph_replays_match_eager(dev):
     ws = torch.randn(200, 80, device=dev)
     xk = torch.randn(2, 4096, device=dev).half()         # fp16 skinny X W^T: small-product kernel
     wk = (0.05 * torch.randn(2048, 4096, device=dev)).half()
+    xg = torch.randn(1, 2048, device=dev)                 # fp32 NN GEMV (one row)
+    wg = 0.05 * torch.randn(2048, 8192, device=dev)
     w32 = torch.randn(300, 500, device=dev)
     bias = torch.randn(500, device=dev)
     a2 = torch.randn(4600, 64, device=dev).half()        # fp16 row split: two launches
@@ -44,6 +46,7 @@ def test_graph_replays_match_eager(dev):
     y32 = torch.empty(700, 500, device=dev)
     ys = torch.empty(96, 80, device=dev)
     yk = torch.empty(2, 2048, device=dev)
+    yg = torch.empty(1, 8192, device=dev)
     S = torch.empty(4000, 64, device=dev)
     yv = torch.empty(4000, device=dev)
     yp = torch.empty(4000, device=dev)
@@ -56,6 +59,7 @@ def test_graph_replays_match_eager(dev):
         G.gemm(x32, w32, y32, bias=bias, act=G.ACT_GELU)
         G.gemm(xs, ws, ys, bias=bias[:80], act=G.ACT_RELU)
         G.gemm(xk, wk, yk, transB=True)
+        G.gemm(xg, wg, yg, bias=bias.repeat(17)[:8192], act=G.ACT_RELU)
         G.spmm_csr(4000, 64, 3000, val.size, d_rp, d_col, d_val, D, S)
         G.spmv_csr(4000, 3000, val.size, d_rp, d_col, d_val, xv, yv)
         plan.run(d_val, xv, yp)
@@ -72,7 +76,7 @@ def test_graph_replays_match_eager(dev):
     torch.cuda.synchronize()
 
     assert val.size >= 1 << 16
-    outs = (c16, c2, y32, S, yv, yp, ys, yk)
+    outs = (c16, c2, y32, S, yv, yp, ys, yk, yg)
     for rep in range(3):
         # new inputs, eager work and a synchronisation between replays
         with torch.no_grad():
@@ -81,6 +85,7 @@ def test_graph_replays_match_eager(dev):
             w32.mul_(0.5).add_(0.1)
             ws.mul_(-0.5).add_(0.2)
             xk.copy_(torch.randn_like(xk, dtype=torch.float32).half())
+            xg.mul_(-1.25)
             D.copy_(torch.randn_like(D))
             xv.mul_(-1.5)
             d_val.mul_(0.75)
@@ -91,7 +96,7 @@ def test_graph_replays_match_eager(dev):
         work()  # eager, on the current stream
         torch.cuda.synchronize()
         for name, gt, ref in zip(("gemm f16", "gemm f16 row split", "gemm f32", "spmm", "spmv", "spmv plan",
-                                  "gemm f32 small", "gemm f16 skinny"), got,
+                                  "gemm f32 small", "gemm f16 skinny", "gemv f32"), got,
                                  outs):
             same = torch.equal(gt, ref)
             _say("replay", rep, name, "bit-identical" if same else "DIFFERS")
