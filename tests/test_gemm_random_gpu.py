@@ -10,7 +10,10 @@ activation or ReLU are compared whole (relFrob <= 1e-5, the fp32 bar; for fp16 i
 reference uses the rounded operands, as the fixed fp16 tests do); for the other activations
 1024 sampled elements are compared with the oracle's activation (orc_act_f64, the
 reference's formulas) applied to the float64 pre-activation. The padding columns of C must be
-left as they were."""
+left as they were.
+
+The second: 120 products of 1-16 rows with wide N and long K (test_gemm_random_few_rows),
+where the dispatch chooses between the GEMV, small-product and tiled kernels."""
 import random
 import sys
 
