@@ -32,7 +32,10 @@ operands with the headline's distributions and on all-zero operands. Under the b
 power limit the clock, and so this rate, depends on the operand values; the first figure
 is the most any GEMM on such data can reach on the box.
 
-`--only a,b,...` runs a subset of {c3, ceiling, c2, c1, c4, spmm, spmv, e2e, copy} (used by
+`rows` times products of a few rows (a linear layer at batch 1-16: the NN GEMV kernel, the
+small-product kernel's skinny NT branch, a small MLP layer) beside torch.mm, for scale.
+
+`--only a,b,...` runs a subset of {c3, ceiling, c2, c1, c4, rows, spmm, spmv, e2e, copy} (used by
 the rocprofv3 passes that produce profiles/); `copy` is a 1 GiB device copy used to
 calibrate the HBM byte counters.
 """
@@ -52,7 +55,7 @@ PEAK_F16_TFLOPS = 2516.6  # dense MFMA fp16, 256 CU x 4096 flop/clk x 2.4 GHz
 PEAK_F32_TFLOPS = 157.3   # fp32 MFMA
 MIN_WARM_MS = 50.0        # least untimed GPU time before each timed leg (see timed())
 PEAK_HBM_GBS = 8000.0
-ALL = ("c3", "ceiling", "c2", "c1", "c4", "spmm", "spmv", "e2e", "copy")
+ALL = ("c3", "ceiling", "c2", "c1", "c4", "rows", "spmm", "spmv", "e2e", "copy")
 
 
 def log(*a):
@@ -463,6 +466,37 @@ def run_c4(c, steps, warmup):
     return res
 
 
+def run_rows(c, steps):
+    """Products of a few rows beside torch.mm (TF32 off; fp32 output for fp16 inputs), event
+    timing of back-to-back launches: X W with W stored K x N (NN, the GEMV kernel), X W^T with W
+    stored N x K (NT, the small-product kernel's skinny branch), and a small MLP layer. The rate
+    is W's bytes over the time (W is read once; X and C are a few rows)."""
+    t = c.torch
+    t.backends.cuda.matmul.allow_tf32 = False
+    cases = [("f32", "NN", 1, 11008, 4096), ("f32", "NN", 2, 16384, 2048), ("f32", "NT", 1, 11008, 4096),
+             ("f16", "NN", 1, 16384, 2048), ("f16", "NT", 2, 11008, 4096), ("f32", "NN", 128, 784, 784)]
+    out = {}
+    for dt, lay, M, N, K in cases:
+        tdt = t.float16 if dt == "f16" else t.float32
+        X = t.randn(M, K, device=c.dev).to(tdt)
+        W = (0.02 * t.randn(N, K, device=c.dev)).to(tdt) if lay == "NT" else (0.02 * t.randn(K, N, device=c.dev)).to(tdt)
+        Y = t.empty(M, N, device=c.dev)
+        tb = lay == "NT"
+        ours = timed(lambda: c.G.gemm(X, W, Y, transB=tb, stream_ptr=c.sp), steps, 10, c.stream, MIN_WARM_MS / 5)
+        Wm = W.t() if tb else W
+        ref = (lambda: t.mm(X, Wm, out_dtype=t.float32)) if dt == "f16" else (lambda: t.mm(X, Wm, out=Y))
+        theirs = timed(ref, steps, 10, c.stream, MIN_WARM_MS / 5)
+        wb = N * K * (2 if dt == "f16" else 4)
+        key = f"{dt}_{lay}_{M}x{N}x{K}"
+        out[key] = {"us": round(ours * 1e3, 2), "TB/s_of_W": round(wb / (ours * 1e-3) / 1e12, 2),
+                    "torch_mm_us": round(theirs * 1e3, 2)}
+        log(f"rows {key}: {ours * 1e3:.1f} us ({wb / (ours * 1e-3) / 1e12:.2f} TB/s of W), torch.mm {theirs * 1e3:.1f} us")
+    out["what"] = ("kernel time per launch (back-to-back launches, HIP events) of this library's gn_gemm and of "
+                   "torch.mm on the same operands; torch.mm's launches from Python cost ~18 us each, so its "
+                   "figures below that are its call floor, not its kernel")
+    return out
+
+
 def c4_interleaved(c, X16, W16, bias, Y, flop, steps, rounds=7):
     """The C4 lines again in alternation: each round times ReLU, GELU and torch.mm (hipBLASLt,
     fp32 and fp16 output) back to back on the same operands, and each line reports its median
@@ -787,6 +821,8 @@ def main():
         c.torch.cuda.empty_cache()
     if "c1" in only:
         secondary["c1_f32_256"] = run_c1(c, steps2 * 20, 20)
+    if "rows" in only:
+        secondary["few_rows"] = reference_or_note(run_rows, c, steps2 * 4)
     if "c4" in only:
         secondary.update(run_c4(c, steps2 * 4, 5))
         c.torch.cuda.empty_cache()
