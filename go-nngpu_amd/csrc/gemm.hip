@@ -1815,13 +1815,14 @@ hipError_t launch_f32_ring_best(const GemmParams &p, long batch, hipStream_t s) 
 // tiled kernels. It is taken while the 64 x 64 tiles would leave at least three quarters of
 // the CUs idle (at most 64 tiles), for K up to 1024, for K up to 4096 at 4 tiles or fewer,
 // and for any K below 2^24 multiply-adds in all (where the tiled path has no split-K).
-// Workgroups of 16 x 16 tiles while there are at most 256 of them (or K is at most 32),
-// 32 x 32 beyond; as many K-splitting waves (4, 8, or 16 with 16 x 16 tiles) as leave each
-// wave at least three 16-element K steps and the grid at most 2048 waves. Kernel times on
-// MI355X (rocprofv3 kernel trace), tiled -> small: 256^3 7.7 -> 4.2 us; 128 x 784 x 784
-// 21.5 -> 10.1 us; 100 x 130 x 1000 49.7 -> 10.6 us; 512^2 x 1024 16.3 -> 11.1 us;
-// 16 x 16 x 4096 66.3 -> 13.6 us. At 768^2 (144 tiles), at 256^2 x 4096 and at 64^2 x 16384
-// the tiled path (split-K for the long K) is as fast or faster.
+// Workgroups of 16 x 16 tiles while there are at most 256 of them (or K is at most 32), or at
+// most 512 with K over 272; 32 x 32 beyond (128 x 784 x 784: 8.4 us on 16 x 16 tiles against
+// 10.2 on 32 x 32; 256 x 512 x 256: 7.3 against 6.6). As many K-splitting waves (4, 8, or 16
+// with 16 x 16 tiles) as leave each wave at least three 16-element K steps and the grid at most
+// 2048 waves. Kernel times on MI355X (rocprofv3 kernel trace), tiled -> small: 256^3 7.7 -> 4.2
+// us; 128 x 784 x 784 21.5 -> 8.4 us; 100 x 130 x 1000 49.7 -> 10.6 us; 512^2 x 1024 16.3 ->
+// 11.1 us; 16 x 16 x 4096 66.3 -> 13.6 us. At 768^2 (144 tiles), at 256^2 x 4096 and at 64^2 x
+// 16384 the tiled path (split-K for the long K) is as fast or faster.
 inline int f32_small_tile(long M, long N, long K, long batch, bool ta, bool tb) {
   if (const int c = skinny_tile(M, N, K, batch, false, ta, tb)) return c;
   const long tiles64 = ((M + 63) / 64) * ((N + 63) / 64) * batch;
@@ -1829,7 +1830,7 @@ inline int f32_small_tile(long M, long N, long K, long batch, bool ta, bool tb) 
   const bool few_macs = (double)M * N * K * batch < (double)(1L << 24);
   if (!(K <= 1024 || (tiles64 <= 4 && K <= 4096) || few_macs)) return 0;
   const long t16 = ((M + 15) / 16) * ((N + 15) / 16) * batch, steps = (K + 15) / 16;
-  const bool f11 = t16 <= 256 || steps <= 2;
+  const bool f11 = t16 <= 256 || steps <= 2 || (t16 <= 512 && steps >= 18);
   const long wgs = f11 ? t16 : (t16 + 3) / 4;
   int kw = 4;
   for (int c : {16, 8}) {
